@@ -1,0 +1,357 @@
+#!/usr/bin/env python3
+"""W8A8 linear-path benchmark on one MI355X.
+
+Workload (one "step"): the W8A8 linear stack of one LLaMA-7B decode step at
+M decode rows (default 8): 32 layers x {packed QKV [12288x4096], O
+[4096x4096], packed gate/up [22016x4096] with fused SiLU*mul -> [M, 11008],
+down [4096x11008]}.  Every layer has its own random-init weights (~N(0, 0.02),
+per-output int8, 6.48 GB packed in HBM) so nothing is served from the 256 MB
+Infinity Cache; RMSNorm and attention are stubbed by seeded fp16 activations,
+and the down projection consumes the gate/up output.  The step is captured
+once in a HIP graph and replayed.  Inputs are resident in HBM before timing.
+
+`value` = algorithmic HBM bytes of the step / step time (GB/s), with bytes =
+N*K + 2N + 2MK + 2M*N_out per linear.  The `roofline` object is for the
+dominant kernel (the packed gate/up GEMV with fused SiLU*mul), timed with HIP
+events on the stream it is launched on.  `cpu_baseline` times the numpy
+restatement of the reference CPU integer path on a bounded sample (rank 0,
+N=1 only).  `extra` carries per-projection decode GB/s at M=1,4,8 and the
+prefill GEMM TOPS at M=560.
+
+    python bench.py [--steps K] [--warmup W] [--m 8] [--no-extra] [--no-cpu]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "nano-pointllm_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--m", type=int, default=8, help="decode rows (tokens) per step")
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--no-extra", action="store_true", help="skip the per-projection sweeps")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU sample")
+    return ap.parse_args()
+
+
+class Layer:
+    """One decoder layer's four packed W8A8 projections plus stub inputs."""
+
+    def __init__(self, idx: int, m: int, device):
+        import torch
+
+        from nanopointllm_amd import _lib, w8a8, workloads as W
+        from nanopointllm_amd.linear import PackedW8A8Weight
+
+        self.weights = {}
+        for j, spec in enumerate(W.PROJECTIONS):
+            w16 = W.linear_weight(spec.n, spec.k, seed=1000 * idx + j, device=device)
+            layout = _lib.ROWS_INTERLEAVE_HALVES if spec.silu else _lib.ROWS_AS_IS
+            self.weights[spec.name] = PackedW8A8Weight.from_float(w16, None, layout=layout)
+            del w16
+        self.x = {name: W.decode_activations(m, W.HIDDEN, seed=100 * idx + j).to(device)
+                  for j, name in enumerate(("qkv", "o", "gateup"))}
+        self.m = m
+        self.w8a8 = w8a8
+        self.lib = _lib
+        torch.cuda.synchronize()
+
+    def step(self):
+        w, x, f = self.weights, self.x, self.w8a8
+        f.linear_dynamic(x["qkv"], w["qkv"].packed, w["qkv"].scale, None, w["qkv"].out_features)
+        f.linear_dynamic(x["o"], w["o"].packed, w["o"].scale, None, w["o"].out_features)
+        h = f.linear_dynamic(x["gateup"], w["gateup"].packed, w["gateup"].scale, None,
+                             w["gateup"].out_features, epilogue=self.lib.EPI_SILU_MUL)
+        f.linear_dynamic(h, w["down"].packed, w["down"].scale, None, w["down"].out_features)
+
+
+def step_bytes(m: int, layers: int) -> int:
+    from nanopointllm_amd import workloads as W
+
+    return layers * sum(W.algorithmic_bytes(m, p.n, p.k, silu=p.silu) for p in W.PROJECTIONS)
+
+
+def time_graph(fn, steps: int, warmup: int):
+    """Capture fn in a HIP graph; return (ms per replay, graph)."""
+    import torch
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()                               # eager warm-up (allocator, code objects)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        g.replay()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) * 1e3 / steps, g
+
+
+def event_time_ms(fn, reps: int) -> float:
+    """Average ms of fn over reps, bracketed by HIP events on the current stream."""
+    import torch
+
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    start.record()
+    for _ in range(reps):
+        fn()
+    stop.record()
+    stop.synchronize()
+    return start.elapsed_time(stop) / reps
+
+
+def gateup_kernel_roofline(layers, m: int, device) -> dict:
+    """Average duration of the gate/up GEMV kernel alone (int8-in, fused SiLU*mul)."""
+    import torch
+
+    from nanopointllm_amd import _lib, w8a8, workloads as W
+
+    spec = {p.name: p for p in W.PROJECTIONS}["gateup"]
+    xq, sx = w8a8.quant_rows(layers[0].x["gateup"])
+    outs = [torch.empty(m, spec.n // 2, dtype=torch.float16, device=device) for _ in layers]
+    ws = torch.empty(w8a8.workspace_bytes(m, spec.k), dtype=torch.uint8, device=device)
+    lib = _lib.load()
+    stream = _lib.stream_handle(device)
+    args = []
+    for layer, y in zip(layers, outs):
+        p = layer.weights["gateup"]
+        args.append((xq.data_ptr(), spec.k, sx.data_ptr(), p.packed.data_ptr(), p.scale.data_ptr(),
+                     None, _lib.EPI_SILU_MUL, y.data_ptr(), _lib.F16, spec.n // 2, 0.0, _lib.F16,
+                     m, spec.n, spec.k, ws.data_ptr(), ws.numel(), stream))
+
+    def run_all():
+        for a in args:
+            rc = lib.w8a8_linear_i8in(*a)
+            if rc:
+                _lib.check(rc, "w8a8_linear_i8in")
+
+    reps = 20
+    ms = event_time_ms(run_all, reps) / len(args)
+    nbytes = W.algorithmic_bytes(m, spec.n, spec.k, silu=True, int8_in=True)
+    achieved = nbytes / (ms * 1e-3) / 1e9
+    return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "gemv_kernel (packed gate/up, SiLU*mul epilogue, int8 in)",
+            "avg_launch_us": round(ms * 1e3, 3), "algorithmic_bytes_per_launch": nbytes}
+
+
+def projection_sweep(layers, device, ms_list=(1, 4, 8)) -> dict:
+    """Decode GB/s per projection (graph of 32 launches over distinct weights)."""
+    import torch
+
+    from nanopointllm_amd import _lib, w8a8, workloads as W
+
+    out = {}
+    for m in ms_list:
+        row = {}
+        for spec in W.PROJECTIONS:
+            if spec.silu:
+                fn_args = dict(epilogue=_lib.EPI_SILU_MUL)
+            else:
+                fn_args = {}
+            x16 = W.decode_activations(m, spec.k, seed=7).to(device)
+
+            def run(spec=spec, x16=x16, fn_args=fn_args):
+                for layer in layers:
+                    p = layer.weights[spec.name]
+                    w8a8.linear_dynamic(x16, p.packed, p.scale, None, p.out_features, **fn_args)
+
+            ms, g = time_graph(run, steps=10, warmup=3)
+            del g
+            per = ms / len(layers)
+            nbytes = W.algorithmic_bytes(m, spec.n, spec.k, silu=spec.silu)
+            row[spec.name] = {"us": round(per * 1e3, 2),
+                              "GBps": round(nbytes / (per * 1e-3) / 1e9, 1)}
+        out[f"M{m}"] = row
+    torch.cuda.synchronize()
+    return out
+
+
+def prefill_sweep(layers, device, m: int = 560) -> dict:
+    """Prefill TOPS per projection: fused linear (quant + GEMM) and GEMM kernel alone."""
+    import torch
+
+    from nanopointllm_amd import _lib, w8a8, workloads as W
+
+    out = {}
+    for spec in W.PROJECTIONS:
+        x16 = W.prefill_activations(m, spec.k, seed=11).to(device)
+        xq, sx = w8a8.quant_rows(x16)
+        fn_args = dict(epilogue=_lib.EPI_SILU_MUL) if spec.silu else {}
+        sub = layers[:8]
+
+        def run_linear(spec=spec, x16=x16, fn_args=fn_args):
+            for layer in sub:
+                p = layer.weights[spec.name]
+                w8a8.linear_dynamic(x16, p.packed, p.scale, None, p.out_features, **fn_args)
+
+        def run_gemm(spec=spec, xq=xq, sx=sx, fn_args=fn_args):
+            for layer in sub:
+                p = layer.weights[spec.name]
+                w8a8.linear_i8in(xq, sx, p.packed, p.scale, None, p.out_features,
+                                 out_dtype=torch.float16, **fn_args)
+
+        ms_lin, g1 = time_graph(run_linear, steps=10, warmup=3)
+        ms_gemm, g2 = time_graph(run_gemm, steps=10, warmup=3)
+        del g1, g2
+        ops = W.algorithmic_ops(m, spec.n, spec.k)
+        lin = ms_lin / len(sub)
+        gemm = ms_gemm / len(sub)
+        out[spec.name] = {
+            "linear_us": round(lin * 1e3, 2),
+            "linear_TOPS": round(ops / (lin * 1e-3) / 1e12, 1),
+            "gemm_us": round(gemm * 1e3, 2),
+            "gemm_TOPS": round(ops / (gemm * 1e-3) / 1e12, 1),
+            "gemm_frac_int8_peak": round(ops / (gemm * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+        }
+    torch.cuda.synchronize()
+    return out
+
+
+def cpu_baseline(layers, m: int, n_layers: int) -> dict:
+    """Reference CPU integer path (numpy restatement) on `n_layers` layers."""
+    import numpy as np
+    import torch
+
+    from nanopointllm_amd import workloads as W
+    from oracle import w8a8_oracle as O
+
+    sample = []
+    for layer in layers[:n_layers]:
+        for spec in W.PROJECTIONS:
+            # Unpack the layer's int8 weight rows back to row-major on the host.
+            q = _unpack_rows(layer.weights[spec.name].packed.cpu().numpy(), spec.n, spec.k)
+            s = layer.weights[spec.name].scale.cpu().numpy()
+            x = (layer.x[spec.name] if spec.name in layer.x else
+                 W.decode_activations(m, spec.k, seed=5).to(torch.float16))
+            sample.append((spec, x.cpu().numpy(), q, s))
+    nbytes = 0
+    t0 = time.perf_counter()
+    for spec, x, q, s in sample:
+        out, _, _, _ = O.w8a8_linear_dynamic(x, q, s, exact_int=True)
+        if spec.silu:
+            O.silu_mul_hf(out[:, 0::2].astype(np.float16), out[:, 1::2].astype(np.float16))
+        else:
+            out.astype(np.float16)
+        nbytes += W.algorithmic_bytes(m, spec.n, spec.k, silu=spec.silu)
+    dt = time.perf_counter() - t0
+    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{n_layers} of 32 layers (4 projections each) at M={m}: numpy int32 "
+                      f"matmul restatement of integer_linear_per_output_reference, "
+                      f"{nbytes / 1e6:.1f} MB in {dt:.1f} s"}
+
+
+def _unpack_rows(packed, rows: int, k: int):
+    import numpy as np
+
+    rp, kp = -(-rows // 16) * 16, -(-k // 64) * 64
+    t = packed.reshape(rp // 16, kp // 64, 4, 16, 16).transpose(0, 3, 1, 2, 4)
+    return np.ascontiguousarray(t.reshape(rp, kp)[:rows, :k])
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the W8A8 path "
+              "is single-GPU; sharding is described in DESIGN.md).", file=sys.stderr)
+        return 2
+    import torch
+
+    from nanopointllm_amd import _lib, workloads as W
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 2
+    _lib.load()
+    device = torch.device("cuda:0")
+    m = args.m
+    log(f"building {args.layers} layers of packed W8A8 weights (M={m})")
+    layers = [Layer(i, m, device) for i in range(args.layers)]
+
+    def step():
+        for layer in layers:
+            layer.step()
+
+    log("capturing step graph")
+    ms_per_step, graph = time_graph(step, args.steps, args.warmup)
+    nbytes = step_bytes(m, args.layers)
+    value = nbytes / (ms_per_step * 1e-3) / 1e9
+    log(f"step {ms_per_step:.4f} ms, {value:.1f} GB/s")
+    del graph
+
+    log("timing gate/up GEMV kernel")
+    roofline = gateup_kernel_roofline(layers, m, device)
+    log(f"gate/up kernel {roofline['avg_launch_us']} us, {roofline['achieved']} GB/s")
+
+    extra = {}
+    if not args.no_extra:
+        log("decode sweep M=1,4,8")
+        extra["decode_per_projection"] = projection_sweep(layers, device)
+        log("prefill sweep M=560")
+        extra["prefill_M560"] = prefill_sweep(layers, device)
+
+    cpu = None
+    if not args.no_cpu:
+        log(f"cpu baseline on {args.cpu_layers} layers")
+        cpu = cpu_baseline(layers, m, args.cpu_layers)
+        log(f"cpu {cpu['value']} GB/s")
+
+    result = {
+        "metric": "W8A8 GEMV HBM GB/s & GEMM int8 TOPS (% roofline) at M=1,8,560, LLaMA-7B",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic",
+        "config": {"workload": f"llama7b_decode_w8a8_linear_stack_{args.layers}L",
+                   "m": m, "layers": args.layers,
+                   "projections": {p.name: [p.n, p.k] for p in W.PROJECTIONS},
+                   "weights": "random-init ~N(0,0.02), per-output int8, packed",
+                   "bytes_per_step": nbytes, "graph": True},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,173 @@
+/*
+ * w8a8_gfx950.h - C ABI of libw8a8_gfx950.so, the MI355X (gfx950) W8A8
+ * quantized linear path of nanopointllm.
+ *
+ * The reference has no FFI: its boundary is the Python call sites of
+ * F.linear / torch.matmul in nanopointllm/llama/{lightweight_runner,
+ * paged_attention}.py and the function API of nanopointllm/compression/
+ * {w8a8,quantized_tensor_package}.py.  Each entry point below names the
+ * reference interface it replaces.  A Python binding (ctypes) is in
+ * nano-pointllm_amd/nanopointllm_amd/_lib.py.
+ *
+ * Conventions
+ *  - Every pointer is device memory owned by the caller, except where noted.
+ *    The library never allocates; scratch is the caller's `workspace`
+ *    (size from w8a8_workspace_bytes), so every call is graph-capturable.
+ *  - Work is enqueued on `stream` and never synchronizes the host.
+ *  - Return value: W8A8_OK (0) or a negative w8a8_status.  Nothing throws.
+ *  - Integer results are exact; int8 values are in [-127, 127]; scales are
+ *    binary32 holding binary16-representable values (CONTRACT,
+ *    nanopointllm/compression/w8a8.py:14-30).
+ *  - Packed weights use the 16x64 tile layout described at
+ *    w8a8_pack_rows; their size is w8a8_packed_bytes(rows, k).
+ */
+#ifndef W8A8_GFX950_H
+#define W8A8_GFX950_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define W8A8_ABI_VERSION 1
+
+typedef enum w8a8_dtype {
+  W8A8_F32 = 0,
+  W8A8_F16 = 1,
+  W8A8_BF16 = 2,
+  W8A8_I32 = 3,
+  W8A8_I8 = 4
+} w8a8_dtype;
+
+typedef enum w8a8_status {
+  W8A8_OK = 0,
+  W8A8_ERR_NULL = -1,      /* required pointer is null */
+  W8A8_ERR_SHAPE = -2,     /* negative size, leading dimension too small, K overflow */
+  W8A8_ERR_DTYPE = -3,     /* unsupported dtype / epilogue combination */
+  W8A8_ERR_ALIGN = -4,     /* pointer or leading dimension misaligned */
+  W8A8_ERR_WORKSPACE = -5, /* workspace missing or too small */
+  W8A8_ERR_HIP = -6        /* kernel launch failed; see w8a8_last_hip_error */
+} w8a8_status;
+
+typedef enum w8a8_epilogue {
+  /* y[m, n] = int32 accumulator */
+  W8A8_EPI_I32 = 0,
+  /* y[m, n] = cast(f32(acc) * s_x[m] * s_w[n] + bias[n]), binary32 steps
+   * (integer_linear_per_output_reference, w8a8.py:134-137) */
+  W8A8_EPI_DEQUANT = 1,
+  /* interleaved packed gate/up (rows g0,u0,g1,u1,...):
+   * g,u = inter(dequant); y[m, c] = inter(inter(SiLU(g)) * u)
+   * (LightweightMLP packed branch, lightweight_runner.py:344-358) */
+  W8A8_EPI_SILU_MUL = 2,
+  /* as W8A8_EPI_SILU_MUL, then int8 = quantize_symmetric(h, y_scale)
+   * (static A8 requant feeding the down projection, w8a8.py:33-43,94-103) */
+  W8A8_EPI_SILU_MUL_Q8 = 3
+} w8a8_epilogue;
+
+typedef enum w8a8_row_layout {
+  W8A8_ROWS_AS_IS = 0,
+  /* source rows [gate(0..R/2); up(0..R/2)] packed as g0,u0,g1,u1,...
+   * (_pack_gateup_tensors layout "interleave", lightweight_runner.py:81-92) */
+  W8A8_ROWS_INTERLEAVE_HALVES = 1
+} w8a8_row_layout;
+
+/* Library ABI version (W8A8_ABI_VERSION). */
+int w8a8_abi_version(void);
+
+/* Static text for a w8a8_status value. */
+const char* w8a8_status_string(int status);
+
+/* hipError_t of the last failed launch on the calling thread (0 if none). */
+int w8a8_last_hip_error(void);
+
+/* Bytes of a packed [rows, k] int8 operand: ceil(rows/16)*16 * ceil(k/64)*64. */
+int64_t w8a8_packed_bytes(int64_t rows, int64_t k);
+
+/* Workspace bytes needed by w8a8_linear / w8a8_linear_i8in / w8a8_gemm_i32
+ * for an [m, k] activation. */
+int64_t w8a8_workspace_bytes(int64_t m, int64_t k);
+
+/*
+ * Per-row symmetric int8 quantization with a dynamic scale per row:
+ *   scales[r] = scale_from_absmax(max_k |x[r, k]|)
+ *   q[r, k]   = quantize_symmetric(x[r, k], scales[r])
+ * Replaces dynamic_per_token_activation_qdq (w8a8.py:106-115, integer part)
+ * for activations and per_output_weight_qdq (w8a8.py:53-62) for weights.
+ * x: [rows, ldx] of x_dtype (F32/F16/BF16); q: int8 [rows, ldq]; scales: [rows].
+ */
+int w8a8_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                    int8_t* q, int64_t ldq, float* scales, hipStream_t stream);
+
+/*
+ * quantize_symmetric (w8a8.py:33-43) with caller scales: scale[r * scale_stride]
+ * (scale_stride 0: one per-tensor scale, the static_activation_qdq case,
+ * w8a8.py:101-103).  Scales must be positive; the caller checks that, as the
+ * reference's ValueError check does on the host.
+ */
+int w8a8_quant_rows_scaled(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                           const float* scale, int64_t scale_stride, int8_t* q, int64_t ldq,
+                           hipStream_t stream);
+
+/*
+ * Packs a row-major int8 [rows, k] matrix (leading dimension ld) into 16x64
+ * MFMA tiles: tile (rb, kb) at byte (rb*ceil(k/64) + kb)*1024; inside it lane
+ * slot l = r + 16g (16 bytes) holds row 16rb + r, columns 64kb + 16g .. +15;
+ * padding is zero.  layout W8A8_ROWS_INTERLEAVE_HALVES reorders rows as the
+ * reference's interleaved gate/up packing.  Replaces the packed-weight
+ * construction of PagedLlamaAttention.from_hf (paged_attention.py:1242-1262)
+ * and _pack_gateup_tensors (lightweight_runner.py:57-93) for int8 weights.
+ * packed: w8a8_packed_bytes(rows, k) bytes, 16-byte aligned.
+ */
+int w8a8_pack_rows(const int8_t* src, int64_t rows, int64_t k, int64_t ld, int layout,
+                   int8_t* packed, hipStream_t stream);
+
+/*
+ * Raw int32 accumulators acc[m, n] = sum_k xq[m, k] * wq[n, k]: the
+ * `flat @ qweight_cpu.transpose(0, 1)` of integer_linear_per_output_reference
+ * (w8a8.py:131-133) and QuantizedLinearTensors.integer_golden
+ * (quantized_tensor_package.py:39-43).  xq: int8 [m, ldq]; w_packed from
+ * w8a8_pack_rows; acc: int32 [m, ldacc].
+ */
+int w8a8_gemm_i32(const int8_t* xq, int64_t ldq, const int8_t* w_packed, int32_t* acc,
+                  int64_t ldacc, int64_t m, int64_t n, int64_t k, void* workspace,
+                  int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * Fused W8A8 linear with dynamic per-token activation quantization:
+ *   s_x = scale_from_absmax(row absmax of x); xq = quantize_symmetric(x, s_x);
+ *   acc = xq @ wq^T (int32); y = epilogue(acc).
+ * Replaces F.linear(x, W, b) at the packed QKV / O / gate-up / down call sites
+ * (paged_attention.py:97-124,1349-1352,1488; lightweight_runner.py:38-54,
+ * 329-379) with the W8A8 contract of integer_linear_per_output_reference
+ * (w8a8.py:118-139, per-token activation scale).
+ *   x: [m, ldx] of x_dtype; w_packed/w_scale/bias: [n] per output (bias
+ *   nullable, binary32); y: [m, ldy] of y_dtype (n/2 columns for the SiLU
+ *   epilogues); y_scale: static scale of W8A8_EPI_SILU_MUL_Q8; inter_dtype
+ *   (F16/BF16): rounding type of the SiLU intermediates; x_scale_out: nullable
+ *   [m], receives s_x.
+ */
+int w8a8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
+                const float* w_scale, const float* bias, int epilogue, void* y, int y_dtype,
+                int64_t ldy, float y_scale, int inter_dtype, int64_t m, int64_t n, int64_t k,
+                float* x_scale_out, void* workspace, int64_t workspace_bytes,
+                hipStream_t stream);
+
+/*
+ * As w8a8_linear for already-quantized activations xq (int8 [m, ldq]) with
+ * per-row scales x_scale[m]: the int8-in down projection fed by
+ * W8A8_EPI_SILU_MUL_Q8 or w8a8_quant_rows (w8a8.py:118-139 with a given
+ * activation_scale).
+ */
+int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
+                     const int8_t* w_packed, const float* w_scale, const float* bias,
+                     int epilogue, void* y, int y_dtype, int64_t ldy, float y_scale,
+                     int inter_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                     int64_t workspace_bytes, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* W8A8_GFX950_H */

@@ -1,0 +1,291 @@
+// extern "C" entry points of libw8a8_gfx950.so (declared in
+// include/w8a8_gfx950.h).  Validation and dispatch only: shapes, dtypes,
+// alignment and workspace are checked here and reported as status codes; the
+// kernels live in quant.hip, gemv.hip and gemm.hip.
+#include "w8a8_gfx950.h"
+#include "w8a8_internal.h"
+
+using namespace w8a8;
+
+namespace {
+
+thread_local int g_last_hip_error = 0;
+
+// Largest K whose worst-case dot product K * 127^2 fits a signed int32
+// (the overflow guard of compare_linear_bf16_qdq_integer, w8a8.py:152-153).
+constexpr int64_t kMaxK = ((int64_t{1} << 31) - 1) / (127 * 127);
+
+inline int status_of(hipError_t e) {
+  if (e == hipSuccess) return W8A8_OK;
+  g_last_hip_error = static_cast<int>(e);
+  return W8A8_ERR_HIP;
+}
+
+inline bool aligned(const void* p, uintptr_t a) {
+  return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0;
+}
+
+inline int64_t round_up(int64_t v, int64_t m) { return ceil_div(v, m) * m; }
+
+inline bool float_dtype(int d) { return d == kF32 || d == kF16 || d == kBF16; }
+inline bool half_dtype(int d) { return d == kF16 || d == kBF16; }
+
+inline int64_t elem_size(int d) {
+  switch (d) {
+    case kF32:
+    case kI32:
+      return 4;
+    case kF16:
+    case kBF16:
+      return 2;
+    case kI8:
+      return 1;
+    default:
+      return 0;
+  }
+}
+
+// Workspace layout: [activation scales: round_up(4m, 256)] [int8 activations:
+// ceil(m/16)*16 rows x ceil(k/64)*64 columns, row-major (GEMV) or packed (GEMM)].
+inline int64_t scale_region(int64_t m) { return round_up(4 * m, 256); }
+inline int64_t act_region(int64_t m, int64_t k) {
+  return round_up(m, kTileRows) * round_up(k, kTileK);
+}
+
+// Checks an epilogue / output dtype pair and returns the number of output
+// columns, or -1 when the combination is unsupported.
+inline int64_t output_cols(int epi, int y_dtype, int inter_dtype, int64_t n) {
+  switch (epi) {
+    case W8A8_EPI_I32:
+      return y_dtype == kI32 ? n : -1;
+    case W8A8_EPI_DEQUANT:
+      return float_dtype(y_dtype) ? n : -1;
+    case W8A8_EPI_SILU_MUL:
+      return (half_dtype(y_dtype) && n % 2 == 0) ? n / 2 : -1;
+    case W8A8_EPI_SILU_MUL_Q8:
+      return (y_dtype == kI8 && half_dtype(inter_dtype) && n % 2 == 0) ? n / 2 : -1;
+    default:
+      return -1;
+  }
+}
+
+// Common checks of the weight side and output of a linear.
+inline int check_linear(const int8_t* w_packed, const float* w_scale, int epi, void* y,
+                        int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,
+                        int64_t n, int64_t k) {
+  if (m < 0 || n < 0 || k < 0) return W8A8_ERR_SHAPE;
+  if (k > kMaxK) return W8A8_ERR_SHAPE;
+  const int64_t cols = output_cols(epi, y_dtype, inter_dtype, n);
+  if (cols < 0) return W8A8_ERR_DTYPE;
+  if (m == 0 || n == 0) return W8A8_OK;
+  // With k == 0 the packed weights are empty (and may be null): the product
+  // kernels read no k-blocks and write bias-only / zero outputs.
+  if ((k > 0 && w_packed == nullptr) || y == nullptr) return W8A8_ERR_NULL;
+  if (epi != W8A8_EPI_I32 && w_scale == nullptr) return W8A8_ERR_NULL;
+  if (ldy < cols) return W8A8_ERR_SHAPE;
+  if (!aligned(w_packed, 16) || !aligned(y, static_cast<uintptr_t>(elem_size(y_dtype))))
+    return W8A8_ERR_ALIGN;
+  if (epi == W8A8_EPI_SILU_MUL_Q8 && !(y_scale > 0.0f)) return W8A8_ERR_SHAPE;
+  return W8A8_OK;
+}
+
+LinearOperands make_ops(const int8_t* a, int64_t lda, const float* sx, const int8_t* w,
+                        const float* sw, const float* bias, int epi, void* y, int y_dtype,
+                        int64_t ldy, float y_scale, int inter_dtype, int64_t m, int64_t n,
+                        int64_t k) {
+  LinearOperands op;
+  op.a = a;
+  op.lda = lda;
+  op.sx = sx;
+  op.w = w;
+  op.sw = sw;
+  op.bias = bias;
+  op.y = y;
+  op.ldy = ldy;
+  op.y_dtype = y_dtype;
+  op.h_dtype = inter_dtype;
+  op.out_scale = y_scale;
+  op.M = m;
+  op.N = n;
+  op.K = k;
+  op.epi = epi;
+  return op;
+}
+
+// Runs the int8 product for activations already staged in `act` (row-major
+// [m, round_up(k,64)] for the GEMV, packed tiles for the GEMM).
+inline hipError_t run_product(const LinearOperands& op, hipStream_t st) {
+  return op.M <= kGemvMaxRows ? launch_gemv(op, st) : launch_gemm(op, st);
+}
+
+// Stages caller int8 activations for run_product: the GEMV reads them in
+// place when rows are 16-byte aligned and zero-padded reads are not needed;
+// otherwise they are copied (GEMV) or packed (GEMM) into the workspace.
+inline hipError_t stage_i8(const int8_t* xq, int64_t ldq, int64_t m, int64_t k, int8_t* act,
+                           const int8_t** a, int64_t* lda, hipStream_t st) {
+  const int64_t kp = round_up(k, kTileK);
+  if (m <= kGemvMaxRows) {
+    if (k % kTileK == 0 && ldq % 16 == 0 && aligned(xq, 16)) {
+      *a = xq;
+      *lda = ldq;
+      return hipSuccess;
+    }
+    *a = act;
+    *lda = kp;
+    return launch_pad_rows(xq, m, k, ldq, act, kp, st);
+  }
+  *a = act;
+  *lda = kp;
+  return launch_pack_rows(xq, m, k, ldq, W8A8_ROWS_AS_IS, act, st);
+}
+
+}  // namespace
+
+extern "C" {
+
+int w8a8_abi_version(void) { return W8A8_ABI_VERSION; }
+
+const char* w8a8_status_string(int status) {
+  switch (status) {
+    case W8A8_OK:
+      return "ok";
+    case W8A8_ERR_NULL:
+      return "required pointer is null";
+    case W8A8_ERR_SHAPE:
+      return "invalid shape, leading dimension or scale";
+    case W8A8_ERR_DTYPE:
+      return "unsupported dtype or epilogue";
+    case W8A8_ERR_ALIGN:
+      return "misaligned pointer or leading dimension";
+    case W8A8_ERR_WORKSPACE:
+      return "workspace missing or too small";
+    case W8A8_ERR_HIP:
+      return "HIP kernel launch failed";
+    default:
+      return "unknown status";
+  }
+}
+
+int w8a8_last_hip_error(void) { return g_last_hip_error; }
+
+int64_t w8a8_packed_bytes(int64_t rows, int64_t k) {
+  if (rows < 0 || k < 0) return -1;
+  return round_up(rows, kTileRows) * round_up(k, kTileK);
+}
+
+int64_t w8a8_workspace_bytes(int64_t m, int64_t k) {
+  if (m < 0 || k < 0) return -1;
+  return scale_region(m) + act_region(m, k);
+}
+
+int w8a8_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                    int8_t* q, int64_t ldq, float* scales, hipStream_t stream) {
+  if (rows < 0 || k < 0) return W8A8_ERR_SHAPE;
+  if (!float_dtype(x_dtype)) return W8A8_ERR_DTYPE;
+  if (rows == 0) return W8A8_OK;
+  if (x == nullptr || q == nullptr || scales == nullptr) return W8A8_ERR_NULL;
+  if (ldx < k || ldq < k) return W8A8_ERR_SHAPE;
+  if (!aligned(x, static_cast<uintptr_t>(elem_size(x_dtype))) || !aligned(scales, 4))
+    return W8A8_ERR_ALIGN;
+  return status_of(launch_quant_rows(x, x_dtype, ldx, rows, k, nullptr, 0, q, ldq, k, false,
+                                     scales, stream));
+}
+
+int w8a8_quant_rows_scaled(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
+                           const float* scale, int64_t scale_stride, int8_t* q, int64_t ldq,
+                           hipStream_t stream) {
+  if (rows < 0 || k < 0 || scale_stride < 0) return W8A8_ERR_SHAPE;
+  if (!float_dtype(x_dtype)) return W8A8_ERR_DTYPE;
+  if (rows == 0) return W8A8_OK;
+  if (x == nullptr || q == nullptr || scale == nullptr) return W8A8_ERR_NULL;
+  if (ldx < k || ldq < k) return W8A8_ERR_SHAPE;
+  if (!aligned(x, static_cast<uintptr_t>(elem_size(x_dtype))) || !aligned(scale, 4))
+    return W8A8_ERR_ALIGN;
+  return status_of(launch_quant_rows(x, x_dtype, ldx, rows, k, scale, scale_stride, q, ldq, k,
+                                     false, nullptr, stream));
+}
+
+int w8a8_pack_rows(const int8_t* src, int64_t rows, int64_t k, int64_t ld, int layout,
+                   int8_t* packed, hipStream_t stream) {
+  if (rows < 0 || k < 0) return W8A8_ERR_SHAPE;
+  if (layout != W8A8_ROWS_AS_IS && layout != W8A8_ROWS_INTERLEAVE_HALVES) return W8A8_ERR_DTYPE;
+  if (layout == W8A8_ROWS_INTERLEAVE_HALVES && rows % 2 != 0) return W8A8_ERR_SHAPE;
+  if (rows == 0 || k == 0) return W8A8_OK;
+  if (src == nullptr || packed == nullptr) return W8A8_ERR_NULL;
+  if (ld < k) return W8A8_ERR_SHAPE;
+  if (!aligned(packed, 16)) return W8A8_ERR_ALIGN;
+  return status_of(launch_pack_rows(src, rows, k, ld, layout, packed, stream));
+}
+
+int w8a8_gemm_i32(const int8_t* xq, int64_t ldq, const int8_t* w_packed, int32_t* acc,
+                  int64_t ldacc, int64_t m, int64_t n, int64_t k, void* workspace,
+                  int64_t workspace_bytes, hipStream_t stream) {
+  int rc = check_linear(w_packed, nullptr, W8A8_EPI_I32, acc, kI32, ldacc, 0.0f, kF16, m, n, k);
+  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
+  if (k > 0 && xq == nullptr) return W8A8_ERR_NULL;
+  if (ldq < k) return W8A8_ERR_SHAPE;
+  if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
+    return W8A8_ERR_WORKSPACE;
+  if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
+  int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
+  const int8_t* a = nullptr;
+  int64_t lda = 0;
+  hipError_t e = stage_i8(xq, ldq, m, k, act, &a, &lda, stream);
+  if (e != hipSuccess) return status_of(e);
+  LinearOperands op = make_ops(a, lda, nullptr, w_packed, nullptr, nullptr, W8A8_EPI_I32, acc,
+                               kI32, ldacc, 0.0f, kF16, m, n, k);
+  return status_of(run_product(op, stream));
+}
+
+int w8a8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
+                const float* w_scale, const float* bias, int epilogue, void* y, int y_dtype,
+                int64_t ldy, float y_scale, int inter_dtype, int64_t m, int64_t n, int64_t k,
+                float* x_scale_out, void* workspace, int64_t workspace_bytes,
+                hipStream_t stream) {
+  if (!float_dtype(x_dtype)) return W8A8_ERR_DTYPE;
+  int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
+                        n, k);
+  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
+  if (x == nullptr) return W8A8_ERR_NULL;
+  if (ldx < k) return W8A8_ERR_SHAPE;
+  if (!aligned(x, static_cast<uintptr_t>(elem_size(x_dtype)))) return W8A8_ERR_ALIGN;
+  if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
+    return W8A8_ERR_WORKSPACE;
+  if (!aligned(workspace, 16) || (x_scale_out != nullptr && !aligned(x_scale_out, 4)))
+    return W8A8_ERR_ALIGN;
+  float* sx = x_scale_out != nullptr ? x_scale_out : static_cast<float*>(workspace);
+  int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
+  const int64_t kp = round_up(k, kTileK);
+  const bool gemv = m <= kGemvMaxRows;
+  hipError_t e = launch_quant_rows(x, x_dtype, ldx, m, k, nullptr, 0, act, kp, kp, !gemv, sx,
+                                   stream);
+  if (e != hipSuccess) return status_of(e);
+  LinearOperands op = make_ops(act, kp, sx, w_packed, w_scale, bias, epilogue, y, y_dtype, ldy,
+                               y_scale, inter_dtype, m, n, k);
+  return status_of(run_product(op, stream));
+}
+
+int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
+                     const int8_t* w_packed, const float* w_scale, const float* bias,
+                     int epilogue, void* y, int y_dtype, int64_t ldy, float y_scale,
+                     int inter_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                     int64_t workspace_bytes, hipStream_t stream) {
+  int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
+                        n, k);
+  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
+  if (xq == nullptr || (epilogue != W8A8_EPI_I32 && x_scale == nullptr)) return W8A8_ERR_NULL;
+  if (ldq < k) return W8A8_ERR_SHAPE;
+  if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
+    return W8A8_ERR_WORKSPACE;
+  if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
+  int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
+  const int8_t* a = nullptr;
+  int64_t lda = 0;
+  hipError_t e = stage_i8(xq, ldq, m, k, act, &a, &lda, stream);
+  if (e != hipSuccess) return status_of(e);
+  LinearOperands op = make_ops(a, lda, x_scale, w_packed, w_scale, bias, epilogue, y, y_dtype,
+                               ldy, y_scale, inter_dtype, m, n, k);
+  return status_of(run_product(op, stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,225 @@
+// Decode-regime W8A8 GEMV (M <= 64): y[m, n] = epi(sum_k xq[m, k] * wq[n, k]).
+//
+// Replaces the F.linear call sites of the decode path
+// (llama/paged_attention.py:97-124, llama/lightweight_runner.py:38-54,
+// 329-379) for the int8 contract of integer_linear_per_output_reference
+// (nanopointllm/compression/w8a8.py:118-139).
+//
+// Design (HBM-bound): one workgroup per 16-output block of packed weights.
+// Its WAVES wavefronts split K into contiguous k-block ranges, so each wave
+// streams a contiguous slab of the block's 16 x K packed tile column with
+// fully coalesced 1 KiB global_load_dwordx4 (one MFMA B fragment per load),
+// double-buffered CH fragments deep in registers.  The activation fragment of
+// each k-block (16 rows x 64 int8) comes from the L2-resident quantized
+// activations.  v_mfma_i32_16x16x64_i8 does the int8 dot products (16 cycles of
+// the matrix pipe per KiB of weights, so the VALU stays free), then the
+// per-wave 16x16 int32 partial tiles are summed through LDS and the fused
+// epilogue (dequant / SiLU*mul / int8 requant) writes the outputs.
+#include "w8a8_internal.h"
+
+namespace w8a8 {
+
+namespace {
+
+struct GemvParams {
+  const int8_t* xq;
+  int64_t ldq;
+  const float* sx;
+  const i32x4* w;
+  const float* sw;
+  const float* bias;
+  void* y;
+  int64_t ldy;
+  float out_scale;
+  int M;
+  int N;
+  int KB;
+};
+
+__device__ inline i32x4 mfma_16x16x64(i32x4 a, i32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+template <int WAVES, int MT, int CH, int EPI, typename TY, typename TH>
+__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
+  constexpr int NT = WAVES * 64;
+  __shared__ int32_t red[WAVES][MT * 256];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int li = lane & 15;
+  const int lg = lane >> 4;
+  const int64_t nb = blockIdx.x;
+  const int KB = p.KB;
+  const int kb_begin = (KB * wave) / WAVES;
+  const int kb_end = (KB * (wave + 1)) / WAVES;
+
+  const i32x4* wt = p.w + nb * KB * 64 + lane;
+  const int8_t* arow[MT];
+  bool alive[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int m = mt * 16 + li;
+    alive[mt] = m < p.M;
+    arow[mt] = p.xq + static_cast<int64_t>(alive[mt] ? m : 0) * p.ldq + lg * 16;
+  }
+
+  i32x4 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = i32x4{0, 0, 0, 0};
+
+  i32x4 wb0[CH], wb1[CH];
+  i32x4 ab0[MT][CH], ab1[MT][CH];
+
+  // Loads CH k-blocks starting at kc.  Indices past the wave's range are
+  // clamped to its last k-block (an in-bounds, cache-hot address); their
+  // MFMAs are skipped in compute().
+  auto load = [&](i32x4(&wb)[CH], i32x4(&ab)[MT][CH], int kc) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int kb = (kc + c < kb_end) ? kc + c : kb_end - 1;
+      wb[c] = __builtin_nontemporal_load(wt + static_cast<int64_t>(kb) * 64);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        ab[mt][c] = alive[mt] ? *reinterpret_cast<const i32x4*>(arow[mt] + kb * 64)
+                              : i32x4{0, 0, 0, 0};
+      }
+    }
+  };
+  auto compute = [&](const i32x4(&wb)[CH], const i32x4(&ab)[MT][CH], int kc) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      if (kc + c < kb_end) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = mfma_16x16x64(ab[mt][c], wb[c], acc[mt]);
+      }
+    }
+  };
+
+  if (kb_begin < kb_end) {
+    load(wb0, ab0, kb_begin);
+    for (int kc = kb_begin; kc < kb_end; kc += 2 * CH) {
+      const bool second = kc + CH < kb_end;
+      if (second) load(wb1, ab1, kc + CH);
+      compute(wb0, ab0, kc);
+      if (second) {
+        if (kc + 2 * CH < kb_end) load(wb0, ab0, kc + 2 * CH);
+        compute(wb1, ab1, kc + CH);
+      }
+    }
+  }
+
+  // C layout of v_mfma_i32_16x16x64_i8: lane (li, lg), register r holds
+  // row 4*lg + r (activation row) and column li (output within the block).
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[wave][mt * 256 + (4 * lg + r) * 16 + li] = acc[mt][r];
+  }
+  __syncthreads();
+
+  if constexpr (EPI == kEpiI32 || EPI == kEpiDequant) {
+    for (int e = tid; e < MT * 256; e += NT) {
+      const int m = (e >> 8) * 16 + ((e & 255) >> 4);
+      const int64_t n = nb * 16 + (e & 15);
+      if (m >= p.M || n >= p.N) continue;
+      int32_t s = 0;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) s += red[w][e];
+      TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n;
+      if constexpr (EPI == kEpiI32) {
+        *y = s;
+      } else {
+        *y = from_f32<TY>(dequant1(s, p.sx[m], p.sw[n], p.bias, n));
+      }
+    }
+  } else {
+    // Interleaved gate/up: packed rows 2c (gate) and 2c+1 (up) of this block
+    // produce output column nb*8 + c.
+    const int64_t n_out_total = p.N / 2;
+    for (int e = tid; e < MT * 128; e += NT) {
+      const int mt = e >> 7;
+      const int i = (e & 127) >> 3;
+      const int c = e & 7;
+      const int m = mt * 16 + i;
+      const int64_t n_out = nb * 8 + c;
+      if (m >= p.M || n_out >= n_out_total) continue;
+      const int base = mt * 256 + i * 16 + 2 * c;
+      int32_t sg = 0, su = 0;
+#pragma unroll
+      for (int w = 0; w < WAVES; ++w) {
+        sg += red[w][base];
+        su += red[w][base + 1];
+      }
+      const int64_t ng = nb * 16 + 2 * c;
+      const float sxm = p.sx[m];
+      const float g = to_f32(from_f32<TH>(dequant1(sg, sxm, p.sw[ng], p.bias, ng)));
+      const float u = to_f32(from_f32<TH>(dequant1(su, sxm, p.sw[ng + 1], p.bias, ng + 1)));
+      const TH h = from_f32<TH>(silu_mul<TH>(g, u));
+      TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n_out;
+      if constexpr (EPI == kEpiSilu) {
+        *y = h;
+      } else {
+        *y = static_cast<int8_t>(quant1(to_f32(h), p.out_scale));
+      }
+    }
+  }
+}
+
+template <int MT, int CH, int EPI, typename TY, typename TH>
+hipError_t launch_cfg(const GemvParams& p, int64_t nblocks, hipStream_t st) {
+  constexpr int WAVES = 4;
+  hipLaunchKernelGGL((gemv_kernel<WAVES, MT, CH, EPI, TY, TH>),
+                     dim3(static_cast<unsigned>(nblocks)), dim3(WAVES * 64), 0, st, p);
+  return hipGetLastError();
+}
+
+template <int EPI, typename TY, typename TH>
+hipError_t launch_mt(const GemvParams& p, int64_t nblocks, hipStream_t st) {
+  if (p.M <= 16) return launch_cfg<1, 8, EPI, TY, TH>(p, nblocks, st);
+  if (p.M <= 32) return launch_cfg<2, 4, EPI, TY, TH>(p, nblocks, st);
+  return launch_cfg<4, 2, EPI, TY, TH>(p, nblocks, st);
+}
+
+}  // namespace
+
+hipError_t launch_gemv(const LinearOperands& op, hipStream_t st) {
+  GemvParams p;
+  p.xq = op.a;
+  p.ldq = op.lda;
+  p.sx = op.sx;
+  p.w = reinterpret_cast<const i32x4*>(op.w);
+  p.sw = op.sw;
+  p.bias = op.bias;
+  p.y = op.y;
+  p.ldy = op.ldy;
+  p.out_scale = op.out_scale;
+  p.M = static_cast<int>(op.M);
+  p.N = static_cast<int>(op.N);
+  p.KB = static_cast<int>(ceil_div(op.K, kTileK));
+  const int64_t nblocks = ceil_div(op.N, kTileRows);
+  if (op.M <= 0 || nblocks == 0) return hipSuccess;
+  switch (op.epi) {
+    case kEpiI32:
+      return launch_mt<kEpiI32, int32_t, float>(p, nblocks, st);
+    case kEpiDequant:
+      if (op.y_dtype == kF16) return launch_mt<kEpiDequant, __half, float>(p, nblocks, st);
+      if (op.y_dtype == kBF16) return launch_mt<kEpiDequant, __hip_bfloat16, float>(p, nblocks, st);
+      if (op.y_dtype == kF32) return launch_mt<kEpiDequant, float, float>(p, nblocks, st);
+      return hipErrorInvalidValue;
+    case kEpiSilu:
+      if (op.y_dtype == kF16) return launch_mt<kEpiSilu, __half, __half>(p, nblocks, st);
+      if (op.y_dtype == kBF16)
+        return launch_mt<kEpiSilu, __hip_bfloat16, __hip_bfloat16>(p, nblocks, st);
+      return hipErrorInvalidValue;
+    case kEpiSiluQ8:
+      if (op.h_dtype == kF16) return launch_mt<kEpiSiluQ8, int8_t, __half>(p, nblocks, st);
+      if (op.h_dtype == kBF16) return launch_mt<kEpiSiluQ8, int8_t, __hip_bfloat16>(p, nblocks, st);
+      return hipErrorInvalidValue;
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace w8a8

@@ -1,0 +1,228 @@
+// Per-row symmetric int8 quantization and 16x64 tile packing.
+//
+// quant_rows_kernel restates, per row r of a [rows, K] matrix:
+//   scale_from_absmax  (nanopointllm/compression/w8a8.py:46-50)
+//   quantize_symmetric (nanopointllm/compression/w8a8.py:33-43)
+// It serves both per-token activation quantization
+// (dynamic_per_token_activation_qdq, w8a8.py:106-115) and per-output weight
+// quantization (per_output_weight_qdq, w8a8.py:53-62): both are "one scale per
+// row of a row-major matrix".
+#include "w8a8_internal.h"
+
+namespace w8a8 {
+
+namespace {
+
+constexpr int kQuantThreads = 256;
+
+// One workgroup per row.  Pass 1 reduces |x| over the row (or reads the
+// caller's scale); pass 2 quantizes 8 elements per thread-iteration and
+// writes either a row-major int8 row or the row's slots of the packed tiles.
+// For packed output the grid covers ceil(rows/16)*16 rows and every row
+// writes all ceil(K/64)*64 columns, so tile padding is zero-filled.
+template <typename TX, bool PACKED, bool DYNAMIC>
+__global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
+    const TX* __restrict__ x, int64_t ldx, int64_t rows, int64_t K, int vec_in,
+    const float* __restrict__ scale_in, int64_t scale_stride, int8_t* __restrict__ q,
+    int64_t ldq, int64_t ncols_out, int vec_out, int64_t KB, float* __restrict__ scales_out) {
+  __shared__ float red[kQuantThreads / 64];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const bool live = row < rows;
+  const TX* xr = x + (live ? row : 0) * ldx;
+  const int64_t nchunk_in = (K + 7) / 8;
+
+  float s = 1.0f;
+  if constexpr (DYNAMIC) {
+    float amax = 0.0f;
+    if (live) {
+      for (int64_t c = tid; c < nchunk_in; c += kQuantThreads) {
+        float v[8];
+        const int64_t k0 = c * 8;
+        load8(xr + k0, v, vec_in != 0, static_cast<int>(K - k0 < 8 ? K - k0 : 8));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+      }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    if ((tid & 63) == 0) red[tid >> 6] = amax;
+    __syncthreads();
+    amax = red[0];
+#pragma unroll
+    for (int w = 1; w < kQuantThreads / 64; ++w) amax = fmaxf(amax, red[w]);
+    s = scale_from_absmax(amax);
+  } else {
+    if (live) s = scale_in[row * scale_stride];
+  }
+  if (live && tid == 0 && scales_out != nullptr) scales_out[row] = s;
+
+  const int64_t nchunk_out = PACKED ? KB * 8 : (ncols_out + 7) / 8;
+  for (int64_t c = tid; c < nchunk_out; c += kQuantThreads) {
+    const int64_t k0 = c * 8;
+    const int64_t rem = K - k0;
+    const int valid = live ? static_cast<int>(rem <= 0 ? 0 : (rem < 8 ? rem : 8)) : 0;
+    float v[8];
+    if (valid > 0) {
+      load8(xr + k0, v, vec_in != 0, valid);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+    }
+    int32_t qi[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qi[j] = (j < valid) ? quant1(v[j], s) : 0;
+    u32x2 word = {pack4_i8(qi[0], qi[1], qi[2], qi[3]), pack4_i8(qi[4], qi[5], qi[6], qi[7])};
+    if constexpr (PACKED) {
+      *reinterpret_cast<u32x2*>(q + packed_offset(row, k0, KB)) = word;
+    } else {
+      // Row-major: columns K..ncols_out-1 are written as zeros.
+      int8_t* dst = q + row * ldq + k0;
+      const int nw = static_cast<int>(ncols_out - k0 < 8 ? ncols_out - k0 : 8);
+      if (vec_out && nw == 8) {
+        *reinterpret_cast<u32x2*>(dst) = word;
+      } else {
+        for (int j = 0; j < nw; ++j) dst[j] = static_cast<int8_t>(qi[j]);
+      }
+    }
+  }
+}
+
+// Packs a row-major int8 [rows, K] matrix into 16x64 tiles.  One thread per
+// 16-byte lane slot.  layout 1 maps packed row p to source row p/2 (p even)
+// or rows/2 + p/2 (p odd): the gate/up "interleave" order of
+// _pack_gateup_tensors (llama/lightweight_runner.py:81-92) applied to a
+// split-packed [gate; up] source.
+__global__ __launch_bounds__(256) void pack_rows_kernel(const int8_t* __restrict__ src,
+                                                         int64_t rows, int64_t K, int64_t ld,
+                                                         int layout, int vec, int64_t KB,
+                                                         int64_t nslots,
+                                                         int8_t* __restrict__ dst) {
+  const int64_t slot = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (slot >= nslots) return;
+  const int64_t tile = slot >> 6;
+  const int lane = static_cast<int>(slot & 63);
+  const int64_t rb = tile / KB;
+  const int64_t kb = tile - rb * KB;
+  const int64_t prow = rb * 16 + (lane & 15);
+  const int64_t k0 = kb * 64 + (lane >> 4) * 16;
+  u32x4 out = {0u, 0u, 0u, 0u};
+  if (prow < rows && k0 < K) {
+    int64_t srow = prow;
+    if (layout == 1) srow = (prow & 1) ? (rows / 2 + (prow >> 1)) : (prow >> 1);
+    const int8_t* p = src + srow * ld + k0;
+    const int64_t valid = K - k0 < 16 ? K - k0 : 16;
+    if (vec && valid == 16) {
+      out = *reinterpret_cast<const u32x4*>(p);
+    } else {
+      uint8_t b[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) b[j] = (j < valid) ? static_cast<uint8_t>(p[j]) : 0u;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        out[j] = static_cast<uint32_t>(b[4 * j]) | (static_cast<uint32_t>(b[4 * j + 1]) << 8) |
+                 (static_cast<uint32_t>(b[4 * j + 2]) << 16) |
+                 (static_cast<uint32_t>(b[4 * j + 3]) << 24);
+      }
+    }
+  }
+  reinterpret_cast<u32x4*>(dst)[slot] = out;
+}
+
+// Row-major int8 copy [rows, K] -> [rows, ldd] with zero columns K..ldd-1.
+// One thread per 16-byte destination chunk.
+__global__ __launch_bounds__(256) void pad_rows_kernel(const int8_t* __restrict__ src,
+                                                        int64_t rows, int64_t K, int64_t ld,
+                                                        int8_t* __restrict__ dst, int64_t ldd) {
+  const int64_t chunks_per_row = ldd / 16;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (idx >= rows * chunks_per_row) return;
+  const int64_t r = idx / chunks_per_row;
+  const int64_t k0 = (idx - r * chunks_per_row) * 16;
+  uint8_t b[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) b[j] = (k0 + j < K) ? static_cast<uint8_t>(src[r * ld + k0 + j]) : 0u;
+  u32x4 out;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    out[j] = static_cast<uint32_t>(b[4 * j]) | (static_cast<uint32_t>(b[4 * j + 1]) << 8) |
+             (static_cast<uint32_t>(b[4 * j + 2]) << 16) | (static_cast<uint32_t>(b[4 * j + 3]) << 24);
+  }
+  *reinterpret_cast<u32x4*>(dst + r * ldd + k0) = out;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
+
+template <typename TX>
+hipError_t quant_dispatch(const TX* x, int64_t ldx, int64_t rows, int64_t K,
+                          const float* scale_in, int64_t scale_stride, int8_t* q, int64_t ldq,
+                          int64_t ncols_out, bool packed, float* scales_out, hipStream_t st) {
+  const int vec_in = aligned16(x) && (ldx % 8 == 0) && (K % 8 == 0);
+  const int vec_out = aligned8(q) && (ldq % 8 == 0);
+  const int64_t KB = ceil_div(K, kTileK);
+  const int64_t grid = packed ? ceil_div(rows, kTileRows) * kTileRows : rows;
+  if (grid == 0) return hipSuccess;
+  const bool dyn = scale_in == nullptr;
+  dim3 g(static_cast<unsigned>(grid)), b(kQuantThreads);
+  if (packed) {
+    if (dyn)
+      hipLaunchKernelGGL((quant_rows_kernel<TX, true, true>), g, b, 0, st, x, ldx, rows, K,
+                         vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+    else
+      hipLaunchKernelGGL((quant_rows_kernel<TX, true, false>), g, b, 0, st, x, ldx, rows, K,
+                         vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+  } else {
+    if (dyn)
+      hipLaunchKernelGGL((quant_rows_kernel<TX, false, true>), g, b, 0, st, x, ldx, rows, K,
+                         vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+    else
+      hipLaunchKernelGGL((quant_rows_kernel<TX, false, false>), g, b, 0, st, x, ldx, rows, K,
+                         vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_quant_rows(const void* x, int x_dtype, int64_t ldx, int64_t rows, int64_t K,
+                             const float* scale_in, int64_t scale_stride, int8_t* q,
+                             int64_t ldq, int64_t ncols_out, bool packed, float* scales_out,
+                             hipStream_t st) {
+  switch (x_dtype) {
+    case kF32:
+      return quant_dispatch(static_cast<const float*>(x), ldx, rows, K, scale_in, scale_stride,
+                            q, ldq, ncols_out, packed, scales_out, st);
+    case kF16:
+      return quant_dispatch(static_cast<const __half*>(x), ldx, rows, K, scale_in, scale_stride,
+                            q, ldq, ncols_out, packed, scales_out, st);
+    case kBF16:
+      return quant_dispatch(static_cast<const __hip_bfloat16*>(x), ldx, rows, K, scale_in,
+                            scale_stride, q, ldq, ncols_out, packed, scales_out, st);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+hipError_t launch_pack_rows(const int8_t* src, int64_t rows, int64_t K, int64_t ld, int layout,
+                            int8_t* dst, hipStream_t st) {
+  const int64_t KB = ceil_div(K, kTileK);
+  const int64_t nslots = ceil_div(rows, kTileRows) * KB * kTileVec;
+  if (nslots == 0) return hipSuccess;
+  const int vec = aligned16(src) && (ld % 16 == 0);
+  const int64_t blocks = ceil_div(nslots, 256);
+  hipLaunchKernelGGL(pack_rows_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0, st,
+                     src, rows, K, ld, layout, vec, KB, nslots, dst);
+  return hipGetLastError();
+}
+
+hipError_t launch_pad_rows(const int8_t* src, int64_t rows, int64_t K, int64_t ld, int8_t* dst,
+                           int64_t ldd, hipStream_t st) {
+  const int64_t total = rows * (ldd / 16);
+  if (total == 0) return hipSuccess;
+  hipLaunchKernelGGL(pad_rows_kernel, dim3(static_cast<unsigned>(ceil_div(total, 256))), dim3(256),
+                     0, st, src, rows, K, ld, dst, ldd);
+  return hipGetLastError();
+}
+
+}  // namespace w8a8

@@ -1,0 +1,143 @@
+// Shared device helpers for the W8A8 linear kernels (gfx950 / CDNA4).
+//
+// Numerical contract (nanopointllm/compression/w8a8.py:14-62,118-139):
+//   * int8 values in [-127, 127], ties-to-even rounding (v_rndne_f32);
+//   * scale = max(f32(f16_rne(max(absmax, 2^-14) / 127)), 2^-14) with an
+//     IEEE-correct binary32 division (hipcc's default division lowering);
+//   * q = clamp(rne(f32(x) / s), -127, 127) with a correct binary32 division;
+//   * signed int32 accumulation;
+//   * dequant: f32(acc) * s_x, then * s_w, then + bias: three separate binary32
+//     roundings, never contracted into an FMA (explicit __fmul_rn/__fadd_rn).
+//
+// Packed operand layout ("16x64 tiles").  An int8 matrix R[rows][K] is stored
+// as tiles of 16 rows x 64 K (1 KiB each).  Tile (rb, kb) sits at byte offset
+// (rb * KB + kb) * 1024 with KB = ceil(K / 64).  Inside a tile, bytes
+// [16*l, 16*l+16) belong to lane l = r + 16*g and hold R[16*rb + r][64*kb + 16*g
+// .. +15].  That is the register image of one operand of
+// v_mfma_i32_16x16x64_i8, so a wave fetches a whole fragment with one
+// coalesced 1 KiB global_load_dwordx4 (or one global_load_lds_dwordx4 into
+// LDS) and reads it back from LDS conflict-free with ds_read_b128.  Rows past
+// `rows` and columns past K are zero, so padded work contributes nothing.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <hip/hip_bf16.h>
+#include <stdint.h>
+
+namespace w8a8 {
+
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kScaleMin = 6.103515625e-05f;  // 2^-14, smallest normal binary16
+constexpr int kTileRows = 16;
+constexpr int kTileK = 64;
+constexpr int kTileBytes = kTileRows * kTileK;  // 1024
+constexpr int kTileVec = kTileBytes / 16;       // 64 x 16-byte lane slots
+
+// Element-type tags shared with the C ABI (include/w8a8_gfx950.h).
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2, kI32 = 3, kI8 = 4 };
+
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------- conversions
+__device__ inline float to_f32(float v) { return v; }
+__device__ inline float to_f32(__half v) { return __half2float(v); }
+__device__ inline float to_f32(__hip_bfloat16 v) {
+  return __uint_as_float(static_cast<uint32_t>(__builtin_bit_cast(uint16_t, v)) << 16);
+}
+
+template <typename T> __device__ inline T from_f32(float v);
+template <> __device__ inline float from_f32<float>(float v) { return v; }
+template <> __device__ inline __half from_f32<__half>(float v) { return __float2half_rn(v); }
+template <> __device__ inline __hip_bfloat16 from_f32<__hip_bfloat16>(float v) {
+  // binary32 -> bfloat16, round to nearest even; NaN stays a quiet NaN.
+  uint32_t u = __float_as_uint(v);
+  uint16_t b;
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    b = static_cast<uint16_t>((u >> 16) | 0x0040u);
+  } else {
+    b = static_cast<uint16_t>((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+  }
+  return __builtin_bit_cast(__hip_bfloat16, b);
+}
+
+// Loads 8 consecutive elements as binary32.  `vec` selects one (fp16/bf16)
+// or two (f32) 16-byte loads; callers guarantee 16-byte alignment then.
+template <typename T>
+__device__ inline void load8(const T* __restrict__ p, float (&v)[8], bool vec, int valid) {
+  if (vec && valid >= 8) {
+    if constexpr (sizeof(T) == 2) {
+      u32x4 raw = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        uint16_t lo = static_cast<uint16_t>(raw[j] & 0xffffu);
+        uint16_t hi = static_cast<uint16_t>(raw[j] >> 16);
+        v[2 * j] = to_f32(__builtin_bit_cast(T, lo));
+        v[2 * j + 1] = to_f32(__builtin_bit_cast(T, hi));
+      }
+    } else {
+      u32x4 r0 = reinterpret_cast<const u32x4*>(p)[0];
+      u32x4 r1 = reinterpret_cast<const u32x4*>(p)[1];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[j] = __uint_as_float(r0[j]);
+        v[4 + j] = __uint_as_float(r1[j]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (j < valid) ? to_f32(p[j]) : 0.0f;
+  }
+}
+
+// --------------------------------------------------------------- quant math
+// scale_from_absmax (nanopointllm/compression/w8a8.py:46-50).
+__device__ inline float scale_from_absmax(float absmax) {
+  float raw = fmaxf(absmax, kScaleMin) / 127.0f;  // IEEE binary32 division
+  float s = __half2float(__float2half_rn(raw));
+  return fmaxf(s, kScaleMin);
+}
+
+// quantize_symmetric (nanopointllm/compression/w8a8.py:33-43) for one value.
+__device__ inline int32_t quant1(float x, float s) {
+  float q = __builtin_rintf(x / s);  // IEEE binary32 division, ties-to-even
+  q = fminf(fmaxf(q, -127.0f), 127.0f);
+  return static_cast<int32_t>(q);
+}
+
+__device__ inline uint32_t pack4_i8(int32_t a, int32_t b, int32_t c, int32_t d) {
+  return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
+         ((static_cast<uint32_t>(c) & 0xffu) << 16) | ((static_cast<uint32_t>(d) & 0xffu) << 24);
+}
+
+// Dequant epilogue (w8a8.py:134-137): three separate binary32 roundings.
+__device__ inline float dequant1(int32_t acc, float sx, float sw, const float* __restrict__ bias,
+                                 int64_t n) {
+  float v = static_cast<float>(acc);  // v_cvt_f32_i32: round to nearest even
+  v = __fmul_rn(v, sx);
+  v = __fmul_rn(v, sw);
+  if (bias != nullptr) v = __fadd_rn(v, bias[n]);
+  return v;
+}
+
+// SiLU(g) * u on binary16 operands (llama/lightweight_runner.py:358):
+// SiLU in binary32, rounded to the activation type, then the product
+// (exact in binary32) rounded once.
+template <typename T>
+__device__ inline float silu_mul(float g, float u) {
+  float s = g / (1.0f + expf(-g));
+  s = to_f32(from_f32<T>(s));
+  return __fmul_rn(s, u);
+}
+
+// Packed-tile byte offset of element (r, k) of a [rows, K] operand.
+__host__ __device__ inline int64_t packed_offset(int64_t r, int64_t k, int64_t KB) {
+  int64_t tile = (r >> 4) * KB + (k >> 6);
+  int64_t lane = (r & 15) + 16 * ((k & 63) >> 4);
+  return tile * kTileBytes + lane * 16 + (k & 15);
+}
+
+}  // namespace w8a8

@@ -1,0 +1,58 @@
+// Internal launch interface shared by the kernel translation units and the
+// C ABI layer (capi.hip).  Nothing here is exported from the shared library.
+#pragma once
+
+#include "w8a8_common.h"
+
+namespace w8a8 {
+
+// Epilogue selector shared by the GEMV and GEMM kernels.
+enum Epilogue : int {
+  kEpiI32 = 0,      // raw int32 accumulators
+  kEpiDequant = 1,  // f32(acc) * s_x * s_w (+ bias) -> output type
+  kEpiSilu = 2,     // packed interleaved gate/up: SiLU(g) * u -> output type
+  kEpiSiluQ8 = 3,   // as kEpiSilu, then int8 with a static scale
+};
+
+struct LinearOperands {
+  // Activations.  GEMV: row-major int8 [M, lda], lda % 16 == 0, 16-byte
+  // aligned, readable and zero past K up to KB*64.  GEMM: packed tiles.
+  const int8_t* a;
+  int64_t lda;
+  const float* sx;  // per-row activation scales [M]
+  const int8_t* w;  // packed weights [NB][KB] tiles
+  const float* sw;  // per-output weight scales [N]
+  const float* bias;  // [N] or null
+  void* y;
+  int64_t ldy;
+  int y_dtype;      // output element type (kF32/kF16/kBF16/kI32/kI8)
+  int h_dtype;      // SiLU intermediate rounding type for kEpiSiluQ8 (kF16/kBF16)
+  float out_scale;  // static requant scale for kEpiSiluQ8
+  int64_t M, N, K;
+  int epi;
+};
+
+// Quantizes each row of x (scale_in == nullptr: dynamic per-row scale).
+// Row-major output writes columns [0, ncols_out) (zeros past K); packed
+// output writes whole tiles for ceil(rows/16)*16 rows.
+hipError_t launch_quant_rows(const void* x, int x_dtype, int64_t ldx, int64_t rows, int64_t K,
+                             const float* scale_in, int64_t scale_stride, int8_t* q,
+                             int64_t ldq, int64_t ncols_out, bool packed, float* scales_out,
+                             hipStream_t st);
+
+hipError_t launch_pack_rows(const int8_t* src, int64_t rows, int64_t K, int64_t ld, int layout,
+                            int8_t* dst, hipStream_t st);
+
+// Copies a row-major int8 [rows, K] matrix into [rows, ldd] with zeros in
+// columns K..ldd-1 (ldd % 16 == 0).
+hipError_t launch_pad_rows(const int8_t* src, int64_t rows, int64_t K, int64_t ld, int8_t* dst,
+                           int64_t ldd, hipStream_t st);
+
+// M <= 64 (the GEMV regime).
+hipError_t launch_gemv(const LinearOperands& op, hipStream_t st);
+// Any M; activations packed.
+hipError_t launch_gemm(const LinearOperands& op, hipStream_t st);
+
+constexpr int64_t kGemvMaxRows = 64;
+
+}  // namespace w8a8

@@ -1,0 +1,215 @@
+"""W8A8 linear modules for the lightweight LLaMA runner's projection call sites.
+
+Each module owns its quantized weight, packed once into 16x64 MFMA tiles,
+and replaces one of the reference's dense call sites:
+
+* :class:`W8A8Linear`            - ``F.linear(x, W, b)`` (O proj,
+  ``_project_output_decode_staged``, llama/paged_attention.py:118-124; down
+  proj, ``_decode_linear_rows``, llama/lightweight_runner.py:38-54).
+* :class:`W8A8PackedQKV`         - the packed QKV projection
+  (``PagedLlamaAttention.from_hf`` packing, llama/paged_attention.py:1242-1262;
+  ``_project_qkv_decode_packed``, :97-115).
+* :class:`W8A8GateUpSiluMul`     - packed gate/up plus ``act_fn(gate) * up``
+  (``LightweightMLP`` packed branch, llama/lightweight_runner.py:320-358) in one
+  kernel, with the interleaved weight layout of ``_pack_gateup_tensors``
+  (:81-92).
+* :class:`W8A8MLP`               - gate/up + SiLU*mul + down
+  (``LightweightMLP.forward``, :320-383), optionally as an int8 chain where the
+  gate/up epilogue requantizes ``h`` with a static (calibrated) scale and the
+  down projection consumes int8 directly.
+
+Weights follow ``per_output_weight_qdq`` (nanopointllm/compression/w8a8.py:53-62);
+activations are quantized per token (w8a8.py:106-115); results follow the
+integer contract of ``integer_linear_per_output_reference`` (w8a8.py:118-139).
+Per-row quantization commutes with row packing, so the packed QKV / gate-up
+scales are the concatenation / interleave of the per-module scales.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from . import w8a8 as _w
+
+
+@dataclass
+class PackedW8A8Weight:
+    """Per-output int8 weight in packed tiles, with f32 scales and bias."""
+
+    packed: torch.Tensor          # int8, w8a8_packed_bytes(N, K) bytes
+    scale: torch.Tensor           # f32 [N] (binary16-representable values)
+    bias: torch.Tensor | None     # f32 [N] or None
+    out_features: int
+    in_features: int
+    layout: int = _lib.ROWS_AS_IS
+
+    @classmethod
+    def from_int8(cls, qweight: torch.Tensor, scale: torch.Tensor,
+                  bias: torch.Tensor | None = None, *,
+                  layout: int = _lib.ROWS_AS_IS) -> "PackedW8A8Weight":
+        """Pack an already-quantized row-major weight.
+
+        With ``layout == ROWS_INTERLEAVE_HALVES`` the rows of ``qweight`` (and
+        ``scale``/``bias``) are ``[gate; up]`` and are packed as g0,u0,g1,u1...
+        """
+        device = _lib.require_cuda(qweight, scale, bias)
+        n, k = qweight.shape
+        packed = _w.pack_rows(qweight.contiguous(), layout)
+        s = scale.detach().to(device=device, dtype=torch.float32).reshape(-1)
+        b = None if bias is None else bias.detach().to(device=device, dtype=torch.float32).reshape(-1)
+        if s.numel() != n or (b is not None and b.numel() != n):
+            raise ValueError("scale/bias must have one value per output")
+        if layout == _lib.ROWS_INTERLEAVE_HALVES:
+            s = _interleave_halves(s)
+            b = None if b is None else _interleave_halves(b)
+        return cls(packed, s.contiguous(), None if b is None else b.contiguous(), n, k, layout)
+
+    @classmethod
+    def from_float(cls, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
+                   layout: int = _lib.ROWS_AS_IS) -> "PackedW8A8Weight":
+        """Quantize per output row (``per_output_weight_qdq``) and pack."""
+        q, s = _w.quant_rows(weight.detach())
+        return cls.from_int8(q, s, bias, layout=layout)
+
+
+def _interleave_halves(v: torch.Tensor) -> torch.Tensor:
+    half = v.numel() // 2
+    return torch.stack([v[:half], v[half:]], dim=1).reshape(-1)
+
+
+def _linear_parts(module: nn.Module) -> tuple[torch.Tensor, torch.Tensor | None]:
+    return module.weight, getattr(module, "bias", None)
+
+
+class W8A8Linear(nn.Module):
+    """``F.linear(x, W, b)`` with dynamic per-token A8 and per-output W8."""
+
+    def __init__(self, weight: PackedW8A8Weight) -> None:
+        super().__init__()
+        self.weight_q = weight
+        self.in_features = weight.in_features
+        self.out_features = weight.out_features
+
+    @classmethod
+    def from_linear(cls, linear: nn.Module) -> "W8A8Linear":
+        w, b = _linear_parts(linear)
+        return cls(PackedW8A8Weight.from_float(w, b))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        p = self.weight_q
+        return _w.linear_dynamic(x, p.packed, p.scale, p.bias, p.out_features)
+
+    def forward_i8(self, xq: torch.Tensor, x_scale: torch.Tensor,
+                   out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+        """Same product for int8 activations with per-row scales."""
+        p = self.weight_q
+        return _w.linear_i8in(xq, x_scale, p.packed, p.scale, p.bias, p.out_features,
+                              out_dtype=out_dtype)
+
+    def accumulators(self, x: torch.Tensor) -> torch.Tensor:
+        """Raw int32 accumulators of ``forward`` (for exactness checks)."""
+        p = self.weight_q
+        return _w.linear_dynamic(x, p.packed, p.scale, None, p.out_features,
+                                 epilogue=_lib.EPI_I32)
+
+
+class W8A8PackedQKV(nn.Module):
+    """Packed ``[Wq; Wk; Wv]`` projection (paged_attention.py:1242-1262)."""
+
+    def __init__(self, q_proj: nn.Module, k_proj: nn.Module, v_proj: nn.Module, *,
+                 num_heads: int, num_kv_heads: int, head_dim: int) -> None:
+        super().__init__()
+        parts = [_linear_parts(m) for m in (q_proj, k_proj, v_proj)]
+        weight = torch.cat([w for w, _ in parts], dim=0)
+        if all(b is None for _, b in parts):
+            bias = None
+        else:
+            bias = torch.cat([b if b is not None else w.new_zeros(w.shape[0])
+                              for w, b in parts], dim=0)
+        self.linear = W8A8Linear(PackedW8A8Weight.from_float(weight, bias))
+        self.num_heads = num_heads
+        self.num_kv_heads = num_kv_heads
+        self.head_dim = head_dim
+
+    def forward(self, hidden_states: torch.Tensor) -> torch.Tensor:
+        return self.linear(hidden_states)
+
+    def project(self, hidden_states: torch.Tensor
+                ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """``_project_qkv_decode_packed`` (paged_attention.py:97-115) semantics."""
+        staged = hidden_states[0] if hidden_states.dim() == 3 else hidden_states
+        qkv = self.linear(staged)
+        q_size = self.num_heads * self.head_dim
+        kv_size = self.num_kv_heads * self.head_dim
+        q, k, v = torch.split(qkv, (q_size, kv_size, kv_size), dim=-1)
+        return (q.view(-1, self.num_heads, self.head_dim),
+                k.view(-1, self.num_kv_heads, self.head_dim),
+                v.view(-1, self.num_kv_heads, self.head_dim))
+
+
+class W8A8GateUpSiluMul(nn.Module):
+    """Packed gate/up projection fused with ``act_fn(gate) * up``.
+
+    Weights are packed in the reference's interleave layout (g0,u0,g1,u1...),
+    so each 16-output tile carries 8 (gate, up) pairs and the epilogue emits
+    ``SiLU(g) * u`` with the reference's binary16 roundings
+    (lightweight_runner.py:344-358).
+    """
+
+    def __init__(self, gate_proj: nn.Module, up_proj: nn.Module) -> None:
+        super().__init__()
+        (wg, bg), (wu, bu) = _linear_parts(gate_proj), _linear_parts(up_proj)
+        weight = torch.cat([wg, wu], dim=0)
+        if bg is None and bu is None:
+            bias = None
+        else:
+            bias = torch.cat([bg if bg is not None else wg.new_zeros(wg.shape[0]),
+                              bu if bu is not None else wu.new_zeros(wu.shape[0])])
+        self.weight_q = PackedW8A8Weight.from_float(
+            weight, bias, layout=_lib.ROWS_INTERLEAVE_HALVES)
+        self.intermediate = wg.shape[0]
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        p = self.weight_q
+        return _w.linear_dynamic(x, p.packed, p.scale, p.bias, p.out_features,
+                                 epilogue=_lib.EPI_SILU_MUL)
+
+    def forward_q8(self, x: torch.Tensor, h_scale: float) -> torch.Tensor:
+        """``quantize_symmetric(SiLU(g) * u, h_scale)`` as int8 (static requant)."""
+        p = self.weight_q
+        return _w.linear_dynamic(x, p.packed, p.scale, p.bias, p.out_features,
+                                 epilogue=_lib.EPI_SILU_MUL_Q8, y_scale=h_scale)
+
+    def accumulators(self, x: torch.Tensor) -> torch.Tensor:
+        """int32 accumulators in packed (interleaved) column order."""
+        p = self.weight_q
+        return _w.linear_dynamic(x, p.packed, p.scale, None, p.out_features,
+                                 epilogue=_lib.EPI_I32)
+
+
+class W8A8MLP(nn.Module):
+    """LLaMA MLP ``down(SiLU(gate(x)) * up(x))`` on the W8A8 kernels.
+
+    With ``h_scale`` (a calibrated static scale for ``h``, e.g. from
+    ``static_activation_scale``) the gate/up kernel writes int8 ``h`` and the
+    down projection consumes it directly (int8-in chain); otherwise ``h`` is
+    kept in the activation dtype and quantized per token by the down
+    projection.
+    """
+
+    def __init__(self, gate_proj: nn.Module, up_proj: nn.Module, down_proj: nn.Module, *,
+                 h_scale: float | None = None) -> None:
+        super().__init__()
+        self.gate_up = W8A8GateUpSiluMul(gate_proj, up_proj)
+        self.down = W8A8Linear.from_linear(down_proj)
+        self.h_scale = h_scale
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.h_scale is None:
+            return self.down(self.gate_up(x))
+        hq = self.gate_up.forward_q8(x, self.h_scale)
+        s = torch.full((1,), self.h_scale, dtype=torch.float32, device=x.device)
+        return self.down.forward_i8(hq, s, out_dtype=x.dtype)

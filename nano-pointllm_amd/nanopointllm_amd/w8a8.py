@@ -1,0 +1,277 @@
+"""W8A8 numerical contract on the GPU (HIP kernels through libw8a8_gfx950.so).
+
+Mirrors the function API of ``nanopointllm.compression.w8a8``
+(nanopointllm/compression/w8a8.py) for CUDA tensors: same names, same
+argument meaning, same results, same error messages.  Every integer result is
+produced by the HIP kernels; torch is used only for device memory, reshapes
+and the trivial elementwise QDQ reconstruction (``q * s``).
+"""
+from __future__ import annotations
+
+from dataclasses import asdict, dataclass
+from typing import Any
+
+import torch
+
+from . import _lib
+
+_F16_TINY = torch.finfo(torch.float16).tiny  # 2**-14
+
+
+@dataclass(frozen=True)
+class W8A8Contract:
+    """Same fields and values as the reference contract (w8a8.py:14-30)."""
+
+    weight_bits: int = 8
+    activation_bits: int = 8
+    symmetric_min: int = -127
+    symmetric_max: int = 127
+    rounding: str = "round_to_nearest_ties_to_even"
+    scale_storage: str = "float16"
+    accumulator: str = "signed_int32"
+    bias: str = "floating_point_after_dequantization"
+    nonlinear_norm_residual: str = "bf16_or_fp16"
+
+    def as_dict(self) -> dict[str, Any]:
+        return asdict(self)
+
+
+CONTRACT = W8A8Contract()
+
+
+# ---------------------------------------------------------------- low level
+def packed_bytes(rows: int, k: int) -> int:
+    return int(_lib.load().w8a8_packed_bytes(rows, k))
+
+
+def workspace_bytes(m: int, k: int) -> int:
+    return int(_lib.load().w8a8_workspace_bytes(m, k))
+
+
+def _rows_view(x: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """2-D [rows, K] view with unit column stride, plus its leading dimension."""
+    k = x.shape[-1]
+    x2 = x.reshape(-1, k)
+    if x2.shape[0] > 0 and (x2.stride(-1) != 1 or (x2.shape[0] > 1 and x2.stride(0) < k)):
+        x2 = x2.contiguous()
+    ld = x2.stride(0) if x2.shape[0] > 1 else max(k, 1)
+    return x2, ld
+
+
+def quant_rows(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Dynamic per-row int8 quantization of ``x[..., K]``.
+
+    Returns ``(q int8 [..., K], scales f32 [...])``; the scale of each row is
+    ``scale_from_absmax(|row|.amax())`` (w8a8.py:46-50, 106-115).
+    """
+    device = _lib.require_cuda(x)
+    x2, ldx = _rows_view(x)
+    rows, k = x2.shape
+    q = torch.empty((rows, k), dtype=torch.int8, device=device)
+    s = torch.empty((rows,), dtype=torch.float32, device=device)
+    if rows:
+        lib = _lib.load()
+        _lib.check(lib.w8a8_quant_rows(x2.data_ptr(), _lib.dtype_code(x2.dtype), rows, k, ldx,
+                                       q.data_ptr(), max(k, 1), s.data_ptr(),
+                                       _lib.stream_handle(device)), "w8a8_quant_rows")
+    return q.reshape(x.shape), s.reshape(x.shape[:-1])
+
+
+def quant_rows_scaled(x: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """``quantize_symmetric`` with one scale per tensor or per row (no checks)."""
+    device = _lib.require_cuda(x, scale)
+    x2, ldx = _rows_view(x)
+    rows, k = x2.shape
+    s = scale.detach().to(device=device, dtype=torch.float32).contiguous()
+    if s.numel() == 1:
+        stride = 0
+    elif s.numel() == rows:
+        stride = 1
+    else:
+        raise ValueError("scale must be per-tensor or one value per row of the last dimension")
+    q = torch.empty((rows, k), dtype=torch.int8, device=device)
+    if rows:
+        lib = _lib.load()
+        _lib.check(lib.w8a8_quant_rows_scaled(x2.data_ptr(), _lib.dtype_code(x2.dtype), rows, k,
+                                              ldx, s.data_ptr(), stride, q.data_ptr(),
+                                              max(k, 1), _lib.stream_handle(device)),
+                   "w8a8_quant_rows_scaled")
+    return q.reshape(x.shape)
+
+
+def pack_rows(q: torch.Tensor, layout: int = _lib.ROWS_AS_IS) -> torch.Tensor:
+    """Pack int8 ``q[rows, K]`` into 16x64 MFMA tiles (flat int8 tensor)."""
+    device = _lib.require_cuda(q)
+    if q.dtype != torch.int8 or q.dim() != 2:
+        raise ValueError("pack_rows expects a 2-D int8 tensor")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    rows, k = q.shape
+    out = torch.empty((packed_bytes(rows, k),), dtype=torch.int8, device=device)
+    if rows and k:
+        lib = _lib.load()
+        _lib.check(lib.w8a8_pack_rows(q.data_ptr(), rows, k, q.stride(0) if rows > 1 else k,
+                                      layout, out.data_ptr(), _lib.stream_handle(device)),
+                   "w8a8_pack_rows")
+    return out
+
+
+def _workspace(m: int, k: int, device: torch.device) -> torch.Tensor:
+    return torch.empty((max(workspace_bytes(m, k), 16),), dtype=torch.uint8, device=device)
+
+
+def gemm_i32(xq: torch.Tensor, w_packed: torch.Tensor, n: int) -> torch.Tensor:
+    """Exact ``int32(xq) @ int32(wq).T`` for packed ``wq`` ([..., K] -> [..., n])."""
+    device = _lib.require_cuda(xq, w_packed)
+    x2, ldq = _rows_view(xq)
+    m, k = x2.shape
+    acc = torch.empty((m, n), dtype=torch.int32, device=device)
+    if m and n:
+        ws = _workspace(m, k, device)
+        lib = _lib.load()
+        _lib.check(lib.w8a8_gemm_i32(x2.data_ptr(), ldq, w_packed.data_ptr(), acc.data_ptr(), n,
+                                     m, n, k, ws.data_ptr(), ws.numel(),
+                                     _lib.stream_handle(device)), "w8a8_gemm_i32")
+    return acc.reshape(*xq.shape[:-1], n)
+
+
+def _out_cols(epilogue: int, n: int) -> int:
+    return n // 2 if epilogue in (_lib.EPI_SILU_MUL, _lib.EPI_SILU_MUL_Q8) else n
+
+
+def linear_dynamic(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
+                   bias: torch.Tensor | None, n: int, *, epilogue: int = _lib.EPI_DEQUANT,
+                   out_dtype: torch.dtype | None = None, y_scale: float = 0.0,
+                   inter_dtype: torch.dtype | None = None,
+                   x_scale_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-token dynamic A8 x per-output W8 linear with a fused epilogue."""
+    device = _lib.require_cuda(x, w_packed, w_scale, bias)
+    x2, ldx = _rows_view(x)
+    m, k = x2.shape
+    if out_dtype is None:
+        out_dtype = torch.int8 if epilogue == _lib.EPI_SILU_MUL_Q8 else (
+            torch.int32 if epilogue == _lib.EPI_I32 else x.dtype)
+    if inter_dtype is None:
+        inter_dtype = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.float16
+    cols = _out_cols(epilogue, n)
+    y = torch.empty((m, cols), dtype=out_dtype, device=device)
+    if m and n:
+        ws = _workspace(m, k, device)
+        lib = _lib.load()
+        _lib.check(lib.w8a8_linear(
+            x2.data_ptr(), _lib.dtype_code(x2.dtype), ldx, w_packed.data_ptr(),
+            w_scale.data_ptr(), _lib.ptr(bias), epilogue, y.data_ptr(),
+            _lib.dtype_code(out_dtype), cols, float(y_scale), _lib.dtype_code(inter_dtype),
+            m, n, k, _lib.ptr(x_scale_out), ws.data_ptr(), ws.numel(),
+            _lib.stream_handle(device)), "w8a8_linear")
+    return y.reshape(*x.shape[:-1], cols)
+
+
+def linear_i8in(xq: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor,
+                w_scale: torch.Tensor, bias: torch.Tensor | None, n: int, *,
+                epilogue: int = _lib.EPI_DEQUANT, out_dtype: torch.dtype = torch.float16,
+                y_scale: float = 0.0, inter_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """W8A8 linear on already-quantized activations with per-row scales."""
+    device = _lib.require_cuda(xq, x_scale, w_packed, w_scale, bias)
+    x2, ldq = _rows_view(xq)
+    m, k = x2.shape
+    s = x_scale.detach().to(dtype=torch.float32).reshape(-1)
+    if s.numel() == 1 and m != 1:
+        s = s.expand(m)
+    s = s.contiguous()
+    if s.numel() != m:
+        raise ValueError("x_scale must be per-tensor or one value per row")
+    cols = _out_cols(epilogue, n)
+    y = torch.empty((m, cols), dtype=out_dtype, device=device)
+    if m and n:
+        ws = _workspace(m, k, device)
+        lib = _lib.load()
+        _lib.check(lib.w8a8_linear_i8in(
+            x2.data_ptr(), ldq, s.data_ptr(), w_packed.data_ptr(), w_scale.data_ptr(),
+            _lib.ptr(bias), epilogue, y.data_ptr(), _lib.dtype_code(out_dtype), cols,
+            float(y_scale), _lib.dtype_code(inter_dtype), m, n, k, ws.data_ptr(), ws.numel(),
+            _lib.stream_handle(device)), "w8a8_linear_i8in")
+    return y.reshape(*xq.shape[:-1], cols)
+
+
+# ------------------------------------------- reference-named contract functions
+def quantize_symmetric(values: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """``quantize_symmetric`` (w8a8.py:33-43) on the GPU.
+
+    ``scale`` is one per-tensor value or one value per row of the last
+    dimension (shape ``[..., 1]`` or ``[rows]``), the forms the contract uses.
+    Non-positive scales raise ``ValueError`` (a host sync, as in the reference).
+    """
+    scale = torch.as_tensor(scale, device=values.device)
+    if torch.any(scale <= 0):
+        raise ValueError("quantization scale must be positive")
+    return quant_rows_scaled(values, scale)
+
+
+def scale_from_absmax(absmax: torch.Tensor) -> torch.Tensor:
+    """``scale_from_absmax`` (w8a8.py:46-50): binary16-stored scale as f32."""
+    _lib.require_cuda(absmax)
+    raw = absmax.float().clamp_min(_F16_TINY) / CONTRACT.symmetric_max
+    return raw.to(torch.float16).float().clamp_min(_F16_TINY)
+
+
+def static_activation_scale(absmax, device: torch.device | str = "cuda") -> torch.Tensor:
+    """``static_activation_scale`` (w8a8.py:94-98)."""
+    value = torch.as_tensor(absmax, dtype=torch.float32, device=device)
+    if value.numel() != 1:
+        raise ValueError("static activation scale expects one tensor-wide absmax")
+    return scale_from_absmax(value.reshape(()))
+
+
+def static_activation_qdq(values: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """``static_activation_qdq`` (w8a8.py:101-103)."""
+    q = quantize_symmetric(values, scale)
+    return (q.float() * scale.float().to(values.device)).to(values.dtype)
+
+
+def dynamic_per_token_activation_qdq(values: torch.Tensor, *, axis: int = -1
+                                     ) -> tuple[torch.Tensor, torch.Tensor]:
+    """``dynamic_per_token_activation_qdq`` (w8a8.py:106-115)."""
+    if values.dim() == 0:
+        raise ValueError("dynamic per-token quantization expects a tensor")
+    moved = values.movedim(axis, -1)
+    q, s = quant_rows(moved)
+    scales = s.unsqueeze(-1)
+    qdq = (q.float() * scales).to(values.dtype)
+    return qdq.movedim(-1, axis), scales.movedim(-1, axis)
+
+
+def per_output_weight_qdq(weight: torch.Tensor
+                          ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``per_output_weight_qdq`` (w8a8.py:53-62): (dequant, int8, f32 scales [N])."""
+    if weight.dim() < 2:
+        raise ValueError("weight must have at least two dimensions")
+    rows = weight.detach().reshape(weight.shape[0], -1)
+    q, scales = quant_rows(rows)
+    deq = (q.float() * scales[:, None]).reshape_as(weight)
+    return deq.to(weight.dtype), q.reshape_as(weight), scales
+
+
+def integer_linear_per_output(values: torch.Tensor, weight: torch.Tensor, *,
+                              activation_scale: torch.Tensor,
+                              bias: torch.Tensor | None = None
+                              ) -> tuple[torch.Tensor, torch.Tensor]:
+    """GPU execution of ``integer_linear_per_output_reference`` (w8a8.py:118-139).
+
+    Returns ``(out f32 [..., N], acc int32 [..., N])`` with the reference's
+    arithmetic: int8 x int8 -> int32, then ``f32(acc) * s_x * s_w + bias``.
+    """
+    if values.shape[-1] != weight.shape[1] or weight.dim() != 2:
+        raise ValueError("linear input/weight shapes do not match")
+    device = _lib.require_cuda(values, weight)
+    n = weight.shape[0]
+    qa = quantize_symmetric(values, activation_scale)
+    _, qw, sw = per_output_weight_qdq(weight)
+    w_packed = pack_rows(qw)
+    acc = gemm_i32(qa, w_packed, n)
+    rows = qa.reshape(-1, qa.shape[-1]).shape[0]
+    s = torch.as_tensor(activation_scale, device=device).float().reshape(-1)
+    s = (s.expand(rows) if s.numel() == 1 else s).contiguous()
+    b = None if bias is None else bias.detach().float().to(device).contiguous()
+    out = linear_i8in(qa, s, w_packed, sw, b, n, out_dtype=torch.float32)
+    return out, acc

@@ -1,0 +1,91 @@
+"""C ABI surface of libw8a8_gfx950.so, checked without a GPU: the library
+loads, exports every entry point include/w8a8_gfx950.h declares, reports
+sizes, and rejects bad arguments with status codes before any launch."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from nanopointllm_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "w8a8_gfx950.h"
+
+
+def declared_symbols() -> list[str]:
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w[\w\s\*]*?\b(w8a8_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declarations_are_exported():
+    lib = _lib.load()
+    names = declared_symbols()
+    assert len(names) == 11
+    for name in names:
+        assert hasattr(lib, name), name
+    assert sorted(_lib.EXPORTED_SYMBOLS) == names
+
+
+def test_sizes_and_version():
+    lib = _lib.load()
+    assert lib.w8a8_abi_version() == _lib.ABI_VERSION
+    assert lib.w8a8_packed_bytes(12288, 4096) == 12288 * 4096
+    assert lib.w8a8_packed_bytes(50, 100) == 64 * 128
+    assert lib.w8a8_packed_bytes(-1, 4) == -1
+    assert lib.w8a8_workspace_bytes(8, 4096) == 256 + 16 * 4096
+    assert lib.w8a8_workspace_bytes(560, 11008) == 2304 + 560 * 11008
+    assert lib.w8a8_status_string(_lib.ERR_WORKSPACE) == b"workspace missing or too small"
+
+
+def test_invalid_arguments_return_status_without_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    # negative shape
+    assert lib.w8a8_quant_rows(fake, _lib.F16, -1, 4, 4, fake, 4, fake, None) == _lib.ERR_SHAPE
+    # unsupported input dtype
+    assert lib.w8a8_quant_rows(fake, _lib.I8, 1, 4, 4, fake, 4, fake, None) == _lib.ERR_DTYPE
+    # null pointers
+    assert lib.w8a8_quant_rows(None, _lib.F16, 1, 4, 4, fake, 4, fake, None) == _lib.ERR_NULL
+    # leading dimension too small
+    assert lib.w8a8_quant_rows(fake, _lib.F16, 2, 8, 4, fake, 8, fake, None) == _lib.ERR_SHAPE
+    # K beyond the int32 accumulator bound (K * 127**2 >= 2**31)
+    assert lib.w8a8_linear(fake, _lib.F16, 200000, fake, fake, None, _lib.EPI_DEQUANT, fake,
+                           _lib.F16, 8, 0.0, _lib.F16, 1, 8, 133145, None, fake, 1 << 30,
+                           None) == _lib.ERR_SHAPE
+    # SiLU epilogue needs an even N and a 16-bit output
+    assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_SILU_MUL, fake,
+                           _lib.F32, 8, 0.0, _lib.F16, 1, 16, 64, None, fake, 1 << 20,
+                           None) == _lib.ERR_DTYPE
+    # int8 requant epilogue needs a positive static scale
+    assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_SILU_MUL_Q8, fake,
+                           _lib.I8, 8, 0.0, _lib.F16, 1, 16, 64, None, fake, 1 << 20,
+                           None) == _lib.ERR_SHAPE
+    # workspace too small
+    assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_DEQUANT, fake,
+                           _lib.F16, 16, 0.0, _lib.F16, 1, 16, 64, None, fake, 10,
+                           None) == _lib.ERR_WORKSPACE
+    # misaligned packed weights
+    assert lib.w8a8_gemm_i32(fake, 64, ctypes.c_void_p(0x1001), fake, 16, 1, 16, 64, fake,
+                             1 << 20, None) == _lib.ERR_ALIGN
+    # interleaved packing needs an even row count
+    assert lib.w8a8_pack_rows(fake, 3, 64, 64, _lib.ROWS_INTERLEAVE_HALVES, fake,
+                              None) == _lib.ERR_SHAPE
+    # empty problems are valid no-ops
+    assert lib.w8a8_linear(None, _lib.F16, 64, None, None, None, _lib.EPI_DEQUANT, None,
+                           _lib.F16, 16, 0.0, _lib.F16, 0, 16, 64, None, None, 0, None) == _lib.OK
+
+
+def test_status_errors_map_to_python_exceptions():
+    with pytest.raises(ValueError, match="workspace"):
+        _lib.check(_lib.ERR_WORKSPACE, "w8a8_linear")
+
+
+def test_cpu_tensors_are_rejected_not_computed():
+    import torch
+
+    from nanopointllm_amd import w8a8
+
+    with pytest.raises(RuntimeError, match="only on the GPU"):
+        w8a8.quant_rows(torch.ones(2, 8, dtype=torch.float16))

@@ -1,0 +1,455 @@
+"""GPU parity: libw8a8_gfx950.so against the CPU oracle on identical inputs.
+
+Bars: int8 / int32 results bit-exact; binary16 / bfloat16 / binary32 outputs
+bit-equal to the oracle's binary32 result rounded once; SiLU*mul outputs
+within one binary16 ulp (the GPU and CPU ``exp`` may differ by an ulp), with
+the downstream int32 of the int8 chain bit-exact against the oracle fed the
+GPU's own int8 ``h``.
+"""
+from __future__ import annotations
+
+import json
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import w8a8_oracle as O
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+
+
+def note(msg: str) -> None:
+    """Name the case on stderr before its GPU work (survives a crashed run)."""
+    sys.__stderr__.write(f"[gpu-case] {msg}\n")
+    sys.__stderr__.flush()
+
+
+def f16_to_np(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def bf16_bits(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def rand_i8(shape, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
+
+
+def weight_q(n, k, seed):
+    from nanopointllm_amd import workloads as W
+
+    w = W.linear_weight(n, k, seed=seed)
+    _, q, s = O.per_output_weight_qdq(w.float().numpy())
+    return w, q, s
+
+
+# ------------------------------------------------------------ quantization
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape", [(1, 4096), (16, 4096), (7, 100), (3, 11008), (33, 4096), (5, 3)])
+def test_quant_rows_bit_exact(cuda, dtype, shape):
+    from nanopointllm_amd import w8a8
+
+    g = torch.Generator().manual_seed(hash(shape) % 1000)
+    x = torch.randn(*shape, generator=g) * 3
+    x[0, : min(4, shape[1])] *= 50
+    if shape[0] > 2:
+        x[1] = 0.0                      # all-zero row -> scale 2**-14
+        x[2] *= 1e-6                    # tiny row -> scale clamps to 2**-14
+    x = x.to(dtype)
+    note(f"quant_rows {dtype} {shape}")
+    q, s = w8a8.quant_rows(x.to(cuda))
+    xn = x.float().numpy()
+    eq, es = O.dynamic_per_token_quant(xn)
+    np.testing.assert_array_equal(s.cpu().numpy(), es[:, 0])
+    np.testing.assert_array_equal(q.cpu().numpy(), eq)
+
+
+def test_quant_ties_round_to_even(cuda):
+    from nanopointllm_amd import w8a8
+
+    s = np.float32(np.float16(0.25))
+    vals = (np.arange(-130, 130) + 0.5).astype(np.float32) * s   # exact half-integers
+    x = torch.from_numpy(vals.astype(np.float16)).reshape(1, -1)
+    note("quant_rows_scaled ties")
+    q = w8a8.quantize_symmetric(x.to(cuda), torch.tensor(float(s), device=cuda))
+    np.testing.assert_array_equal(q.cpu().numpy(), O.quantize_symmetric(x.float().numpy(), s))
+
+
+def test_quantize_symmetric_reference_kat(cuda):
+    from nanopointllm_amd import w8a8
+
+    kat = GOLDEN["rounding_clipping"]
+    note("quantize_symmetric KAT")
+    q = w8a8.quantize_symmetric(torch.tensor(kat["values"], device=cuda),
+                                torch.tensor(kat["scale"], device=cuda))
+    assert q.dtype == torch.int8
+    assert q.cpu().tolist() == kat["asserted"]
+    with pytest.raises(ValueError, match="positive"):
+        w8a8.quantize_symmetric(torch.ones(1, device=cuda), torch.tensor(0.0, device=cuda))
+
+
+def test_quantize_per_row_scales(cuda):
+    from nanopointllm_amd import w8a8
+
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(6, 257, generator=g).to(torch.float16)
+    scales = torch.tensor(O.scale_from_absmax(np.abs(x.float().numpy()).max(1, keepdims=True)))
+    note("quantize_symmetric per-row")
+    q = w8a8.quantize_symmetric(x.to(cuda), scales.to(cuda))
+    np.testing.assert_array_equal(q.cpu().numpy(),
+                                  O.quantize_symmetric(x.float().numpy(), scales.numpy()))
+
+
+def test_per_output_weight_qdq(cuda):
+    from nanopointllm_amd import w8a8
+
+    g = torch.Generator().manual_seed(4)
+    w = torch.randn(5, 259, generator=g)
+    note("per_output_weight_qdq")
+    deq, q, s = w8a8.per_output_weight_qdq(w.to(cuda))
+    edeq, eq, es = O.per_output_weight_qdq(w.numpy())
+    np.testing.assert_array_equal(q.cpu().numpy(), eq)
+    np.testing.assert_array_equal(s.cpu().numpy(), es)
+    np.testing.assert_array_equal(deq.cpu().numpy(), edeq)
+
+
+# ------------------------------------------------------------------ packing
+def _pack_numpy(q: np.ndarray, interleave: bool = False) -> np.ndarray:
+    rows, k = q.shape
+    src = q
+    if interleave:
+        half = rows // 2
+        src = np.stack([q[:half], q[half:]], 1).reshape(rows, k)
+    rp, kp = -(-rows // 16) * 16, -(-k // 64) * 64
+    pad = np.zeros((rp, kp), np.int8)
+    pad[:rows, :k] = src
+    # [rb, r, kb, g, b] -> tile (rb, kb), lane r + 16 g, byte b
+    t = pad.reshape(rp // 16, 16, kp // 64, 4, 16).transpose(0, 2, 3, 1, 4)
+    return t.reshape(-1)
+
+
+@pytest.mark.parametrize("rows,k", [(16, 64), (37, 200), (1, 4096), (48, 100)])
+def test_pack_rows_layout(cuda, rows, k):
+    from nanopointllm_amd import _lib, w8a8
+
+    q = rand_i8((rows, k), rows * 7 + k)
+    note(f"pack_rows {rows}x{k}")
+    got = w8a8.pack_rows(q.to(cuda)).cpu().numpy()
+    np.testing.assert_array_equal(got, _pack_numpy(q.numpy()))
+    if rows % 2 == 0:
+        got = w8a8.pack_rows(q.to(cuda), _lib.ROWS_INTERLEAVE_HALVES).cpu().numpy()
+        np.testing.assert_array_equal(got, _pack_numpy(q.numpy(), interleave=True))
+
+
+# ----------------------------------------------------------- int32 products
+GEMM_MS = [1, 2, 3, 8, 15, 16, 17, 31, 33, 64, 65, 100, 128, 129, 300]
+GEMM_NK = [(48, 64), (50, 100), (16, 4096), (136, 320)]
+
+
+@pytest.mark.parametrize("n,k", GEMM_NK)
+@pytest.mark.parametrize("m", GEMM_MS)
+def test_gemm_i32_exact(cuda, m, n, k):
+    from nanopointllm_amd import w8a8
+
+    a = rand_i8((m, k), m * 131 + n)
+    w = rand_i8((n, k), n * 17 + k)
+    note(f"gemm_i32 m={m} n={n} k={k}")
+    acc = w8a8.gemm_i32(a.to(cuda), w8a8.pack_rows(w.to(cuda)), n)
+    np.testing.assert_array_equal(acc.cpu().numpy(), O.int32_matmul_f64(a.numpy(), w.numpy()))
+
+
+def test_gemm_i32_extreme_values(cuda):
+    from nanopointllm_amd import w8a8
+
+    k = 11008
+    a = torch.full((3, k), 127, dtype=torch.int8)
+    a[1] = -127
+    a[2, ::2] = -127
+    w = torch.full((20, k), -127, dtype=torch.int8)
+    w[5] = 127
+    note("gemm_i32 extremes")
+    acc = w8a8.gemm_i32(a.to(cuda), w8a8.pack_rows(w.to(cuda)), 20)
+    np.testing.assert_array_equal(acc.cpu().numpy(), O.int32_matmul_f64(a.numpy(), w.numpy()))
+
+
+def test_gemm_i32_unaligned_and_strided_input(cuda):
+    from nanopointllm_amd import w8a8
+
+    big = rand_i8((80, 130), 77)
+    a = big[:, 1:101]            # leading dimension 130, odd byte offset
+    w = rand_i8((30, 100), 78)
+    wp = w8a8.pack_rows(w.to(cuda))
+    big_d = big.to(cuda)
+    for m in (8, 70):
+        note(f"gemm_i32 strided m={m}")
+        acc = w8a8.gemm_i32(big_d[:m, 1:101], wp, 30)
+        np.testing.assert_array_equal(acc.cpu().numpy(),
+                                      O.int32_matmul_f64(a[:m].numpy(), w.numpy()))
+
+
+def test_package_fixture_on_gpu(cuda, tmp_path):
+    from nanopointllm_amd import package
+
+    pkg = GOLDEN["package"]
+    package.write_quantized_linear_package(
+        tmp_path, activation=np.array(pkg["activation"], np.int8),
+        weight=np.array(pkg["weight"], np.int8),
+        activation_scale=np.array([pkg["activation_scale"]], np.float16),
+        weight_scale=np.array(pkg["weight_scale"], np.float16),
+        smooth_scale=np.array(pkg["smooth_scale"], np.float16),
+        output_scale=np.array([pkg["output_scale"]], np.float16), provenance=pkg["provenance"])
+    loaded = package.load_quantized_linear_package(tmp_path)
+    note("package golden on GPU")
+    got = package.package_integer_golden_gpu(loaded, device=cuda).cpu().numpy()
+    np.testing.assert_array_equal(got, np.array(pkg["derived_integer_golden"], np.int32))
+    np.testing.assert_array_equal(got, loaded.integer_golden())
+
+
+# --------------------------------------------------------------- linears
+def _expected_linear(x: torch.Tensor, q: np.ndarray, s: np.ndarray, bias=None):
+    out, acc, _, _ = O.w8a8_linear_dynamic(x.float().numpy(), q, s, bias)
+    return out, acc
+
+
+def test_config1_single_linear_bit_exact(cuda):
+    """X fp16 [16,4096] with 8 outlier channels x20, W [4096,4096] ~N(0,0.02), seed 0."""
+    from nanopointllm_amd import linear, workloads as W
+
+    x, w = W.config1(seed=0)
+    note("config1 M=16 4096x4096")
+    lin = linear.W8A8Linear(linear.PackedW8A8Weight.from_float(w.to(cuda)))
+    y = lin(x.to(cuda))
+    acc = lin.accumulators(x.to(cuda))
+    _, qw, sw = O.per_output_weight_qdq(w.float().numpy())
+    exp, eacc = _expected_linear(x, qw, sw)
+    np.testing.assert_array_equal(acc.cpu().numpy(), eacc)
+    np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+    err = O.tensor_error(exp, f16_to_np(y).astype(np.float32))
+    note(f"config1 fp16 vs oracle f32: {err}")
+
+
+@pytest.mark.parametrize("m", [1, 4, 8, 16, 17, 40, 64, 65, 130, 560])
+@pytest.mark.parametrize("n,k", [(64, 128), (48, 100), (200, 4096)])
+@pytest.mark.parametrize("with_bias", [False, True])
+def test_linear_fp16_bit_exact(cuda, m, n, k, with_bias):
+    from nanopointllm_amd import w8a8
+
+    x = torch.from_numpy(np.asarray(
+        torch.randn(m, k, generator=torch.Generator().manual_seed(m + n)).numpy() * 2)).to(torch.float16)
+    _, qw, sw = weight_q(n, k, seed=n + k)
+    bias = (np.linspace(-1, 1, n).astype(np.float32) if with_bias else None)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    note(f"linear fp16 m={m} n={n} k={k} bias={with_bias}")
+    y = w8a8.linear_dynamic(x.to(cuda), wp, torch.from_numpy(sw).to(cuda),
+                            None if bias is None else torch.from_numpy(bias).to(cuda), n)
+    exp, _ = _expected_linear(x, qw, sw, bias)
+    np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+
+
+@pytest.mark.parametrize("m", [8, 200])
+def test_linear_other_dtypes(cuda, m):
+    from nanopointllm_amd import w8a8
+
+    n, k = 96, 256
+    g = torch.Generator().manual_seed(m)
+    _, qw, sw = weight_q(n, k, seed=9)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    swt = torch.from_numpy(sw).to(cuda)
+    xb = (torch.randn(m, k, generator=g) * 4).to(torch.bfloat16)
+    note(f"linear bf16->bf16/f32 m={m}")
+    exp, _ = _expected_linear(xb, qw, sw)
+    yb = w8a8.linear_dynamic(xb.to(cuda), wp, swt, None, n)
+    np.testing.assert_array_equal(bf16_bits(yb), O.f32_to_bf16_bits(exp))
+    yf = w8a8.linear_dynamic(xb.to(cuda), wp, swt, None, n, out_dtype=torch.float32)
+    np.testing.assert_array_equal(yf.cpu().numpy(), exp)
+    xf = torch.randn(m, k, generator=g)
+    note(f"linear f32 in m={m}")
+    expf, _ = _expected_linear(xf, qw, sw)
+    yf2 = w8a8.linear_dynamic(xf.to(cuda), wp, swt, None, n, out_dtype=torch.float32)
+    np.testing.assert_array_equal(yf2.cpu().numpy(), expf)
+
+
+def test_linear_3d_and_empty(cuda):
+    from nanopointllm_amd import linear
+
+    g = torch.Generator().manual_seed(2)
+    w = torch.randn(32, 64, generator=g).to(torch.float16)
+    lin = linear.W8A8Linear(linear.PackedW8A8Weight.from_float(w.to(cuda)))
+    x = torch.randn(1, 5, 64, generator=g).to(torch.float16)
+    note("linear 3d + empty")
+    y = lin(x.to(cuda))
+    assert y.shape == (1, 5, 32)
+    _, qw, sw = O.per_output_weight_qdq(w.float().numpy())
+    exp, _ = _expected_linear(x[0], qw, sw)
+    np.testing.assert_array_equal(f16_to_np(y[0]), exp.astype(np.float16))
+    assert lin(torch.empty(0, 64, dtype=torch.float16, device=cuda)).shape == (0, 32)
+
+
+@pytest.mark.parametrize("m", [1, 8, 16, 64, 100, 567])
+def test_linear_i8in_exact(cuda, m):
+    from nanopointllm_amd import w8a8
+
+    n, k = 80, 11008 if m <= 16 else 704
+    xq = rand_i8((m, k), m)
+    sx = O.scale_from_absmax(np.abs(np.random.default_rng(m).standard_normal((m, 1))) * 3)
+    _, qw, sw = weight_q(n, k, seed=5)
+    note(f"linear_i8in m={m} k={k}")
+    y = w8a8.linear_i8in(xq.to(cuda), torch.from_numpy(sx).to(cuda),
+                         w8a8.pack_rows(torch.from_numpy(qw).to(cuda)),
+                         torch.from_numpy(sw).to(cuda), None, n, out_dtype=torch.float16)
+    exp, _ = O.linear_from_quantized(xq.numpy(), sx, qw, sw)
+    np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+
+
+def test_integer_linear_per_output_kat_and_random(cuda):
+    from nanopointllm_amd import w8a8
+
+    kat = GOLDEN["tiny_int32_linear"]
+    x = torch.tensor(kat["values"])
+    w = torch.tensor(kat["weight"])
+    b = torch.tensor(kat["bias"])
+    s = torch.tensor(O.static_activation_scale(np.abs(x.numpy()).max()))
+    note("integer_linear_per_output KAT")
+    out, acc = w8a8.integer_linear_per_output(x.to(cuda), w.to(cuda),
+                                              activation_scale=s.to(cuda), bias=b.to(cuda))
+    eout, eacc = O.integer_linear_per_output(x.numpy(), w.numpy(), activation_scale=s.numpy(),
+                                             bias=b.numpy())
+    assert acc.dtype == torch.int32
+    np.testing.assert_array_equal(acc.cpu().numpy(), eacc)
+    np.testing.assert_array_equal(out.cpu().numpy(), eout)
+    g = torch.Generator().manual_seed(6)
+    x = torch.randn(9, 300, generator=g)
+    w = torch.randn(70, 300, generator=g)
+    s = torch.tensor(O.scale_from_absmax(np.abs(x.numpy()).max(1, keepdims=True)))
+    note("integer_linear_per_output per-token")
+    out, acc = w8a8.integer_linear_per_output(x.to(cuda), w.to(cuda), activation_scale=s.to(cuda))
+    eout, eacc = O.integer_linear_per_output(x.numpy(), w.numpy(), activation_scale=s.numpy())
+    np.testing.assert_array_equal(acc.cpu().numpy(), eacc)
+    np.testing.assert_array_equal(out.cpu().numpy(), eout)
+
+
+# --------------------------------------------------------- gate/up + SiLU
+def _gateup_case(m, inter, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = (torch.randn(m, k, generator=g) * 1.5).to(torch.float16)
+    wg = (torch.randn(inter, k, generator=g) * 0.05).to(torch.float16)
+    wu = (torch.randn(inter, k, generator=g) * 0.05).to(torch.float16)
+    return x, wg, wu
+
+
+def _fp16_ulps(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """Distance in binary16 ulps (ordered-integer difference)."""
+    def key(v):
+        i = v.astype(np.float16).view(np.int16).astype(np.int32)
+        return np.where(i < 0, -(i & 0x7FFF), i)
+    return np.abs(key(a) - key(b))
+
+
+@pytest.mark.parametrize("m", [1, 8, 16, 64, 65, 567])
+def test_gateup_silu_mul(cuda, m):
+    from nanopointllm_amd import linear
+
+    inter, k = 264, 512
+    x, wg, wu = _gateup_case(m, inter, k, seed=m)
+    gate = torch.nn.Linear(k, inter, bias=False)
+    up = torch.nn.Linear(k, inter, bias=False)
+    gate.weight.data, up.weight.data = wg.to(cuda), wu.to(cuda)
+    mod = linear.W8A8GateUpSiluMul(gate, up)
+    note(f"gateup silu m={m}")
+    h = f16_to_np(mod(x.to(cuda)))
+    acc = mod.accumulators(x.to(cuda)).cpu().numpy()
+    _, qg, sg = O.per_output_weight_qdq(wg.float().numpy())
+    _, qu, su = O.per_output_weight_qdq(wu.float().numpy())
+    qp = O.pack_gateup_rows(qg, qu, "interleave")
+    sp = O.pack_gateup_rows(sg[:, None], su[:, None], "interleave")[:, 0]
+    xq, sx = O.dynamic_per_token_quant(x.float().numpy())
+    eacc = O.int32_matmul_f64(xq, qp)
+    np.testing.assert_array_equal(acc, eacc)
+    eh = O.gateup_silu_mul_from_acc(eacc, sx, sp, layout="interleave")
+    ulps = _fp16_ulps(h, eh)
+    note(f"gateup silu m={m}: exact {np.mean(ulps == 0):.6f}, max ulp {ulps.max()}")
+    assert ulps.max() <= 1
+    assert np.mean(ulps == 0) > 0.99
+
+
+@pytest.mark.parametrize("m", [8, 567])
+def test_mlp_int8_chain(cuda, m):
+    """gate/up -> SiLU*mul -> static int8 requant -> int8-in down projection."""
+    from nanopointllm_amd import linear, w8a8
+
+    inter, k = 264, 512
+    x, wg, wu = _gateup_case(m, inter, k, seed=100 + m)
+    g = torch.Generator().manual_seed(7)
+    wd = (torch.randn(k, inter, generator=g) * 0.05).to(torch.float16)
+    mods = [torch.nn.Linear(k, inter, bias=False), torch.nn.Linear(k, inter, bias=False),
+            torch.nn.Linear(inter, k, bias=False)]
+    for mod_, wt in zip(mods, (wg, wu, wd)):
+        mod_.weight.data = wt.to(cuda)
+    h_ref = linear.W8A8GateUpSiluMul(mods[0], mods[1])(x.to(cuda))
+    h_scale = float(O.static_activation_scale(float(h_ref.abs().max().item())))
+    mlp = linear.W8A8MLP(*mods, h_scale=h_scale)
+    note(f"mlp int8 chain m={m}")
+    hq = mlp.gate_up.forward_q8(x.to(cuda), h_scale).cpu().numpy()
+    y = f16_to_np(mlp(x.to(cuda)))
+    # Stage 1: the int8 epilogue equals the oracle's requant of the GPU's own h.
+    eq = O.quantize_symmetric(f16_to_np(h_ref).astype(np.float32), np.float32(h_scale))
+    np.testing.assert_array_equal(hq, eq)
+    # Stage 2: the down projection on the GPU's int8 h is exact.
+    _, qd, sd = O.per_output_weight_qdq(wd.float().numpy())
+    sx = np.full((m, 1), h_scale, np.float32)
+    exp, _ = O.linear_from_quantized(hq, sx, qd, sd)
+    np.testing.assert_array_equal(y, exp.astype(np.float16))
+    acc = w8a8.gemm_i32(torch.from_numpy(hq).to(cuda), mlp.down.weight_q.packed, k)
+    np.testing.assert_array_equal(acc.cpu().numpy(), O.int32_matmul_f64(hq, qd))
+
+
+def test_packed_qkv_split_matches_separate_linears(cuda):
+    from nanopointllm_amd import linear
+
+    g = torch.Generator().manual_seed(11)
+    k, heads, hd = 256, 4, 32
+    projs = []
+    for _ in range(3):
+        p = torch.nn.Linear(k, heads * hd, bias=True)
+        p.weight.data = (torch.randn(heads * hd, k, generator=g) * 0.05).to(torch.float16).to(cuda)
+        p.bias.data = torch.randn(heads * hd, generator=g).to(torch.float16).to(cuda)
+        projs.append(p)
+    qkv = linear.W8A8PackedQKV(*projs, num_heads=heads, num_kv_heads=heads, head_dim=hd)
+    x = torch.randn(1, 6, k, generator=g).to(torch.float16)
+    note("packed qkv")
+    q, kk, v = qkv.project(x.to(cuda))
+    for got, p in zip((q, kk, v), projs):
+        sep = linear.W8A8Linear.from_linear(p)(x[0].to(cuda))
+        np.testing.assert_array_equal(f16_to_np(got.reshape(6, -1)), f16_to_np(sep))
+
+
+# ----------------------------------------------------- full LLaMA-7B shapes
+@pytest.mark.parametrize("m", [1, 8, 560])
+@pytest.mark.parametrize("proj", ["qkv", "o", "gateup", "down"])
+def test_llama7b_shapes_exact(cuda, m, proj):
+    from nanopointllm_amd import w8a8, workloads as W
+
+    spec = {p.name: p for p in W.PROJECTIONS}[proj]
+    x = (W.decode_activations(m, spec.k, seed=m) if m <= 16
+         else W.prefill_activations(m, spec.k, seed=m))
+    wq = torch.randint(-127, 128, (spec.n, spec.k), generator=torch.Generator().manual_seed(3),
+                       dtype=torch.int8)
+    sw = O.scale_from_absmax(np.abs(np.random.default_rng(1).standard_normal(spec.n)) * 0.08)
+    note(f"llama7b {proj} m={m} n={spec.n} k={spec.k}")
+    wp = w8a8.pack_rows(wq.to(cuda))
+    xc = x.to(cuda)
+    acc = w8a8.linear_dynamic(xc, wp, torch.from_numpy(sw).to(cuda), None, spec.n,
+                              epilogue=0).cpu().numpy()
+    xq, sx = O.dynamic_per_token_quant(x.float().numpy())
+    eacc = O.int32_matmul_f64(xq, wq.numpy())
+    np.testing.assert_array_equal(acc, eacc)
+    if not spec.silu:
+        y = w8a8.linear_dynamic(xc, wp, torch.from_numpy(sw).to(cuda), None, spec.n)
+        np.testing.assert_array_equal(f16_to_np(y), O.dequant_epilogue(eacc, sx, sw).astype(np.float16))
