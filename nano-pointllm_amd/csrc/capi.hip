@@ -249,10 +249,16 @@ int w8a8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
   if (x == nullptr) return W8A8_ERR_NULL;
   if (ldx < k) return W8A8_ERR_SHAPE;
   if (!aligned(x, static_cast<uintptr_t>(elem_size(x_dtype)))) return W8A8_ERR_ALIGN;
+  if (x_scale_out != nullptr && !aligned(x_scale_out, 4)) return W8A8_ERR_ALIGN;
+  if (k > 0 && fused_gemv_supported(x, x_dtype, ldx, m, k)) {
+    // Decode: quantization fused into the GEMV, no workspace.
+    LinearOperands op = make_ops(nullptr, 0, nullptr, w_packed, w_scale, bias, epilogue, y,
+                                 y_dtype, ldy, y_scale, inter_dtype, m, n, k);
+    return status_of(launch_gemv_fused(x, x_dtype, ldx, op, x_scale_out, stream));
+  }
   if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
     return W8A8_ERR_WORKSPACE;
-  if (!aligned(workspace, 16) || (x_scale_out != nullptr && !aligned(x_scale_out, 4)))
-    return W8A8_ERR_ALIGN;
+  if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
   float* sx = x_scale_out != nullptr ? x_scale_out : static_cast<float*>(workspace);
   int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
   const int64_t kp = round_up(k, kTileK);

@@ -167,19 +167,28 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   }
 }
 
-template <int MT, int CH, int EPI, typename TY, typename TH>
+template <int WAVES, int MT, int CH, int EPI, typename TY, typename TH>
 hipError_t launch_cfg(const GemvParams& p, int64_t nblocks, hipStream_t st) {
-  constexpr int WAVES = 4;
   hipLaunchKernelGGL((gemv_kernel<WAVES, MT, CH, EPI, TY, TH>),
                      dim3(static_cast<unsigned>(nblocks)), dim3(WAVES * 64), 0, st, p);
   return hipGetLastError();
 }
 
+// Launch shape.  Few output blocks (O / down: 256 blocks for 256 CUs) get
+// 16 wavefronts per block so every CU keeps ~64 KiB of weight loads in
+// flight; many blocks (QKV, gate/up) use 4 wavefronts and several resident
+// blocks per CU.
 template <int EPI, typename TY, typename TH>
 hipError_t launch_mt(const GemvParams& p, int64_t nblocks, hipStream_t st) {
-  if (p.M <= 16) return launch_cfg<1, 8, EPI, TY, TH>(p, nblocks, st);
-  if (p.M <= 32) return launch_cfg<2, 4, EPI, TY, TH>(p, nblocks, st);
-  return launch_cfg<4, 2, EPI, TY, TH>(p, nblocks, st);
+  const bool few = nblocks <= 512;
+  if (p.M <= 16)
+    return few ? launch_cfg<16, 1, 4, EPI, TY, TH>(p, nblocks, st)
+               : launch_cfg<4, 1, 8, EPI, TY, TH>(p, nblocks, st);
+  if (p.M <= 32)
+    return few ? launch_cfg<8, 2, 4, EPI, TY, TH>(p, nblocks, st)
+               : launch_cfg<4, 2, 4, EPI, TY, TH>(p, nblocks, st);
+  return few ? launch_cfg<8, 4, 2, EPI, TY, TH>(p, nblocks, st)
+             : launch_cfg<4, 4, 2, EPI, TY, TH>(p, nblocks, st);
 }
 
 }  // namespace

@@ -14,13 +14,47 @@ namespace w8a8 {
 namespace {
 
 constexpr int kQuantThreads = 256;
+// Rows up to kQuantThreads * 8 * kRegChunks elements are held in registers
+// between the absmax pass and the quantize pass (one global read).
+constexpr int kRegChunks = 8;
 
-// One workgroup per row.  Pass 1 reduces |x| over the row (or reads the
-// caller's scale); pass 2 quantizes 8 elements per thread-iteration and
-// writes either a row-major int8 row or the row's slots of the packed tiles.
-// For packed output the grid covers ceil(rows/16)*16 rows and every row
-// writes all ceil(K/64)*64 columns, so tile padding is zero-filled.
-template <typename TX, bool PACKED, bool DYNAMIC>
+// Quantizes one value with the row scale s.  The division-free form needs a
+// 16-bit input and a binary16-representable scale (always true for dynamic
+// scales; checked per row for caller scales); otherwise divide.
+template <typename TX>
+__device__ inline int32_t quant_elem(float x, float s, float r, bool fast) {
+  if constexpr (sizeof(TX) == 2) {
+    if (fast) return quant1_h(x, s, r);
+  }
+  return quant1(x, s);
+}
+
+// Writes 8 quantized values of row `row` starting at column k0.
+template <bool PACKED>
+__device__ inline void store8(int8_t* __restrict__ q, int64_t row, int64_t k0, int64_t ldq,
+                              int64_t ncols_out, int vec_out, int64_t KB, const int32_t (&qi)[8]) {
+  u32x2 word = {pack4_i8(qi[0], qi[1], qi[2], qi[3]), pack4_i8(qi[4], qi[5], qi[6], qi[7])};
+  if constexpr (PACKED) {
+    *reinterpret_cast<u32x2*>(q + packed_offset(row, k0, KB)) = word;
+  } else {
+    // Row-major: columns K..ncols_out-1 are written as zeros.
+    int8_t* dst = q + row * ldq + k0;
+    const int nw = static_cast<int>(ncols_out - k0 < 8 ? ncols_out - k0 : 8);
+    if (vec_out && nw == 8) {
+      *reinterpret_cast<u32x2*>(dst) = word;
+    } else {
+      for (int j = 0; j < nw; ++j) dst[j] = static_cast<int8_t>(qi[j]);
+    }
+  }
+}
+
+// One workgroup per row.  The row (8 elements per thread-chunk) is read once
+// into registers when it fits (REG), reduced to |x|max for a dynamic scale
+// (or the caller's scale is read), then quantized and written either as a
+// row-major int8 row or as the row's slots of the packed tiles.  For packed
+// output the grid covers ceil(rows/16)*16 rows and every row writes all
+// ceil(K/64)*64 columns, so tile padding is zero-filled.
+template <typename TX, bool PACKED, bool DYNAMIC, bool REG>
 __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
     const TX* __restrict__ x, int64_t ldx, int64_t rows, int64_t K, int vec_in,
     const float* __restrict__ scale_in, int64_t scale_stride, int8_t* __restrict__ q,
@@ -31,17 +65,38 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
   const bool live = row < rows;
   const TX* xr = x + (live ? row : 0) * ldx;
   const int64_t nchunk_in = (K + 7) / 8;
+  const int64_t nchunk_out = PACKED ? KB * 8 : (ncols_out + 7) / 8;
+
+  float v[REG ? kRegChunks : 1][8];
+  if constexpr (REG) {
+#pragma unroll
+    for (int c = 0; c < kRegChunks; ++c) {
+      const int64_t k0 = (tid + static_cast<int64_t>(c) * kQuantThreads) * 8;
+      const int64_t rem = K - k0;
+      if (live && rem > 0) {
+        load8(xr + k0, v[c], vec_in != 0, static_cast<int>(rem < 8 ? rem : 8));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[c][j] = 0.0f;
+      }
+    }
+  }
 
   float s = 1.0f;
   if constexpr (DYNAMIC) {
     float amax = 0.0f;
-    if (live) {
-      for (int64_t c = tid; c < nchunk_in; c += kQuantThreads) {
-        float v[8];
-        const int64_t k0 = c * 8;
-        load8(xr + k0, v, vec_in != 0, static_cast<int>(K - k0 < 8 ? K - k0 : 8));
+    if constexpr (REG) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[j]));
+      for (int c = 0; c < kRegChunks; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[c][j]));
+    } else if (live) {
+      for (int64_t c = tid; c < nchunk_in; c += kQuantThreads) {
+        float t[8];
+        const int64_t k0 = c * 8;
+        load8(xr + k0, t, vec_in != 0, static_cast<int>(K - k0 < 8 ? K - k0 : 8));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(t[j]));
       }
     }
 #pragma unroll
@@ -55,35 +110,38 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
   } else {
     if (live) s = scale_in[row * scale_stride];
   }
+  const float r = 1.0f / s;
+  const bool fast = DYNAMIC || __half2float(__float2half_rn(s)) == s;
   if (live && tid == 0 && scales_out != nullptr) scales_out[row] = s;
 
-  const int64_t nchunk_out = PACKED ? KB * 8 : (ncols_out + 7) / 8;
-  for (int64_t c = tid; c < nchunk_out; c += kQuantThreads) {
-    const int64_t k0 = c * 8;
-    const int64_t rem = K - k0;
-    const int valid = live ? static_cast<int>(rem <= 0 ? 0 : (rem < 8 ? rem : 8)) : 0;
-    float v[8];
-    if (valid > 0) {
-      load8(xr + k0, v, vec_in != 0, valid);
-    } else {
+  if constexpr (REG) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-    }
-    int32_t qi[8];
+    for (int c = 0; c < kRegChunks; ++c) {
+      const int64_t chunk = tid + static_cast<int64_t>(c) * kQuantThreads;
+      if (chunk < nchunk_out) {
+        const int64_t k0 = chunk * 8;
+        int32_t qi[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) qi[j] = (j < valid) ? quant1(v[j], s) : 0;
-    u32x2 word = {pack4_i8(qi[0], qi[1], qi[2], qi[3]), pack4_i8(qi[4], qi[5], qi[6], qi[7])};
-    if constexpr (PACKED) {
-      *reinterpret_cast<u32x2*>(q + packed_offset(row, k0, KB)) = word;
-    } else {
-      // Row-major: columns K..ncols_out-1 are written as zeros.
-      int8_t* dst = q + row * ldq + k0;
-      const int nw = static_cast<int>(ncols_out - k0 < 8 ? ncols_out - k0 : 8);
-      if (vec_out && nw == 8) {
-        *reinterpret_cast<u32x2*>(dst) = word;
-      } else {
-        for (int j = 0; j < nw; ++j) dst[j] = static_cast<int8_t>(qi[j]);
+        for (int j = 0; j < 8; ++j) qi[j] = quant_elem<TX>(v[c][j], s, r, fast);
+        store8<PACKED>(q, row, k0, ldq, ncols_out, vec_out, KB, qi);
       }
+    }
+  } else {
+    for (int64_t c = tid; c < nchunk_out; c += kQuantThreads) {
+      const int64_t k0 = c * 8;
+      const int64_t rem = K - k0;
+      const int valid = live ? static_cast<int>(rem <= 0 ? 0 : (rem < 8 ? rem : 8)) : 0;
+      float t[8];
+      if (valid > 0) {
+        load8(xr + k0, t, vec_in != 0, valid);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) t[j] = 0.0f;
+      }
+      int32_t qi[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qi[j] = (j < valid) ? quant_elem<TX>(t[j], s, r, fast) : 0;
+      store8<PACKED>(q, row, k0, ldq, ncols_out, vec_out, KB, qi);
     }
   }
 }
@@ -154,6 +212,19 @@ __global__ __launch_bounds__(256) void pad_rows_kernel(const int8_t* __restrict_
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
+template <typename TX, bool PACKED, bool DYN>
+void quant_launch(dim3 g, dim3 b, hipStream_t st, bool reg, const TX* x, int64_t ldx,
+                  int64_t rows, int64_t K, int vec_in, const float* scale_in,
+                  int64_t scale_stride, int8_t* q, int64_t ldq, int64_t ncols_out, int vec_out,
+                  int64_t KB, float* scales_out) {
+  if (reg)
+    hipLaunchKernelGGL((quant_rows_kernel<TX, PACKED, DYN, true>), g, b, 0, st, x, ldx, rows, K,
+                       vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+  else
+    hipLaunchKernelGGL((quant_rows_kernel<TX, PACKED, DYN, false>), g, b, 0, st, x, ldx, rows, K,
+                       vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+}
+
 template <typename TX>
 hipError_t quant_dispatch(const TX* x, int64_t ldx, int64_t rows, int64_t K,
                           const float* scale_in, int64_t scale_stride, int8_t* q, int64_t ldq,
@@ -163,22 +234,24 @@ hipError_t quant_dispatch(const TX* x, int64_t ldx, int64_t rows, int64_t K,
   const int64_t KB = ceil_div(K, kTileK);
   const int64_t grid = packed ? ceil_div(rows, kTileRows) * kTileRows : rows;
   if (grid == 0) return hipSuccess;
+  const int64_t chunks = packed ? KB * 8 : ceil_div(ncols_out > K ? ncols_out : K, 8);
+  const bool reg = chunks <= static_cast<int64_t>(kQuantThreads) * kRegChunks;
   const bool dyn = scale_in == nullptr;
   dim3 g(static_cast<unsigned>(grid)), b(kQuantThreads);
   if (packed) {
     if (dyn)
-      hipLaunchKernelGGL((quant_rows_kernel<TX, true, true>), g, b, 0, st, x, ldx, rows, K,
-                         vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+      quant_launch<TX, true, true>(g, b, st, reg, x, ldx, rows, K, vec_in, scale_in,
+                                   scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
     else
-      hipLaunchKernelGGL((quant_rows_kernel<TX, true, false>), g, b, 0, st, x, ldx, rows, K,
-                         vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+      quant_launch<TX, true, false>(g, b, st, reg, x, ldx, rows, K, vec_in, scale_in,
+                                    scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
   } else {
     if (dyn)
-      hipLaunchKernelGGL((quant_rows_kernel<TX, false, true>), g, b, 0, st, x, ldx, rows, K,
-                         vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+      quant_launch<TX, false, true>(g, b, st, reg, x, ldx, rows, K, vec_in, scale_in,
+                                    scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
     else
-      hipLaunchKernelGGL((quant_rows_kernel<TX, false, false>), g, b, 0, st, x, ldx, rows, K,
-                         vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+      quant_launch<TX, false, false>(g, b, st, reg, x, ldx, rows, K, vec_in, scale_in,
+                                     scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
   }
   return hipGetLastError();
 }

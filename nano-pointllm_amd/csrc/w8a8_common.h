@@ -108,6 +108,25 @@ __device__ inline int32_t quant1(float x, float s) {
   return static_cast<int32_t>(q);
 }
 
+// quantize_symmetric for a binary16 / bfloat16 input x without a division.
+// r is any binary32 approximation of 1/s within a few ulps (v_rcp_f32 is).
+// Exactness: with s binary16 and x of at most 11 significant bits, the exact
+// quotient z = x/s is either a half-integer k+0.5 or at least 2^-12 away
+// from every half-integer (x - (k+0.5)s is a nonzero multiple of
+// 2^(e(s)-11) and s < 2^(e(s)+1)), while |x*r - z| <= 128 * 3 * 2^-24 <
+// 2^-15 for |z| < 128.  So rint(x*r) == rint(fl32(x/s)) except at exact
+// ties, which are detected exactly: c*s is exact for c = floor(x*r) + 0.5,
+// and fma(-c, s, x) is zero iff x == c*s.  Ties round to even via rint(c).
+// |z| >= 128 always clamps to +-127 on both paths.
+__device__ inline int32_t quant1_h(float x, float s, float r) {
+  const float y = x * r;
+  const float c = floorf(y) + 0.5f;
+  const bool tie = __builtin_fmaf(-c, s, x) == 0.0f;
+  float q = __builtin_rintf(tie ? c : y);
+  q = fminf(fmaxf(q, -127.0f), 127.0f);
+  return static_cast<int32_t>(q);
+}
+
 __device__ inline uint32_t pack4_i8(int32_t a, int32_t b, int32_t c, int32_t d) {
   return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
          ((static_cast<uint32_t>(c) & 0xffu) << 16) | ((static_cast<uint32_t>(d) & 0xffu) << 24);

@@ -156,14 +156,19 @@ def linear_dynamic(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tenso
     cols = _out_cols(epilogue, n)
     y = torch.empty((m, cols), dtype=out_dtype, device=device)
     if m and n:
-        ws = _workspace(m, k, device)
         lib = _lib.load()
-        _lib.check(lib.w8a8_linear(
-            x2.data_ptr(), _lib.dtype_code(x2.dtype), ldx, w_packed.data_ptr(),
-            w_scale.data_ptr(), _lib.ptr(bias), epilogue, y.data_ptr(),
-            _lib.dtype_code(out_dtype), cols, float(y_scale), _lib.dtype_code(inter_dtype),
-            m, n, k, _lib.ptr(x_scale_out), ws.data_ptr(), ws.numel(),
-            _lib.stream_handle(device)), "w8a8_linear")
+        args = [x2.data_ptr(), _lib.dtype_code(x2.dtype), ldx, w_packed.data_ptr(),
+                w_scale.data_ptr(), _lib.ptr(bias), epilogue, y.data_ptr(),
+                _lib.dtype_code(out_dtype), cols, float(y_scale), _lib.dtype_code(inter_dtype),
+                m, n, k, _lib.ptr(x_scale_out)]
+        stream = _lib.stream_handle(device)
+        # Decode shapes run fused and need no workspace; others report
+        # ERR_WORKSPACE (before any launch) and are retried with one.
+        rc = lib.w8a8_linear(*args, None, 0, stream)
+        if rc == _lib.ERR_WORKSPACE:
+            ws = _workspace(m, k, device)
+            rc = lib.w8a8_linear(*args, ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "w8a8_linear")
     return y.reshape(*x.shape[:-1], cols)
 
 

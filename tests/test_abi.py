@@ -41,7 +41,9 @@ def test_sizes_and_version():
 
 def test_invalid_arguments_return_status_without_launch():
     lib = _lib.load()
-    fake = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+    # Never dereferenced: every call below fails validation before any launch
+    # (none of them is a valid decode-path call that would run a kernel).
+    fake = ctypes.c_void_p(0x1000)
     # negative shape
     assert lib.w8a8_quant_rows(fake, _lib.F16, -1, 4, 4, fake, 4, fake, None) == _lib.ERR_SHAPE
     # unsupported input dtype
@@ -62,9 +64,9 @@ def test_invalid_arguments_return_status_without_launch():
     assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_SILU_MUL_Q8, fake,
                            _lib.I8, 8, 0.0, _lib.F16, 1, 16, 64, None, fake, 1 << 20,
                            None) == _lib.ERR_SHAPE
-    # workspace too small
+    # workspace too small (m = 9 is outside the workspace-free decode path)
     assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_DEQUANT, fake,
-                           _lib.F16, 16, 0.0, _lib.F16, 1, 16, 64, None, fake, 10,
+                           _lib.F16, 16, 0.0, _lib.F16, 9, 16, 64, None, fake, 10,
                            None) == _lib.ERR_WORKSPACE
     # misaligned packed weights
     assert lib.w8a8_gemm_i32(fake, 64, ctypes.c_void_p(0x1001), fake, 16, 1, 16, 64, fake,

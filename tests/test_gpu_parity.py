@@ -2,7 +2,8 @@
 
 Bars: int8 / int32 results bit-exact; binary16 / bfloat16 / binary32 outputs
 bit-equal to the oracle's binary32 result rounded once; SiLU*mul outputs
-within one binary16 ulp (the GPU and CPU ``exp`` may differ by an ulp), with
+within two binary16 ulps and >99.9% bit-equal (the GPU and CPU ``exp`` may
+differ by an ulp, widened by the binary16 product), with
 the downstream int32 of the int8 chain bit-exact against the oracle fed the
 GPU's own int8 ``h``.
 """
@@ -69,6 +70,26 @@ def test_quant_rows_bit_exact(cuda, dtype, shape):
     eq, es = O.dynamic_per_token_quant(xn)
     np.testing.assert_array_equal(s.cpu().numpy(), es[:, 0])
     np.testing.assert_array_equal(q.cpu().numpy(), eq)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_quant_exhaustive_16bit_inputs(cuda, dtype):
+    """Every finite 16-bit value against the oracle's binary32 division, one
+    scale per row: binary16 scales take the division-free path, the last
+    scale (0.1, not binary16-representable) the dividing path."""
+    from nanopointllm_amd import w8a8
+
+    allv = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(dtype)
+    vals = allv[torch.isfinite(allv.float())]
+    scales = [2.0 ** -14, 2.0 ** -24, 0.0124359130859375, 1.0 / 127, 0.33325, 1.0, 7.5,
+              1000.0, 0.1]
+    s32 = np.array([np.float32(np.float16(v)) for v in scales[:-1]] + [np.float32(0.1)],
+                   np.float32)
+    x = vals.reshape(1, -1).expand(len(scales), -1).contiguous()
+    note(f"quant exhaustive {dtype} {tuple(x.shape)}")
+    q = w8a8.quantize_symmetric(x.to(cuda), torch.from_numpy(s32).reshape(-1, 1).to(cuda))
+    exp = O.quantize_symmetric(x.float().numpy(), s32[:, None])
+    np.testing.assert_array_equal(q.cpu().numpy(), exp)
 
 
 def test_quant_ties_round_to_even(cuda):
@@ -253,6 +274,53 @@ def test_linear_fp16_bit_exact(cuda, m, n, k, with_bias):
     np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
 
 
+@pytest.mark.parametrize("m", [1, 2, 3, 5, 7, 8])
+@pytest.mark.parametrize("n,k", [(16, 8), (40, 64), (300, 1000), (96, 11008), (64, 12288)])
+def test_fused_decode_path(cuda, m, n, k):
+    """Workspace-free decode kernel (quantization fused in): outputs, row
+    scales and int32 accumulators against the oracle."""
+    from nanopointllm_amd import _lib, w8a8
+
+    g = torch.Generator().manual_seed(m * 1000 + k)
+    x = (torch.randn(m, k, generator=g) * 2.5)
+    x[:, :: max(1, k // 7)] *= 30
+    x = x.to(torch.float16)
+    _, qw, sw = weight_q(n, k, seed=n + 3)
+    bias = np.linspace(-2, 2, n).astype(np.float32)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    sx = torch.full((m,), -1.0, device=cuda)
+    note(f"fused decode m={m} n={n} k={k}")
+    y = w8a8.linear_dynamic(x.to(cuda), wp, torch.from_numpy(sw).to(cuda),
+                            torch.from_numpy(bias).to(cuda), n, x_scale_out=sx)
+    acc = w8a8.linear_dynamic(x.to(cuda), wp, torch.from_numpy(sw).to(cuda), None, n,
+                              epilogue=_lib.EPI_I32)
+    exp, eacc, _, esx = O.w8a8_linear_dynamic(x.float().numpy(), qw, sw, bias)
+    np.testing.assert_array_equal(sx.cpu().numpy(), esx[:, 0])
+    np.testing.assert_array_equal(acc.cpu().numpy(), eacc)
+    np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+
+
+def test_fused_path_strided_rows_and_fallbacks(cuda):
+    from nanopointllm_amd import w8a8
+
+    n, k = 48, 512
+    _, qw, sw = weight_q(n, k, seed=12)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    swt = torch.from_numpy(sw).to(cuda)
+    g = torch.Generator().manual_seed(1)
+    big = torch.randn(6, 2 * k + 8, generator=g).to(torch.float16)
+    cases = {
+        "ld 1032 aligned": big[:, :k],            # fused, leading dimension 1032
+        "unaligned base": big[:, 1:k + 1],        # not 16-byte aligned: quant + GEMV
+    }
+    for name, xv in cases.items():
+        note(f"fused strided {name}")
+        y = w8a8.linear_dynamic(big.to(cuda)[:, :k] if name == "ld 1032 aligned"
+                                else big.to(cuda)[:, 1:k + 1], wp, swt, None, n)
+        exp, _, _, _ = O.w8a8_linear_dynamic(xv.float().numpy(), qw, sw)
+        np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+
+
 @pytest.mark.parametrize("m", [8, 200])
 def test_linear_other_dtypes(cuda, m):
     from nanopointllm_amd import w8a8
@@ -375,8 +443,11 @@ def test_gateup_silu_mul(cuda, m):
     eh = O.gateup_silu_mul_from_acc(eacc, sx, sp, layout="interleave")
     ulps = _fp16_ulps(h, eh)
     note(f"gateup silu m={m}: exact {np.mean(ulps == 0):.6f}, max ulp {ulps.max()}")
-    assert ulps.max() <= 1
-    assert np.mean(ulps == 0) > 0.99
+    # GPU and CPU binary32 exp may differ by an ulp; after the binary16
+    # rounding of SiLU(g) that is at most one ulp of the intermediate, which
+    # the binary16 product with u can widen to two ulps of h.
+    assert ulps.max() <= 2
+    assert np.mean(ulps == 0) > 0.999
 
 
 @pytest.mark.parametrize("m", [8, 567])
