@@ -4,16 +4,24 @@
 // 1488; llama/lightweight_runner.py:320-404) for the int8 contract of
 // integer_linear_per_output_reference (nanopointllm/compression/w8a8.py:118-139).
 //
-// Design (MFMA-bound): 256-thread workgroups own a 128 x 128 output tile; the
-// four wavefronts form a 2 x 2 grid of 64 x 64 sub-tiles (4 x 4
-// v_mfma_i32_16x16x64_i8 fragments, 64 accumulator VGPRs each).  Both operands
-// are in the packed 16x64 tile layout, so one k-step (64) of the workgroup
-// tile is 16 fragments of 1 KiB: each wavefront copies four of them with
-// coalesced global_load_dwordx4 into registers one step ahead, and the LDS
-// stage is double-buffered so one barrier per k-step suffices.  Fragments are
-// read back with conflict-free ds_read_b128 (lane l reads bytes 16l..16l+15).
-// Workgroups are mapped XCD-major: consecutive tiles of the same weight
-// column block land on the same XCD and share its L2.
+// Design (MFMA-bound), chosen by measurement on MI355X:
+//   * v_mfma_i32_32x32x32_i8, which sustains ~2x the int8 rate of the
+//     16x16x64 form (4.4 vs 2.7 POPS in a register-only loop).
+//   * Every wavefront owns one 32x32 output block; the workgroup tile is a
+//     WM x WN grid of them: 128x128 with 16 wavefronts for large problems,
+//     64x64 with 4 wavefronts (4 workgroups per CU) when 128x128 tiles would
+//     not cover every CU.  Many resident wavefronts per SIMD hide the LDS and
+//     memory latency better than larger per-wave tiles did.
+//   * Both operands are in the packed 16x64 tile layout, so a k-step (64) of
+//     the workgroup tile is (BM + BN)/16 fragments of 1 KiB.  Each wavefront
+//     copies its share with global_load_lds_dwordx4 straight into a 4-stage
+//     LDS ring (lane l lands at slot base + 16*l, the fragment layout),
+//     keeping three k-steps in flight; explicit vmcnt waits and one barrier
+//     per k-step order the ring.  A 32x32x32 operand is the lane slots of two
+//     adjacent 16-row tiles, read with ds_read_b128 as four contiguous
+//     256-byte runs.
+//   * Workgroups are mapped XCD-major: consecutive tiles of the same weight
+//     column block land on the same XCD and share its L2.
 #include "w8a8_internal.h"
 
 namespace w8a8 {
@@ -40,138 +48,166 @@ struct GemmParams {
 };
 
 constexpr int kXcds = 8;
-constexpr int kBMF = 8;  // 16-row fragments per workgroup tile (128 rows)
-constexpr int kBNF = 8;  // 16-col fragments per workgroup tile (128 cols)
+constexpr int kStages = 4;  // LDS ring depth (k-steps in flight)
 
-__device__ inline i32x4 mfma_16x16x64(i32x4 a, i32x4 b, i32x4 c) {
-  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ inline i32x16 mfma_32x32x32(i32x4 a, i32x4 b, i32x16 c) {
+  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
 }
 
-template <int EPI, typename TY, typename TH>
-__global__ __launch_bounds__(256, 2) void gemm_kernel(GemmParams p) {
-  __shared__ i32x4 lds[2][kBMF + kBNF][64];
+// Waits until at most n of this wave's vector-memory loads (the LDS-DMA
+// fragment copies) are outstanding.  gfx9 s_waitcnt: vmcnt in bits [3:0] and
+// [15:14], expcnt [6:4] and lgkmcnt [11:8] left at their maxima.
+template <int n>
+__device__ inline void wait_vmcnt() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier for the LDS ring.  The wave's own LDS reads complete
+// first (lgkmcnt(0)), so a later LDS-DMA write into the slot they read cannot
+// overtake them; unlike __syncthreads it does not drain outstanding loads.
+__device__ inline void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// WM x WN wavefronts, each owning one 32x32 block (BM = 32 WM, BN = 32 WN).
+template <int WM, int WN, int OCC, int EPI, typename TY, typename TH>
+__global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_kernel(GemmParams p) {
+  constexpr int NW = WM * WN;
+  constexpr int BMF = 2 * WM;  // 16-row activation tiles per k-step
+  constexpr int BNF = 2 * WN;  // 16-row weight tiles per k-step
+  constexpr int F = BMF + BNF;
+  constexpr int LPW = F / NW;  // fragment copies per wave per k-step
+  static_assert(F % NW == 0, "fragments must split evenly over the wavefronts");
+  __shared__ i32x4 lds[kStages][F][64];
 
   // XCD-major tile mapping: workgroup b runs on XCD b % 8.
   const int b = blockIdx.x;
   const int tile = (b % kXcds) * p.per_xcd + b / kXcds;
   if (tile >= p.tiles) return;
-  const int tm = tile % p.tiles_m;
-  const int tn = tile / p.tiles_m;
-  const int mb0 = tm * kBMF;
-  const int nb0 = tn * kBNF;
+  const int mb0 = (tile % p.tiles_m) * BMF;
+  const int nb0 = (tile / p.tiles_m) * BNF;
 
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = tid >> 6;
-  const int wm = wave >> 1;
-  const int wn = wave & 1;
-  const int li = lane & 15;
-  const int lg = lane >> 4;
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
   const int KB = p.KB;
 
-  // Fragment f = 4q + wave of each k-step: f < 8 are activation blocks
-  // mb0 + f, f >= 8 weight blocks nb0 + f - 8.
-  const i32x4* src[4];
-  bool ok[4];
+  // Fragment f = q*NW + wave of each k-step: f < BMF are activation blocks
+  // mb0 + f, the rest weight blocks nb0 + f - BMF.  Blocks past the operand
+  // are clamped to its last block: their products only reach accumulator
+  // rows or columns that the epilogue never stores.
+  const i32x4* src[LPW];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int f = 4 * q + wave;
-    if (f < kBMF) {
-      ok[q] = mb0 + f < p.MB;
-      src[q] = p.a + static_cast<int64_t>(ok[q] ? mb0 + f : 0) * KB * 64 + lane;
+  for (int q = 0; q < LPW; ++q) {
+    const int f = q * NW + wave;
+    if (f < BMF) {
+      src[q] = p.a + static_cast<int64_t>(min(mb0 + f, p.MB - 1)) * KB * 64 + lane;
     } else {
-      ok[q] = nb0 + f - kBMF < p.NB;
-      src[q] = p.w + static_cast<int64_t>(ok[q] ? nb0 + f - kBMF : 0) * KB * 64 + lane;
+      src[q] = p.w + static_cast<int64_t>(min(nb0 + f - BMF, p.NB - 1)) * KB * 64 + lane;
     }
   }
+  auto issue = [&](int kb, int slot) {
+#pragma unroll
+    for (int q = 0; q < LPW; ++q)
+      __builtin_amdgcn_global_load_lds(
+          static_cast<const void*>(src[q] + static_cast<int64_t>(kb) * 64),
+          (lds_void*)(&lds[slot][q * NW + wave][0]), 16, 0, 0);
+  };
 
-  i32x4 acc[4][4];
+  i32x16 acc;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+  for (int r = 0; r < 16; ++r) acc[r] = 0;
 
-  i32x4 st[4];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) st[q] = (ok[q] && KB > 0) ? src[q][0] : i32x4{0, 0, 0, 0};
-#pragma unroll
-  for (int q = 0; q < 4; ++q) lds[0][4 * q + wave][lane] = st[q];
-  __syncthreads();
+  for (int s = 0; s < kStages - 1; ++s)
+    if (s < KB) issue(s, s);
 
+  // 32x32x32 operands of k-half h: lane l takes 16 bytes of row l%32 of a
+  // 16-row tile pair at k 32h + 16(l/32): slot (l%16) + 16(2h + l/32) of
+  // tile (l%32)/16.
+  const int fhalf = (lane >> 4) & 1;
   for (int kb = 0; kb < KB; ++kb) {
-    const int cur = kb & 1;
-    const bool more = kb + 1 < KB;
-    if (more) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q)
-        st[q] = ok[q] ? src[q][static_cast<int64_t>(kb + 1) * 64] : i32x4{0, 0, 0, 0};
+    // Stage kb has landed once only the later stages' loads may remain.
+    if (kb + kStages - 2 < KB) {
+      wait_vmcnt<LPW * (kStages - 2)>();
+    } else {
+      wait_vmcnt<0>();
     }
-    i32x4 af[4], bf[4];
+    ring_barrier();
+    // Every wave has finished reading the slot of stage kb-1: refill it.
+    if (kb + kStages - 1 < KB) issue(kb + kStages - 1, (kb + kStages - 1) % kStages);
+    const int slot = kb % kStages;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) af[i] = lds[cur][wm * 4 + i][lane];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) bf[j] = lds[cur][kBMF + wn * 4 + j][lane];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][j] = mfma_16x16x64(af[i], bf[j], acc[i][j]);
-    if (more) {
-#pragma unroll
-      for (int q = 0; q < 4; ++q) lds[cur ^ 1][4 * q + wave][lane] = st[q];
+    for (int h = 0; h < 2; ++h) {
+      const int fslot = (lane & 15) + 16 * (2 * h + (lane >> 5));
+      const i32x4 af = lds[slot][2 * wm + fhalf][fslot];
+      const i32x4 bf = lds[slot][BMF + 2 * wn + fhalf][fslot];
+      acc = mfma_32x32x32(af, bf, acc);
     }
-    __syncthreads();
   }
 
-  // Epilogue.  Fragment (i, j), register r: row (mb0 + 4wm + i)*16 + 4lg + r,
-  // column (nb0 + 4wn + j)*16 + li.
+  // Epilogue.  Register r of lane l holds row (mb0 + 2wm)*16 + 8(r/4) +
+  // 4(l/32) + r%4 and column (nb0 + 2wn)*16 + l%32.
+  const int64_t n = static_cast<int64_t>(nb0 + 2 * wn) * 16 + (lane & 31);
+  const bool n_ok = n < p.N;
+  float swn = 0.0f;
+  if constexpr (EPI != kEpiI32) swn = n_ok ? p.sw[n] : 0.0f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int64_t n = static_cast<int64_t>(nb0 + wn * 4 + j) * 16 + li;
-    const bool n_ok = n < p.N;
-    float swn = 0.0f;
-    if constexpr (EPI != kEpiI32) swn = n_ok ? p.sw[n] : 0.0f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int m = (mb0 + wm * 4 + i) * 16 + 4 * lg + r;
-        const bool m_ok = m < p.M;
-        if constexpr (EPI == kEpiI32) {
-          if (m_ok && n_ok) static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] = acc[i][j][r];
-        } else if constexpr (EPI == kEpiDequant) {
-          if (m_ok && n_ok) {
-            static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
-                from_f32<TY>(dequant1(acc[i][j][r], p.sx[m], swn, p.bias, n));
-          }
+  for (int r = 0; r < 16; ++r) {
+    const int m = (mb0 + 2 * wm) * 16 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+    const bool m_ok = m < p.M;
+    const int32_t a = acc[r];
+    if constexpr (EPI == kEpiI32) {
+      if (m_ok && n_ok) static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] = a;
+    } else if constexpr (EPI == kEpiDequant) {
+      if (m_ok && n_ok) {
+        static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
+            from_f32<TY>(dequant1(a, p.sx[m], swn, p.bias, n));
+      }
+    } else {
+      // Interleaved gate/up: even column = gate, odd column = up of output
+      // n / 2.  Every lane dequantizes its own column; the even lane takes
+      // the up value from its odd neighbour.
+      const float sxm = m_ok ? p.sx[m] : 0.0f;
+      const float v =
+          (m_ok && n_ok) ? to_f32(from_f32<TH>(dequant1(a, sxm, swn, p.bias, n))) : 0.0f;
+      const float u = __shfl_xor(v, 1);
+      if ((lane & 1) == 0 && m_ok && n_ok) {
+        const TH h = from_f32<TH>(silu_mul<TH>(v, u));
+        TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n / 2;
+        if constexpr (EPI == kEpiSilu) {
+          *y = h;
         } else {
-          // Interleaved gate/up: even column = gate, odd column = up of
-          // output n / 2.  Every lane dequantizes its own column; the even
-          // lane takes the up value from its odd neighbour.
-          const float sxm = m_ok ? p.sx[m] : 0.0f;
-          const float v = (m_ok && n_ok) ? to_f32(from_f32<TH>(dequant1(acc[i][j][r], sxm, swn,
-                                                                        p.bias, n)))
-                                         : 0.0f;
-          const float u = __shfl_xor(v, 1);
-          if ((li & 1) == 0 && m_ok && n_ok) {
-            const TH h = from_f32<TH>(silu_mul<TH>(v, u));
-            TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n / 2;
-            if constexpr (EPI == kEpiSilu) {
-              *y = h;
-            } else {
-              *y = static_cast<int8_t>(quant1(to_f32(h), p.out_scale));
-            }
-          }
+          *y = static_cast<int8_t>(quant1(to_f32(h), p.out_scale));
         }
       }
     }
   }
 }
 
+// Launches one tile configuration for the problem in p (tile counts are
+// filled in here).
+template <int WM, int WN, int OCC, int EPI, typename TY, typename TH>
+hipError_t launch_cfg(GemmParams p, hipStream_t st) {
+  p.tiles_m = static_cast<int>(ceil_div(p.MB, 2 * WM));
+  const int tiles_n = static_cast<int>(ceil_div(p.NB, 2 * WN));
+  p.tiles = p.tiles_m * tiles_n;
+  p.per_xcd = static_cast<int>(ceil_div(p.tiles, kXcds));
+  if (p.tiles == 0) return hipSuccess;
+  hipLaunchKernelGGL((gemm_kernel<WM, WN, OCC, EPI, TY, TH>), dim3(p.per_xcd * kXcds),
+                     dim3(WM * WN * 64), 0, st, p);
+  return hipGetLastError();
+}
+
+// 128x128 tiles (16 waves) when they cover every CU, else 64x64 (4 waves).
 template <int EPI, typename TY, typename TH>
 hipError_t launch_t(const GemmParams& p, hipStream_t st) {
-  const int grid = p.per_xcd * kXcds;
-  hipLaunchKernelGGL((gemm_kernel<EPI, TY, TH>), dim3(grid), dim3(256), 0, st, p);
-  return hipGetLastError();
+  const int64_t big_tiles = ceil_div(p.MB, 8) * ceil_div(p.NB, 8);
+  if (big_tiles >= 256) return launch_cfg<4, 4, 2, EPI, TY, TH>(p, st);
+  return launch_cfg<2, 2, 4, EPI, TY, TH>(p, st);
 }
 
 }  // namespace
@@ -191,11 +227,8 @@ hipError_t launch_gemm(const LinearOperands& op, hipStream_t st) {
   p.MB = static_cast<int>(ceil_div(op.M, kTileRows));
   p.NB = static_cast<int>(ceil_div(op.N, kTileRows));
   p.KB = static_cast<int>(ceil_div(op.K, kTileK));
-  p.tiles_m = static_cast<int>(ceil_div(p.MB, kBMF));
-  const int tiles_n = static_cast<int>(ceil_div(p.NB, kBNF));
-  p.tiles = p.tiles_m * tiles_n;
-  p.per_xcd = static_cast<int>(ceil_div(p.tiles, kXcds));
-  if (p.tiles == 0) return hipSuccess;
+  p.tiles_m = p.tiles = p.per_xcd = 0;
+  if (p.MB == 0 || p.NB == 0) return hipSuccess;
   switch (op.epi) {
     case kEpiI32:
       return launch_t<kEpiI32, int32_t, float>(p, st);

@@ -292,8 +292,12 @@ hipError_t dispatch_f(const FusedParams& p, int epi, int y_dtype, int h_dtype, h
 
 }  // namespace
 
+// Used for single-row decode only: measured on MI355X, quantizing x once per
+// CU in this persistent kernel beats the separate quantization launch at
+// M = 1, but its per-CU quantization work (M*K elements) and per-block
+// barriers make it slower than quantize + gemv_kernel from M = 4 up.
 bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K) {
-  return (x_dtype == kF16 || x_dtype == kBF16) && M >= 1 && M <= kFusedMaxRows && K >= 8 &&
+  return (x_dtype == kF16 || x_dtype == kBF16) && M == 1 && K >= 8 &&
          K % 8 == 0 && ceil_div(K, kTileK) <= kFusedMaxKB && ldx % 8 == 0 &&
          (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
 }

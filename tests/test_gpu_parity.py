@@ -186,6 +186,18 @@ def test_gemm_i32_exact(cuda, m, n, k):
     np.testing.assert_array_equal(acc.cpu().numpy(), O.int32_matmul_f64(a.numpy(), w.numpy()))
 
 
+@pytest.mark.parametrize("m,n,k", [(300, 11000, 200), (129, 16400, 4096), (1000, 2050, 576)])
+def test_gemm_large_tile_config_ragged(cuda, m, n, k):
+    """Shapes that select the 128x128 / 16-wave GEMM tile with ragged M, N, K."""
+    from nanopointllm_amd import w8a8
+
+    a = rand_i8((m, k), m + 5)
+    w = rand_i8((n, k), n + 7)
+    note(f"gemm large tile m={m} n={n} k={k}")
+    acc = w8a8.gemm_i32(a.to(cuda), w8a8.pack_rows(w.to(cuda)), n)
+    np.testing.assert_array_equal(acc.cpu().numpy(), O.int32_matmul_f64(a.numpy(), w.numpy()))
+
+
 def test_gemm_i32_extreme_values(cuda):
     from nanopointllm_amd import w8a8
 
