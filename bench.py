@@ -36,6 +36,10 @@ for p in (ROOT, ROOT / "nano-pointllm_amd"):
 
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
+# Per-launch HBM traffic of the gate/up GEMV, from rocprofv3 FETCH_SIZE /
+# WRITE_SIZE runs of `bench.py --profile-gateup`, scaled by a copy kernel.
+TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_gateup_m8_traffic.json"
+CALIBRATION_COPY_BYTES = 256 << 20
 
 
 def log(msg: str) -> None:
@@ -52,6 +56,9 @@ def parse_args():
     ap.add_argument("--no-extra", action="store_true", help="skip the per-projection sweeps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU sample")
+    ap.add_argument("--profile-gateup", action="store_true",
+                    help="only the counter-calibration copy and the gate/up GEMV loop "
+                         "(the region rocprofv3 --pmc runs measure)")
     return ap.parse_args()
 
 
@@ -160,8 +167,13 @@ def gateup_kernel_roofline(layers, m: int, device) -> dict:
     ms = event_time_ms(run_all, reps) / len(args)
     nbytes = W.algorithmic_bytes(m, spec.n, spec.k, silu=True, int8_in=True)
     achieved = nbytes / (ms * 1e-3) / 1e9
+    traffic = None
+    if TRAFFIC_SUMMARY.exists():
+        t = json.loads(TRAFFIC_SUMMARY.read_text())
+        if t.get("m") == m:
+            traffic = t["hbm_bytes_per_launch"]
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
             "kernel": "gemv_kernel (packed gate/up, SiLU*mul epilogue, int8 in)",
             "avg_launch_us": round(ms * 1e3, 3), "algorithmic_bytes_per_launch": nbytes}
 
@@ -239,6 +251,94 @@ def prefill_sweep(layers, device, m: int = 560) -> dict:
     return out
 
 
+def prefill_sweep_all(layers, device) -> dict:
+    return {f"M{m}": prefill_sweep(layers, device, m) for m in (560, 768, 1024)}
+
+
+def qkv_m_sweep(layers, device, ms_list=(1, 2, 4, 16, 64, 256, 2048)) -> dict:
+    """GEMV -> MFMA crossover on the packed QKV shape (fused linear, fp16 in)."""
+    from nanopointllm_amd import w8a8, workloads as W
+
+    spec = {p.name: p for p in W.PROJECTIONS}["qkv"]
+    sub = layers[:8]
+    out = {}
+    for m in ms_list:
+        x16 = (W.decode_activations(m, spec.k, seed=13) if m <= 16
+               else W.prefill_activations(m, spec.k, seed=13)).to(device)
+
+        def run(x16=x16):
+            for layer in sub:
+                p = layer.weights["qkv"]
+                w8a8.linear_dynamic(x16, p.packed, p.scale, None, p.out_features)
+
+        ms, g = time_graph(run, steps=10, warmup=3)
+        del g
+        per = ms / len(sub)
+        nbytes = W.algorithmic_bytes(m, spec.n, spec.k)
+        out[f"M{m}"] = {"us": round(per * 1e3, 2),
+                        "GBps": round(nbytes / (per * 1e-3) / 1e9, 1),
+                        "TOPS": round(W.algorithmic_ops(m, spec.n, spec.k) / (per * 1e-3) / 1e12, 1)}
+    return out
+
+
+def mixed_chain(layers, device, h_scale_m: int = 567) -> dict:
+    """7 decode rows + a 560-row prefill chunk (M=567): gate/up + SiLU*mul + int8
+    requant (static scale) -> int8-in down projection."""
+    import torch
+
+    from nanopointllm_amd import _lib, w8a8, workloads as W
+
+    m = h_scale_m
+    x = torch.cat([W.decode_activations(7, W.HIDDEN, seed=21),
+                   W.prefill_activations(560, W.HIDDEN, seed=22)]).to(device)
+    sub = layers[:8]
+    gu0 = sub[0].weights["gateup"]
+    h = w8a8.linear_dynamic(x, gu0.packed, gu0.scale, None, gu0.out_features,
+                            epilogue=_lib.EPI_SILU_MUL)
+    from nanopointllm_amd.w8a8 import static_activation_scale
+
+    h_scale = float(static_activation_scale(h.abs().max(), device=device))
+    s_rows = torch.full((m,), h_scale, dtype=torch.float32, device=device)
+
+    def run():
+        for layer in sub:
+            gu, dn = layer.weights["gateup"], layer.weights["down"]
+            hq = w8a8.linear_dynamic(x, gu.packed, gu.scale, None, gu.out_features,
+                                     epilogue=_lib.EPI_SILU_MUL_Q8, y_scale=h_scale)
+            w8a8.linear_i8in(hq, s_rows, dn.packed, dn.scale, None, dn.out_features,
+                             out_dtype=torch.float16)
+
+    ms, g = time_graph(run, steps=10, warmup=3)
+    del g
+    per = ms / len(sub)
+    ops = W.algorithmic_ops(m, 2 * W.INTERMEDIATE, W.HIDDEN) + W.algorithmic_ops(m, W.HIDDEN, W.INTERMEDIATE)
+    return {"M": m, "us_per_layer": round(per * 1e3, 2),
+            "TOPS": round(ops / (per * 1e-3) / 1e12, 1), "h_scale": h_scale}
+
+
+def stack_with_lm_head(layers, m: int, device) -> dict:
+    """The 32-layer W8A8 stack plus the fp16 LM head [32003 x 4096] (torch
+    F.linear: the LM head is not a W8A8 linear)."""
+    import torch
+
+    from nanopointllm_amd import workloads as W
+
+    g = torch.Generator(device=device)
+    g.manual_seed(99)
+    lm = (torch.randn(W.VOCAB, W.HIDDEN, generator=g, device=device) * 0.02).to(torch.float16)
+    xh = W.decode_activations(m, W.HIDDEN, seed=98).to(device)
+
+    def step():
+        for layer in layers:
+            layer.step()
+        torch.nn.functional.linear(xh, lm)
+
+    ms, gr = time_graph(step, steps=10, warmup=3)
+    del gr
+    nbytes = step_bytes(m, len(layers)) + W.VOCAB * W.HIDDEN * 2 + 2 * m * W.HIDDEN + 2 * m * W.VOCAB
+    return {"ms": round(ms, 4), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes}
+
+
 def cpu_baseline(layers, m: int, n_layers: int) -> dict:
     """Reference CPU integer path (numpy restatement) on `n_layers` layers."""
     import numpy as np
@@ -298,6 +398,16 @@ def main() -> int:
     m = args.m
     log(f"building {args.layers} layers of packed W8A8 weights (M={m})")
     layers = [Layer(i, m, device) for i in range(args.layers)]
+    if args.profile_gateup:
+        # Counter calibration: a plain device copy of known size, then the
+        # gate/up GEMV loop timed by the roofline measurement.
+        src = torch.empty(CALIBRATION_COPY_BYTES, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        roof = gateup_kernel_roofline(layers, m, device)
+        print(json.dumps({"profile_gateup": roof, "calibration_copy_bytes": CALIBRATION_COPY_BYTES}))
+        return 0
 
     def step():
         for layer in layers:
@@ -318,8 +428,14 @@ def main() -> int:
     if not args.no_extra:
         log("decode sweep M=1,4,8")
         extra["decode_per_projection"] = projection_sweep(layers, device)
-        log("prefill sweep M=560")
-        extra["prefill_M560"] = prefill_sweep(layers, device)
+        log("prefill sweep M=560,768,1024")
+        extra["prefill"] = prefill_sweep_all(layers, device)
+        log("QKV M sweep")
+        extra["qkv_m_sweep"] = qkv_m_sweep(layers, device)
+        log("mixed M=567 int8 chain")
+        extra["mixed_567_gateup_down_int8_chain"] = mixed_chain(layers, device)
+        log("stack + fp16 LM head")
+        extra["stack_with_fp16_lm_head"] = stack_with_lm_head(layers, m, device)
 
     cpu = None
     if not args.no_cpu:

@@ -91,3 +91,20 @@ def test_cpu_tensors_are_rejected_not_computed():
 
     with pytest.raises(RuntimeError, match="only on the GPU"):
         w8a8.quant_rows(torch.ones(2, 8, dtype=torch.float16))
+
+
+def test_injection_requires_gpu_weights():
+    import torch.nn as nn
+
+    from nanopointllm_amd.inject import inject_w8a8
+
+    model = nn.Module()
+    model.model = nn.Module()
+    layer = nn.Module()
+    layer.mlp = nn.Module()
+    layer.mlp.gate_proj = nn.Linear(8, 8)
+    layer.mlp.up_proj = nn.Linear(8, 8)
+    layer.mlp.down_proj = nn.Linear(8, 8)
+    model.model.layers = nn.ModuleList([layer])
+    with pytest.raises(RuntimeError, match="only on the GPU"):
+        inject_w8a8(model)
