@@ -6,17 +6,22 @@
 // llama/lightweight_runner.py:38-54, 329-379).
 //
 // Design: a persistent grid of one 16-wavefront workgroup per CU.
-//   1. Each wavefront issues its first weight loads (they do not depend on x).
-//   2. While they are in flight the workgroup quantizes all M rows of x into
+//   1. Each thread loads its x chunks and one epilogue operand (a weight scale
+//      or bias of this workgroup's output blocks, kept in LDS), then each
+//      wavefront issues its first weight loads (they do not depend on x).
+//   2. While those are in flight the workgroup quantizes all M rows of x into
 //      LDS (row absmax on the raw 16-bit patterns, binary16 scale, the
 //      division-free exact quantizer), laid out as half MFMA A fragments:
 //      8 rows x 64 K per k-block, so lane (i, g) reads row i, k 16g..16g+15
 //      with one conflict-free ds_read_b128.
 //   3. Workgroup b then streams 16-output weight blocks b, b+G, b+2G, ...; its
-//      16 wavefronts split K, each keeping two chunks of CH 1 KiB fragments in
-//      flight across block boundaries.  Per block, the per-wave 16x16 int32
-//      partials go through one of two LDS buffers, one barrier, and the fused
-//      epilogue (dequant / SiLU*mul / int8 requant) of the GEMV.
+//      16 wavefronts split K.  Each keeps two steps of CH 1 KiB fragments in
+//      flight in a three-buffer register ring that runs across block
+//      boundaries; loads are raw buffer loads whose descriptor range ends at
+//      the wave's last k-block, so the ring never reads past its share.  Per
+//      block, the per-wave 16x16 int32 partials go through one of two LDS
+//      buffers, one barrier (LDS counter only: the ring keeps streaming), and
+//      the fused epilogue (dequant / SiLU*mul / int8 requant).
 // Quantizing x once per CU costs M*K*~10 VALU ops per CU; for decode shapes
 // that hides behind the weight loads already in flight, and it saves the
 // separate quantization launch and its round trip through memory.
@@ -29,8 +34,16 @@ namespace {
 constexpr int kFusedWaves = 16;
 constexpr int kFusedThreads = kFusedWaves * 64;
 constexpr int kFusedCH = 4;
+// Raw buffer loads: descriptor word 3 of gfx9 (32-bit data format), the
+// nontemporal cache policy and the bytes of one 16 x 64 packed k-block.
+constexpr int kBufferWord3 = 0x00020000;
+constexpr int kCacheNT = 2;
+constexpr int kBlockBytes = 1024;
+constexpr int kFusedRing = 3;  // register buffers (the main loop is unrolled by 3)
 constexpr int kFusedMaxRows = 8;
 constexpr int kFusedMaxKB = 192;  // K <= 12288
+constexpr int kFusedMaxBlocks = 64;  // 16-row output blocks per workgroup
+static_assert(kFusedMaxBlocks * 16 == kFusedThreads, "one epilogue operand per thread");
 // Max 16-byte x chunks a thread holds during quantization (1 row: 12288/8/1024).
 constexpr int kFusedMaxChunks = 12;
 
@@ -67,6 +80,62 @@ __device__ inline float bits_to_f32(uint32_t b16) {
   return to_f32(__builtin_bit_cast(TX, static_cast<uint16_t>(b16)));
 }
 
+// Sums the per-wave partials of output block nb and writes its outputs.
+// `ops` holds the block's 16 weight scales followed by its 16 biases.
+template <int EPI, typename TY, typename TH>
+__device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
+                                const float* row_s, int64_t nb, int tid, const float* ops) {
+  const bool has_bias = p.bias != nullptr;
+  const int M = p.M;
+  if constexpr (EPI == kEpiI32 || EPI == kEpiDequant) {
+    if (tid < 256) {
+      const int m = tid >> 4;
+      const int64_t n = nb * 16 + (tid & 15);
+      if (m < M && n < p.N) {
+        int32_t s = 0;
+#pragma unroll
+        for (int w = 0; w < kFusedWaves; ++w) s += red[w][tid];
+        TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n;
+        if constexpr (EPI == kEpiI32) {
+          *y = s;
+        } else {
+          const int r = tid & 15;
+          *y = from_f32<TY>(dequant1b(s, row_s[m], ops[r], has_bias, ops[16 + r]));
+        }
+      }
+    }
+  } else {
+    // Interleaved gate/up: packed rows 2c (gate) and 2c+1 (up) of the block
+    // produce output column nb*8 + c.
+    if (tid < 128) {
+      const int m = tid >> 3;
+      const int cc = tid & 7;
+      const int64_t n_out = nb * 8 + cc;
+      if (m < M && n_out < p.N / 2) {
+        const int base = m * 16 + 2 * cc;
+        int32_t sg = 0, su = 0;
+#pragma unroll
+        for (int w = 0; w < kFusedWaves; ++w) {
+          sg += red[w][base];
+          su += red[w][base + 1];
+        }
+        const float sxm = row_s[m];
+        const float g = to_f32(from_f32<TH>(dequant1b(sg, sxm, ops[2 * cc], has_bias,
+                                                      ops[16 + 2 * cc])));
+        const float u = to_f32(from_f32<TH>(dequant1b(su, sxm, ops[2 * cc + 1], has_bias,
+                                                      ops[17 + 2 * cc])));
+        const TH h = from_f32<TH>(silu_mul<TH>(g, u));
+        TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n_out;
+        if constexpr (EPI == kEpiSilu) {
+          *y = h;
+        } else {
+          *y = static_cast<int8_t>(quant1(to_f32(h), p.out_scale));
+        }
+      }
+    }
+  }
+}
+
 template <int EPI, typename TX, typename TY, typename TH>
 __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p) {
   // A fragments: [kb][g][row < 8][16 bytes]
@@ -74,10 +143,12 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   __shared__ int32_t red[2][kFusedWaves][256];
   __shared__ uint32_t amax_w[kFusedWaves];
   __shared__ float row_s[kFusedMaxRows];
+  __shared__ float ops_lds[kFusedMaxBlocks * 32];  // per block: 16 scales, 16 biases
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  // Wave-uniform, so the step bookkeeping below stays in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int li = lane & 15;
   const int lg = lane >> 4;
   const int KB = p.KB;
@@ -87,24 +158,46 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   const int kbw = (KB + kFusedWaves - 1) / kFusedWaves;
   const int kb0 = min(wave * kbw, KB);
   const int kb1 = min(kb0 + kbw, KB);
-  const bool has_range = kb0 < kb1;
   const int nch = (kbw + kFusedCH - 1) / kFusedCH;
   const int n_mine = (p.NB - static_cast<int>(blockIdx.x) + p.G - 1) / p.G;
   const int total = n_mine * nch;
 
-  auto load = [&](i32x4(&buf)[kFusedCH], int j, int c) {
-    const int64_t nb = static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(j) * p.G;
-    const i32x4* base = p.w + nb * KB * 64 + lane;
+  // The wave's work is a sequence of `total` steps; step (j, c) covers chunk
+  // c (CH k-blocks of the wave's range) of its j-th weight block.  Steps are
+  // loaded kFusedRing - 1 ahead into a ring of register buffers that the
+  // unrolled main loop rotates by name, so no buffer is ever copied (a copy
+  // would wait for every load in flight).
+  // Every step issues its loads unconditionally, so the compiler's load
+  // counting stays exact and it never drains the ring.  Weights are read
+  // with buffer loads over the block's packed tile column whose range ends at
+  // the wave's last k-block (and is empty for a step past the end): the loads
+  // beyond it return zeros without a memory access.
+  int lj = 0, lc = 0;  // next step to load
+  auto issue = [&](i32x4(&buf)[kFusedCH]) {
+    const bool past = lj >= n_mine;
+    // The cursor is wave-uniform; say so, or the descriptor would be built in
+    // vector registers and every load would become a loop over lanes.
+    const int sj = __builtin_amdgcn_readfirstlane(past ? n_mine - 1 : lj);
+    const int nrec = __builtin_amdgcn_readfirstlane(past ? 0 : kb1 * kBlockBytes);
+    const int64_t nb = static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(sj) * p.G;
+    // A wave without a range has kb0 = kb1 = KB: all its loads are beyond.
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<i32x4*>(p.w + nb * KB * 64), 0, nrec, kBufferWord3);
 #pragma unroll
     for (int i = 0; i < kFusedCH; ++i) {
-      int kb = kb0 + c * kFusedCH + i;
-      kb = kb < kb1 ? kb : kb1 - 1;
-      buf[i] = __builtin_nontemporal_load(base + static_cast<int64_t>(kb) * 64);
+      const int off = (kb0 + lc * kFusedCH + i) * kBlockBytes + lane * 16;
+      buf[i] = __builtin_bit_cast(i32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, off, 0,
+                                                                               kCacheNT));
     }
+    // Branch-free update: a store under a branch here would keep the cursor
+    // in scratch memory.
+    const int nc = lc + 1;
+    const bool wrap = nc == nch;
+    lj += wrap ? 1 : 0;
+    lc = wrap ? 0 : nc;
   };
 
-  i32x4 cur[kFusedCH], nxt[kFusedCH];
-  if (has_range && total > 0) load(cur, 0, 0);
+  i32x4 r0[kFusedCH], r1[kFusedCH], r2[kFusedCH];
 
   // ---------------------------------------------------------- quantize x
   // Rows are spread over power-of-two groups of TPR >= 128 threads.
@@ -117,7 +210,6 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   const uint16_t* xr =
       static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(row_live ? row : 0) * p.ldx;
   u32x4 raw[kFusedMaxChunks];
-  uint32_t am = 0;
 #pragma unroll
   for (int i = 0; i < kFusedMaxChunks; ++i) {
     const int c = j0 + i * tpr;
@@ -126,6 +218,33 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
     } else {
       raw[i] = u32x4{0u, 0u, 0u, 0u};
     }
+  }
+  // The epilogue operands of all this workgroup's blocks (n_mine <= 64, one
+  // per thread) go to LDS up front: vmcnt counts loads in issue order, so a
+  // scale loaded at epilogue time would wait for every weight load in flight.
+  float op_s = 0.0f, op_b = 0.0f;
+  const int op_j = tid >> 4;
+  if constexpr (EPI != kEpiI32) {
+    const int64_t n =
+        (static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(op_j) * p.G) * 16 + (tid & 15);
+    if (op_j < n_mine && n < p.N) {
+      op_s = p.sw[n];
+      if (p.bias != nullptr) op_b = p.bias[n];
+    }
+  }
+  // The first weight loads go out after x and the operands (which they do not
+  // depend on), so they stream while x is quantized.
+  issue(r0);
+  issue(r1);
+  if constexpr (EPI != kEpiI32) {
+    if (op_j < n_mine) {
+      ops_lds[op_j * 32 + (tid & 15)] = op_s;
+      ops_lds[op_j * 32 + 16 + (tid & 15)] = op_b;
+    }
+  }
+  uint32_t am = 0;
+#pragma unroll
+  for (int i = 0; i < kFusedMaxChunks; ++i) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) am = max(am, max(abs_lo(raw[i][q]), abs_hi(raw[i][q])));
   }
@@ -168,81 +287,39 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   const bool a_live = li < M;
   const int a_off = (lg * 8 + li) * 16;
   i32x4 acc = i32x4{0, 0, 0, 0};
-  int j = 0, c = 0;
-  for (int step = 0; step < total; ++step) {
-    int jn = j, cn = c + 1;
-    if (cn == nch) {
-      cn = 0;
-      jn = j + 1;
-    }
-    if (has_range && step + 1 < total) load(nxt, jn, cn);
-    if (has_range) {
+  int j = 0, c = 0;  // step being computed
+  auto step = [&](const i32x4(&cur)[kFusedCH], i32x4(&freed)[kFusedCH], int t) {
+    issue(freed);
+    const bool live = t < total;
 #pragma unroll
-      for (int i = 0; i < kFusedCH; ++i) {
-        const int kb = kb0 + c * kFusedCH + i;
-        if (kb < kb1) {
-          const i32x4 a = a_live ? *reinterpret_cast<const i32x4*>(a_lds + kb * 512 + a_off)
-                                 : i32x4{0, 0, 0, 0};
-          acc = mfma_16x16x64(a, cur[i], acc);
-        }
+    for (int i = 0; i < kFusedCH; ++i) {
+      const int kb = kb0 + c * kFusedCH + i;
+      if (live && kb < kb1) {
+        const i32x4 a = a_live ? *reinterpret_cast<const i32x4*>(a_lds + kb * 512 + a_off)
+                               : i32x4{0, 0, 0, 0};
+        acc = mfma_16x16x64(a, cur[i], acc);
       }
     }
-    if (cn == 0) {
-      // Block j done: reduce the wave partials and run the epilogue.
+    const bool last = live && c == nch - 1;
+    if (last) {
+      // Block j done: reduce the wave partials and run the epilogue.  The
+      // barrier waits for LDS traffic only, so the weight loads in flight keep
+      // streaming across it.
       const int par = j & 1;
 #pragma unroll
       for (int r = 0; r < 4; ++r) red[par][wave][(4 * lg + r) * 16 + li] = acc[r];
       acc = i32x4{0, 0, 0, 0};
       __syncthreads();
       const int64_t nb = static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(j) * p.G;
-      if constexpr (EPI == kEpiI32 || EPI == kEpiDequant) {
-        if (tid < 256) {
-          const int m = tid >> 4;
-          const int64_t n = nb * 16 + (tid & 15);
-          if (m < M && n < p.N) {
-            int32_t s = 0;
-#pragma unroll
-            for (int w = 0; w < kFusedWaves; ++w) s += red[par][w][tid];
-            TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n;
-            if constexpr (EPI == kEpiI32) {
-              *y = s;
-            } else {
-              *y = from_f32<TY>(dequant1(s, row_s[m], p.sw[n], p.bias, n));
-            }
-          }
-        }
-      } else {
-        if (tid < 128) {
-          const int m = tid >> 3;
-          const int cc = tid & 7;
-          const int64_t n_out = nb * 8 + cc;
-          if (m < M && n_out < p.N / 2) {
-            const int base = m * 16 + 2 * cc;
-            int32_t sg = 0, su = 0;
-#pragma unroll
-            for (int w = 0; w < kFusedWaves; ++w) {
-              sg += red[par][w][base];
-              su += red[par][w][base + 1];
-            }
-            const int64_t ng = nb * 16 + 2 * cc;
-            const float sxm = row_s[m];
-            const float g = to_f32(from_f32<TH>(dequant1(sg, sxm, p.sw[ng], p.bias, ng)));
-            const float u = to_f32(from_f32<TH>(dequant1(su, sxm, p.sw[ng + 1], p.bias, ng + 1)));
-            const TH h = from_f32<TH>(silu_mul<TH>(g, u));
-            TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n_out;
-            if constexpr (EPI == kEpiSilu) {
-              *y = h;
-            } else {
-              *y = static_cast<int8_t>(quant1(to_f32(h), p.out_scale));
-            }
-          }
-        }
-      }
+      epilogue<EPI, TY, TH>(p, red[par], row_s, nb, tid, ops_lds + j * 32);
     }
-#pragma unroll
-    for (int i = 0; i < kFusedCH; ++i) cur[i] = nxt[i];
-    j = jn;
-    c = cn;
+    j += last ? 1 : 0;
+    c = last ? 0 : c + 1;
+  };
+  for (int t = 0; t < total; t += kFusedRing) {
+    step(r0, r2, t);
+    step(r1, r0, t + 1);
+    step(r2, r1, t + 2);
   }
 }
 
@@ -292,14 +369,26 @@ hipError_t dispatch_f(const FusedParams& p, int epi, int y_dtype, int h_dtype, h
 
 }  // namespace
 
-// Used for single-row decode only: measured on MI355X, quantizing x once per
-// CU in this persistent kernel beats the separate quantization launch at
-// M = 1, but its per-CU quantization work (M*K elements) and per-block
-// barriers make it slower than quantize + gemv_kernel from M = 4 up.
-bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K) {
-  return (x_dtype == kF16 || x_dtype == kBF16) && M == 1 && K >= 8 &&
-         K % 8 == 0 && ceil_div(K, kTileK) <= kFusedMaxKB && ldx % 8 == 0 &&
-         (reinterpret_cast<uintptr_t>(x) & 15u) == 0;
+// Decode shapes: up to 8 rows of 16-bit activations, K <= 12288 and at most
+// 64 output blocks per workgroup (N <= 1024 * CUs).  Each CU quantizes all
+// M x K activations (~11 VALU ops per element, ~2.3 us at M = 8, K = 4096),
+// which only pays off while the CU's share of the weights keeps its loads
+// busy for longer: measured on MI355X, the fused kernel beats quantization +
+// gemv_kernel when a CU streams at least 128 KiB of weights and at least 4
+// bytes per activation element it quantizes (LLaMA-7B at M = 8: packed QKV and
+// gate/up fused, O and down not; at M <= 4 only O is not).
+bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
+                          int64_t K) {
+  if (!((x_dtype == kF16 || x_dtype == kBF16) && M >= 1 && M <= kFusedMaxRows && K >= 8 &&
+        K % 8 == 0 && ceil_div(K, kTileK) <= kFusedMaxKB && ldx % 8 == 0 &&
+        (reinterpret_cast<uintptr_t>(x) & 15u) == 0))
+    return false;
+  const int64_t nb = ceil_div(N, kTileRows);
+  const int64_t g = nb < cu_count() ? nb : cu_count();
+  const int64_t blocks_per_cu = ceil_div(nb, g);
+  const int64_t weight_bytes_per_cu = blocks_per_cu * kTileRows * ceil_div(K, kTileK) * kTileK;
+  return blocks_per_cu <= kFusedMaxBlocks && weight_bytes_per_cu >= (128 << 10) &&
+         weight_bytes_per_cu >= 4 * M * K;
 }
 
 hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const LinearOperands& op,

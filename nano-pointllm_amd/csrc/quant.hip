@@ -14,9 +14,10 @@ namespace w8a8 {
 namespace {
 
 constexpr int kQuantThreads = 256;
-// Rows up to kQuantThreads * 8 * kRegChunks elements are held in registers
-// between the absmax pass and the quantize pass (one global read).
-constexpr int kRegChunks = 8;
+// Rows up to kQuantThreads * 8 * REG elements are held in registers between
+// the absmax pass and the quantize pass (one global read); REG (1, 2, 4 or
+// 8 chunks of 8 elements per thread) is the smallest that covers the row.
+constexpr int kRegChunksMax = 8;
 
 // Quantizes one value with the row scale s.  The division-free form needs a
 // 16-bit input and a binary16-representable scale (always true for dynamic
@@ -54,7 +55,7 @@ __device__ inline void store8(int8_t* __restrict__ q, int64_t row, int64_t k0, i
 // row-major int8 row or as the row's slots of the packed tiles.  For packed
 // output the grid covers ceil(rows/16)*16 rows and every row writes all
 // ceil(K/64)*64 columns, so tile padding is zero-filled.
-template <typename TX, bool PACKED, bool DYNAMIC, bool REG>
+template <typename TX, bool PACKED, bool DYNAMIC, int REG>
 __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
     const TX* __restrict__ x, int64_t ldx, int64_t rows, int64_t K, int vec_in,
     const float* __restrict__ scale_in, int64_t scale_stride, int8_t* __restrict__ q,
@@ -67,10 +68,10 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
   const int64_t nchunk_in = (K + 7) / 8;
   const int64_t nchunk_out = PACKED ? KB * 8 : (ncols_out + 7) / 8;
 
-  float v[REG ? kRegChunks : 1][8];
-  if constexpr (REG) {
+  float v[REG > 0 ? REG : 1][8];
+  if constexpr (REG > 0) {
 #pragma unroll
-    for (int c = 0; c < kRegChunks; ++c) {
+    for (int c = 0; c < REG; ++c) {
       const int64_t k0 = (tid + static_cast<int64_t>(c) * kQuantThreads) * 8;
       const int64_t rem = K - k0;
       if (live && rem > 0) {
@@ -85,9 +86,9 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
   float s = 1.0f;
   if constexpr (DYNAMIC) {
     float amax = 0.0f;
-    if constexpr (REG) {
+    if constexpr (REG > 0) {
 #pragma unroll
-      for (int c = 0; c < kRegChunks; ++c)
+      for (int c = 0; c < REG; ++c)
 #pragma unroll
         for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[c][j]));
     } else if (live) {
@@ -114,9 +115,9 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
   const bool fast = DYNAMIC || __half2float(__float2half_rn(s)) == s;
   if (live && tid == 0 && scales_out != nullptr) scales_out[row] = s;
 
-  if constexpr (REG) {
+  if constexpr (REG > 0) {
 #pragma unroll
-    for (int c = 0; c < kRegChunks; ++c) {
+    for (int c = 0; c < REG; ++c) {
       const int64_t chunk = tid + static_cast<int64_t>(c) * kQuantThreads;
       if (chunk < nchunk_out) {
         const int64_t k0 = chunk * 8;
@@ -212,17 +213,37 @@ __global__ __launch_bounds__(256) void pad_rows_kernel(const int8_t* __restrict_
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
+template <typename TX, bool PACKED, bool DYN, int REG>
+void quant_launch_reg(dim3 g, dim3 b, hipStream_t st, const TX* x, int64_t ldx, int64_t rows,
+                      int64_t K, int vec_in, const float* scale_in, int64_t scale_stride,
+                      int8_t* q, int64_t ldq, int64_t ncols_out, int vec_out, int64_t KB,
+                      float* scales_out) {
+  hipLaunchKernelGGL((quant_rows_kernel<TX, PACKED, DYN, REG>), g, b, 0, st, x, ldx, rows, K,
+                     vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+}
+
 template <typename TX, bool PACKED, bool DYN>
-void quant_launch(dim3 g, dim3 b, hipStream_t st, bool reg, const TX* x, int64_t ldx,
+void quant_launch(dim3 g, dim3 b, hipStream_t st, int64_t chunks, const TX* x, int64_t ldx,
                   int64_t rows, int64_t K, int vec_in, const float* scale_in,
                   int64_t scale_stride, int8_t* q, int64_t ldq, int64_t ncols_out, int vec_out,
                   int64_t KB, float* scales_out) {
-  if (reg)
-    hipLaunchKernelGGL((quant_rows_kernel<TX, PACKED, DYN, true>), g, b, 0, st, x, ldx, rows, K,
-                       vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+  const int64_t per = ceil_div(chunks, kQuantThreads);
+  if (per <= 1)
+    quant_launch_reg<TX, PACKED, DYN, 1>(g, b, st, x, ldx, rows, K, vec_in, scale_in,
+                                         scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+  else if (per <= 2)
+    quant_launch_reg<TX, PACKED, DYN, 2>(g, b, st, x, ldx, rows, K, vec_in, scale_in,
+                                         scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+  else if (per <= 4)
+    quant_launch_reg<TX, PACKED, DYN, 4>(g, b, st, x, ldx, rows, K, vec_in, scale_in,
+                                         scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+  else if (per <= kRegChunksMax)
+    quant_launch_reg<TX, PACKED, DYN, kRegChunksMax>(g, b, st, x, ldx, rows, K, vec_in, scale_in,
+                                                     scale_stride, q, ldq, ncols_out, vec_out,
+                                                     KB, scales_out);
   else
-    hipLaunchKernelGGL((quant_rows_kernel<TX, PACKED, DYN, false>), g, b, 0, st, x, ldx, rows, K,
-                       vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+    quant_launch_reg<TX, PACKED, DYN, 0>(g, b, st, x, ldx, rows, K, vec_in, scale_in,
+                                         scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
 }
 
 template <typename TX>
@@ -235,22 +256,21 @@ hipError_t quant_dispatch(const TX* x, int64_t ldx, int64_t rows, int64_t K,
   const int64_t grid = packed ? ceil_div(rows, kTileRows) * kTileRows : rows;
   if (grid == 0) return hipSuccess;
   const int64_t chunks = packed ? KB * 8 : ceil_div(ncols_out > K ? ncols_out : K, 8);
-  const bool reg = chunks <= static_cast<int64_t>(kQuantThreads) * kRegChunks;
   const bool dyn = scale_in == nullptr;
   dim3 g(static_cast<unsigned>(grid)), b(kQuantThreads);
   if (packed) {
     if (dyn)
-      quant_launch<TX, true, true>(g, b, st, reg, x, ldx, rows, K, vec_in, scale_in,
+      quant_launch<TX, true, true>(g, b, st, chunks, x, ldx, rows, K, vec_in, scale_in,
                                    scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
     else
-      quant_launch<TX, true, false>(g, b, st, reg, x, ldx, rows, K, vec_in, scale_in,
+      quant_launch<TX, true, false>(g, b, st, chunks, x, ldx, rows, K, vec_in, scale_in,
                                     scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
   } else {
     if (dyn)
-      quant_launch<TX, false, true>(g, b, st, reg, x, ldx, rows, K, vec_in, scale_in,
+      quant_launch<TX, false, true>(g, b, st, chunks, x, ldx, rows, K, vec_in, scale_in,
                                     scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
     else
-      quant_launch<TX, false, false>(g, b, st, reg, x, ldx, rows, K, vec_in, scale_in,
+      quant_launch<TX, false, false>(g, b, st, chunks, x, ldx, rows, K, vec_in, scale_in,
                                      scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
   }
   return hipGetLastError();

@@ -133,6 +133,16 @@ __device__ inline uint32_t pack4_i8(int32_t a, int32_t b, int32_t c, int32_t d) 
 }
 
 // Dequant epilogue (w8a8.py:134-137): three separate binary32 roundings.
+// dequant1 with the bias value already loaded (added only when present, so a
+// zero result keeps its sign exactly as without a bias).
+__device__ inline float dequant1b(int32_t acc, float sx, float sw, bool has_bias, float b) {
+  float v = static_cast<float>(acc);
+  v = __fmul_rn(v, sx);
+  v = __fmul_rn(v, sw);
+  if (has_bias) v = __fadd_rn(v, b);
+  return v;
+}
+
 __device__ inline float dequant1(int32_t acc, float sx, float sw, const float* __restrict__ bias,
                                  int64_t n) {
   float v = static_cast<float>(acc);  // v_cvt_f32_i32: round to nearest even

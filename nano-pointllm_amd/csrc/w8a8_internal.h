@@ -56,8 +56,10 @@ hipError_t launch_gemm(const LinearOperands& op, hipStream_t st);
 constexpr int64_t kGemvMaxRows = 64;
 
 // Decode linear with the per-token quantization fused in (gemv_fused.hip):
-// 16-bit x, M == 1, K % 8 == 0, K <= 12288, 16-byte aligned rows.
-bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t K);
+// 16-bit x, 1 <= M <= 8, K % 8 == 0, K <= 12288, 16-byte aligned rows,
+// N <= 1024 * CUs, and enough weight bytes per CU to hide the quantization.
+bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
+                          int64_t K);
 hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const LinearOperands& op,
                              float* sx_out, hipStream_t st);
 

@@ -9,6 +9,7 @@ GPU's own int8 ``h``.
 """
 from __future__ import annotations
 
+import functools
 import json
 import sys
 from pathlib import Path
@@ -43,7 +44,10 @@ def rand_i8(shape, seed):
     return torch.randint(-127, 128, shape, generator=g, dtype=torch.int8)
 
 
+@functools.lru_cache(maxsize=4)
 def weight_q(n, k, seed):
+    """Seeded weight [n, k] and its per-output int8 quantization (cached: the
+    arrays are only read)."""
     from nanopointllm_amd import workloads as W
 
     w = W.linear_weight(n, k, seed=seed)
@@ -53,7 +57,7 @@ def weight_q(n, k, seed):
 
 # ------------------------------------------------------------ quantization
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("shape", [(1, 4096), (16, 4096), (7, 100), (3, 11008), (33, 4096), (5, 3)])
+@pytest.mark.parametrize("shape", [(1, 4096), (16, 4096), (7, 100), (3, 11008), (33, 4096), (5, 3), (3, 20000), (2, 2048)])
 def test_quant_rows_bit_exact(cuda, dtype, shape):
     from nanopointllm_amd import w8a8
 
@@ -286,8 +290,29 @@ def test_linear_fp16_bit_exact(cuda, m, n, k, with_bias):
     np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
 
 
+def _linear_without_workspace(x, wp, sw, bias, n, epi, y_dtype):
+    """w8a8_linear with a null workspace: succeeds only on the fused decode
+    kernel (every other path reports ERR_WORKSPACE before launching)."""
+    from nanopointllm_amd import _lib
+
+    lib = _lib.load()
+    m, k = x.shape
+    ncols = n // 2 if epi in (_lib.EPI_SILU_MUL, _lib.EPI_SILU_MUL_Q8) else n
+    y = torch.empty(m, ncols, dtype=y_dtype, device=x.device)
+    sx = torch.full((m,), -1.0, device=x.device)
+    rc = lib.w8a8_linear(x.data_ptr(), _lib.dtype_code(x.dtype), x.stride(0), wp.data_ptr(),
+                         sw.data_ptr(), None if bias is None else bias.data_ptr(), epi,
+                         y.data_ptr(), _lib.dtype_code(y_dtype), y.stride(0), 0.0, _lib.F16,
+                         m, n, k, sx.data_ptr(), None, 0, _lib.stream_handle(x.device))
+    return rc, y, sx
+
+
+# Shapes the fused kernel takes on a 256-CU MI355X (per CU >= 128 KiB of
+# weights and >= 4 weight bytes per quantized activation element): 3, 8, 32
+# and 2 blocks per CU; K = 256 leaves 12 of the 16 wavefronts without a
+# k-range, K = 12288 is the largest K the kernel takes.
 @pytest.mark.parametrize("m", [1, 2, 3, 5, 7, 8])
-@pytest.mark.parametrize("n,k", [(16, 8), (40, 64), (300, 1000), (96, 11008), (64, 12288)])
+@pytest.mark.parametrize("n,k", [(12288, 4096), (32768, 1000), (131072, 256), (8192, 12288)])
 def test_fused_decode_path(cuda, m, n, k):
     """Workspace-free decode kernel (quantization fused in): outputs, row
     scales and int32 accumulators against the oracle."""
@@ -300,16 +325,34 @@ def test_fused_decode_path(cuda, m, n, k):
     _, qw, sw = weight_q(n, k, seed=n + 3)
     bias = np.linspace(-2, 2, n).astype(np.float32)
     wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
-    sx = torch.full((m,), -1.0, device=cuda)
+    swt, bt, xc = torch.from_numpy(sw).to(cuda), torch.from_numpy(bias).to(cuda), x.to(cuda)
     note(f"fused decode m={m} n={n} k={k}")
-    y = w8a8.linear_dynamic(x.to(cuda), wp, torch.from_numpy(sw).to(cuda),
-                            torch.from_numpy(bias).to(cuda), n, x_scale_out=sx)
-    acc = w8a8.linear_dynamic(x.to(cuda), wp, torch.from_numpy(sw).to(cuda), None, n,
-                              epilogue=_lib.EPI_I32)
+    rc, y, sx = _linear_without_workspace(xc, wp, swt, bt, n, _lib.EPI_DEQUANT, torch.float16)
+    assert rc == 0, _lib.load().w8a8_status_string(rc)
+    rc, acc, _ = _linear_without_workspace(xc, wp, swt, None, n, _lib.EPI_I32, torch.int32)
+    assert rc == 0
     exp, eacc, _, esx = O.w8a8_linear_dynamic(x.float().numpy(), qw, sw, bias)
     np.testing.assert_array_equal(sx.cpu().numpy(), esx[:, 0])
     np.testing.assert_array_equal(acc.cpu().numpy(), eacc)
     np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+
+
+def test_fused_path_not_taken_for_small_shapes(cuda):
+    """O-sized and tiny projections go through quantization + GEMV (they need a
+    workspace) and give the same results."""
+    from nanopointllm_amd import _lib, w8a8
+
+    for n, k in [(4096, 4096), (40, 64), (16, 8)]:
+        _, qw, sw = weight_q(n, k, seed=n + k)
+        wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+        x = torch.randn(4, k, generator=torch.Generator().manual_seed(k)).to(torch.float16)
+        note(f"unfused decode n={n} k={k}")
+        rc, _, _ = _linear_without_workspace(x.to(cuda), wp, torch.from_numpy(sw).to(cuda), None,
+                                             n, _lib.EPI_DEQUANT, torch.float16)
+        assert rc == _lib.ERR_WORKSPACE
+        y = w8a8.linear_dynamic(x.to(cuda), wp, torch.from_numpy(sw).to(cuda), None, n)
+        exp, _, _, _ = O.w8a8_linear_dynamic(x.float().numpy(), qw, sw)
+        np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
 
 
 def test_fused_path_strided_rows_and_fallbacks(cuda):
@@ -331,6 +374,41 @@ def test_fused_path_strided_rows_and_fallbacks(cuda):
                                 else big.to(cuda)[:, 1:k + 1], wp, swt, None, n)
         exp, _, _, _ = O.w8a8_linear_dynamic(xv.float().numpy(), qw, sw)
         np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+
+
+@pytest.mark.parametrize("m,n,k", [(3, 16 * 64 * 256, 128), (8, 16 * 64 * 256 + 32, 64),
+                                   (5, 16 * 256 * 5, 2000), (8, 8192, 11008)])
+def test_fused_decode_many_blocks_silu_bias(cuda, m, n, k):
+    """Decode kernel with many 16-row output blocks per workgroup (64 on a
+    256-CU device at the first shape) and K in several chunks per wavefront,
+    through the SiLU*mul epilogue with a bias and the int32 epilogue.  The
+    second shape is just past the fused kernel's block limit on a 256-CU
+    device and runs quantization + GEMV instead; both must agree with the
+    oracle."""
+    from nanopointllm_amd import _lib, w8a8
+
+    g = torch.Generator().manual_seed(n + k)
+    x = (torch.randn(m, k, generator=g) * 3).to(torch.float16)
+    _, q, s = weight_q(n, k, seed=k + 5)        # rows 2c / 2c+1 = gate / up of column c
+    bias = np.linspace(-1.5, 1.5, n).astype(np.float32)
+    wp = w8a8.pack_rows(torch.from_numpy(q).to(cuda))
+    sw = torch.from_numpy(s).to(cuda)
+    xc = x.to(cuda)
+    note(f"fused many blocks m={m} n={n} k={k}")
+    rc, _, _ = _linear_without_workspace(xc, wp, sw, None, n, _lib.EPI_I32, torch.int32)
+    assert (rc == 0) == (n <= 16 * 64 * 256), "fused path taken iff within the block limit"
+    acc = w8a8.linear_dynamic(xc, wp, sw, None, n, epilogue=_lib.EPI_I32).cpu().numpy()
+    h = f16_to_np(w8a8.linear_dynamic(xc, wp, sw, torch.from_numpy(bias).to(cuda), n,
+                                      epilogue=_lib.EPI_SILU_MUL))
+    xq, sx = O.dynamic_per_token_quant(x.float().numpy())
+    eacc = O.int32_matmul_f64(xq, q)
+    np.testing.assert_array_equal(acc, eacc)
+    eh = O.gateup_silu_mul_from_acc(eacc, sx, s, bias, layout="interleave")
+    ulps = _fp16_ulps(h, eh)
+    note(f"fused many blocks: exact {np.mean(ulps == 0):.6f}, max ulp {ulps.max()}")
+    # Same bound as test_gateup_silu_mul: binary32 exp may differ by an ulp.
+    assert ulps.max() <= 2
+    assert np.mean(ulps == 0) > 0.999
 
 
 @pytest.mark.parametrize("m", [8, 200])
