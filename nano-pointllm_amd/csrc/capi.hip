@@ -64,6 +64,10 @@ inline int64_t output_cols(int epi, int y_dtype, int inter_dtype, int64_t n) {
       return (half_dtype(y_dtype) && n % 2 == 0) ? n / 2 : -1;
     case W8A8_EPI_SILU_MUL_Q8:
       return (y_dtype == kI8 && half_dtype(inter_dtype) && n % 2 == 0) ? n / 2 : -1;
+    case W8A8_EPI_REQUANT:
+      return y_dtype == kI8 ? n : -1;
+    case W8A8_EPI_DEQUANT_BF16_EXACT:
+      return y_dtype == kBF16 ? n : -1;
     default:
       return -1;
   }
@@ -81,7 +85,8 @@ inline int check_linear(const int8_t* w_packed, const float* w_scale, int epi, v
   // With k == 0 the packed weights are empty (and may be null): the product
   // kernels read no k-blocks and write bias-only / zero outputs.
   if ((k > 0 && w_packed == nullptr) || y == nullptr) return W8A8_ERR_NULL;
-  if (epi != W8A8_EPI_I32 && w_scale == nullptr) return W8A8_ERR_NULL;
+  if (epi != W8A8_EPI_I32 && epi != W8A8_EPI_REQUANT && w_scale == nullptr)
+    return W8A8_ERR_NULL;
   if (ldy < cols) return W8A8_ERR_SHAPE;
   if (!aligned(w_packed, 16) || !aligned(y, static_cast<uintptr_t>(elem_size(y_dtype))))
     return W8A8_ERR_ALIGN;
@@ -243,6 +248,10 @@ int w8a8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
                 float* x_scale_out, void* workspace, int64_t workspace_bytes,
                 hipStream_t stream) {
   if (!float_dtype(x_dtype)) return W8A8_ERR_DTYPE;
+  // The integer requant needs int8 activations with a static scale
+  // (w8a8_linear_i8in_requant); the single-rounding bf16 dequant has no bias.
+  if (epilogue == W8A8_EPI_REQUANT) return W8A8_ERR_DTYPE;
+  if (epilogue == W8A8_EPI_DEQUANT_BF16_EXACT && bias != nullptr) return W8A8_ERR_DTYPE;
   int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
                         n, k);
   if (rc != W8A8_OK || m == 0 || n == 0) return rc;
@@ -250,7 +259,7 @@ int w8a8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
   if (ldx < k) return W8A8_ERR_SHAPE;
   if (!aligned(x, static_cast<uintptr_t>(elem_size(x_dtype)))) return W8A8_ERR_ALIGN;
   if (x_scale_out != nullptr && !aligned(x_scale_out, 4)) return W8A8_ERR_ALIGN;
-  if (k > 0 && fused_gemv_supported(x, x_dtype, ldx, m, n, k)) {
+  if (k > 0 && epilogue <= W8A8_EPI_SILU_MUL_Q8 && fused_gemv_supported(x, x_dtype, ldx, m, n, k)) {
     // Decode: quantization fused into the GEMV, no workspace.
     LinearOperands op = make_ops(nullptr, 0, nullptr, w_packed, w_scale, bias, epilogue, y,
                                  y_dtype, ldy, y_scale, inter_dtype, m, n, k);
@@ -276,6 +285,8 @@ int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
                      int epilogue, void* y, int y_dtype, int64_t ldy, float y_scale,
                      int inter_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
                      int64_t workspace_bytes, hipStream_t stream) {
+  if (epilogue == W8A8_EPI_REQUANT) return W8A8_ERR_DTYPE;  // w8a8_linear_i8in_requant
+  if (epilogue == W8A8_EPI_DEQUANT_BF16_EXACT && bias != nullptr) return W8A8_ERR_DTYPE;
   int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
                         n, k);
   if (rc != W8A8_OK || m == 0 || n == 0) return rc;
@@ -292,6 +303,61 @@ int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
   LinearOperands op = make_ops(a, lda, x_scale, w_packed, w_scale, bias, epilogue, y, y_dtype,
                                ldy, y_scale, inter_dtype, m, n, k);
   return status_of(run_product(op, stream));
+}
+
+int w8a8_linear_i8in_requant(const int8_t* xq, int64_t ldq, const int8_t* w_packed,
+                             const uint32_t* multiplier, const int32_t* right_shift,
+                             const int32_t* bias_i32, int8_t* y, int64_t ldy, int64_t m,
+                             int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                             hipStream_t stream) {
+  int rc = check_linear(w_packed, nullptr, W8A8_EPI_REQUANT, y, kI8, ldy, 0.0f, kF16, m, n, k);
+  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
+  if (xq == nullptr || multiplier == nullptr || right_shift == nullptr) return W8A8_ERR_NULL;
+  if (!aligned(multiplier, 4) || !aligned(right_shift, 4) || !aligned(bias_i32, 4))
+    return W8A8_ERR_ALIGN;
+  if (ldq < k) return W8A8_ERR_SHAPE;
+  if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
+    return W8A8_ERR_WORKSPACE;
+  if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
+  int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
+  const int8_t* a = nullptr;
+  int64_t lda = 0;
+  hipError_t e = stage_i8(xq, ldq, m, k, act, &a, &lda, stream);
+  if (e != hipSuccess) return status_of(e);
+  LinearOperands op = make_ops(a, lda, nullptr, w_packed, nullptr, nullptr, W8A8_EPI_REQUANT, y,
+                               kI8, ldy, 0.0f, kF16, m, n, k);
+  op.rq_mult = multiplier;
+  op.rq_shift = right_shift;
+  op.rq_bias = bias_i32;
+  return status_of(run_product(op, stream));
+}
+
+int w8a8_requantize_i32(const int32_t* acc, int64_t ld_acc, const int32_t* bias_i32,
+                        const uint32_t* multiplier, const int32_t* right_shift, int8_t* y,
+                        int64_t ldy, int64_t m, int64_t n, hipStream_t stream) {
+  if (m < 0 || n < 0) return W8A8_ERR_SHAPE;
+  if (m == 0 || n == 0) return W8A8_OK;
+  if (acc == nullptr || multiplier == nullptr || right_shift == nullptr || y == nullptr)
+    return W8A8_ERR_NULL;
+  if (ld_acc < n || ldy < n) return W8A8_ERR_SHAPE;
+  if (!aligned(acc, 4) || !aligned(multiplier, 4) || !aligned(right_shift, 4) ||
+      !aligned(bias_i32, 4))
+    return W8A8_ERR_ALIGN;
+  return status_of(
+      launch_requant_i32(acc, ld_acc, bias_i32, multiplier, right_shift, y, ldy, m, n, stream));
+}
+
+int w8a8_dequant_i32_bf16(const int32_t* acc, int64_t ld_acc, const uint16_t* sa_bits,
+                          const uint16_t* sw_bits, uint16_t* y, int64_t ldy, int64_t m,
+                          int64_t n, hipStream_t stream) {
+  if (m < 0 || n < 0) return W8A8_ERR_SHAPE;
+  if (m == 0 || n == 0) return W8A8_OK;
+  if (acc == nullptr || sa_bits == nullptr || sw_bits == nullptr || y == nullptr)
+    return W8A8_ERR_NULL;
+  if (ld_acc < n || ldy < n) return W8A8_ERR_SHAPE;
+  if (!aligned(acc, 4) || !aligned(sa_bits, 2) || !aligned(sw_bits, 2) || !aligned(y, 2))
+    return W8A8_ERR_ALIGN;
+  return status_of(launch_dequant_i32_bf16(acc, ld_acc, sa_bits, sw_bits, y, ldy, m, n, stream));
 }
 
 }  // extern "C"

@@ -37,6 +37,9 @@ struct GemmParams {
   void* y;
   int64_t ldy;
   float out_scale;
+  const uint32_t* rq_mult;
+  const int32_t* rq_shift;
+  const int32_t* rq_bias;
   int M;
   int N;
   int MB;
@@ -154,7 +157,16 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_kernel(GemmParams p) {
   const int64_t n = static_cast<int64_t>(nb0 + 2 * wn) * 16 + (lane & 31);
   const bool n_ok = n < p.N;
   float swn = 0.0f;
-  if constexpr (EPI != kEpiI32) swn = n_ok ? p.sw[n] : 0.0f;
+  if constexpr (EPI != kEpiI32 && EPI != kEpiRequant) swn = n_ok ? p.sw[n] : 0.0f;
+  uint32_t rq_mult = 0;
+  int32_t rq_shift = 0, rq_bias = 0;
+  if constexpr (EPI == kEpiRequant) {
+    if (n_ok) {
+      rq_mult = p.rq_mult[n];
+      rq_shift = p.rq_shift[n];
+      rq_bias = p.rq_bias != nullptr ? p.rq_bias[n] : 0;
+    }
+  }
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int m = (mb0 + 2 * wm) * 16 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
@@ -166,6 +178,16 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_kernel(GemmParams p) {
       if (m_ok && n_ok) {
         static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
             from_f32<TY>(dequant1(a, p.sx[m], swn, p.bias, n));
+      }
+    } else if constexpr (EPI == kEpiRequant) {
+      if (m_ok && n_ok) {
+        static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
+            static_cast<int8_t>(requant1(a, rq_bias, rq_mult, rq_shift));
+      }
+    } else if constexpr (EPI == kEpiBf16Exact) {
+      if (m_ok && n_ok) {
+        static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
+            __builtin_bit_cast(TY, dequant_bf16_exact(a, f16_bits(p.sx[m]), f16_bits(swn)));
       }
     } else {
       // Interleaved gate/up: even column = gate, odd column = up of output
@@ -222,6 +244,9 @@ hipError_t launch_gemm(const LinearOperands& op, hipStream_t st) {
   p.y = op.y;
   p.ldy = op.ldy;
   p.out_scale = op.out_scale;
+  p.rq_mult = op.rq_mult;
+  p.rq_shift = op.rq_shift;
+  p.rq_bias = op.rq_bias;
   p.M = static_cast<int>(op.M);
   p.N = static_cast<int>(op.N);
   p.MB = static_cast<int>(ceil_div(op.M, kTileRows));
@@ -245,6 +270,10 @@ hipError_t launch_gemm(const LinearOperands& op, hipStream_t st) {
       if (op.h_dtype == kF16) return launch_t<kEpiSiluQ8, int8_t, __half>(p, st);
       if (op.h_dtype == kBF16) return launch_t<kEpiSiluQ8, int8_t, __hip_bfloat16>(p, st);
       return hipErrorInvalidValue;
+    case kEpiRequant:
+      return launch_t<kEpiRequant, int8_t, float>(p, st);
+    case kEpiBf16Exact:
+      return launch_t<kEpiBf16Exact, __hip_bfloat16, float>(p, st);
     default:
       return hipErrorInvalidValue;
   }

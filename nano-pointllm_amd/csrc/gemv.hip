@@ -31,6 +31,9 @@ struct GemvParams {
   void* y;
   int64_t ldy;
   float out_scale;
+  const uint32_t* rq_mult;
+  const int32_t* rq_shift;
+  const int32_t* rq_bias;
   int M;
   int N;
   int KB;
@@ -119,7 +122,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   }
   __syncthreads();
 
-  if constexpr (EPI == kEpiI32 || EPI == kEpiDequant) {
+  if constexpr (EPI == kEpiI32 || EPI == kEpiDequant || EPI == kEpiRequant ||
+                EPI == kEpiBf16Exact) {
     for (int e = tid; e < MT * 256; e += NT) {
       const int m = (e >> 8) * 16 + ((e & 255) >> 4);
       const int64_t n = nb * 16 + (e & 15);
@@ -130,6 +134,11 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
       TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n;
       if constexpr (EPI == kEpiI32) {
         *y = s;
+      } else if constexpr (EPI == kEpiRequant) {
+        *y = static_cast<int8_t>(
+            requant1(s, p.rq_bias != nullptr ? p.rq_bias[n] : 0, p.rq_mult[n], p.rq_shift[n]));
+      } else if constexpr (EPI == kEpiBf16Exact) {
+        *y = __builtin_bit_cast(TY, dequant_bf16_exact(s, f16_bits(p.sx[m]), f16_bits(p.sw[n])));
       } else {
         *y = from_f32<TY>(dequant1(s, p.sx[m], p.sw[n], p.bias, n));
       }
@@ -204,6 +213,9 @@ hipError_t launch_gemv(const LinearOperands& op, hipStream_t st) {
   p.y = op.y;
   p.ldy = op.ldy;
   p.out_scale = op.out_scale;
+  p.rq_mult = op.rq_mult;
+  p.rq_shift = op.rq_shift;
+  p.rq_bias = op.rq_bias;
   p.M = static_cast<int>(op.M);
   p.N = static_cast<int>(op.N);
   p.KB = static_cast<int>(ceil_div(op.K, kTileK));
@@ -226,6 +238,10 @@ hipError_t launch_gemv(const LinearOperands& op, hipStream_t st) {
       if (op.h_dtype == kF16) return launch_mt<kEpiSiluQ8, int8_t, __half>(p, nblocks, st);
       if (op.h_dtype == kBF16) return launch_mt<kEpiSiluQ8, int8_t, __hip_bfloat16>(p, nblocks, st);
       return hipErrorInvalidValue;
+    case kEpiRequant:
+      return launch_mt<kEpiRequant, int8_t, float>(p, nblocks, st);
+    case kEpiBf16Exact:
+      return launch_mt<kEpiBf16Exact, __hip_bfloat16, float>(p, nblocks, st);
     default:
       return hipErrorInvalidValue;
   }

@@ -12,6 +12,8 @@ enum Epilogue : int {
   kEpiDequant = 1,  // f32(acc) * s_x * s_w (+ bias) -> output type
   kEpiSilu = 2,     // packed interleaved gate/up: SiLU(g) * u -> output type
   kEpiSiluQ8 = 3,   // as kEpiSilu, then int8 with a static scale
+  kEpiRequant = 4,  // int8: (acc + bias_i32) * multiplier >> shift (requant1)
+  kEpiBf16Exact = 5,  // bf16: acc * s_x * s_w rounded once (dequant_bf16_exact)
 };
 
 struct LinearOperands {
@@ -28,9 +30,24 @@ struct LinearOperands {
   int y_dtype;      // output element type (kF32/kF16/kBF16/kI32/kI8)
   int h_dtype;      // SiLU intermediate rounding type for kEpiSiluQ8 (kF16/kBF16)
   float out_scale;  // static requant scale for kEpiSiluQ8
+  // kEpiRequant: per-output multiplier, right shift and int32 bias (nullable).
+  const uint32_t* rq_mult = nullptr;
+  const int32_t* rq_shift = nullptr;
+  const int32_t* rq_bias = nullptr;
   int64_t M, N, K;
   int epi;
 };
+
+// Elementwise epilogues over caller int32 accumulators acc[m, ld_acc]:
+// requant1 per element with per-column multiplier / shift / bias (nullable)
+// into int8 y, or dequant_bf16_exact with binary16 scale bit patterns
+// sa_bits[m] and sw_bits[n] into bfloat16 y.
+hipError_t launch_requant_i32(const int32_t* acc, int64_t ld_acc, const int32_t* bias,
+                              const uint32_t* mult, const int32_t* shift, int8_t* y, int64_t ldy,
+                              int64_t M, int64_t N, hipStream_t st);
+hipError_t launch_dequant_i32_bf16(const int32_t* acc, int64_t ld_acc, const uint16_t* sa_bits,
+                                   const uint16_t* sw_bits, uint16_t* y, int64_t ldy, int64_t M,
+                                   int64_t N, hipStream_t st);
 
 // Quantizes each row of x (scale_in == nullptr: dynamic per-row scale).
 // Row-major output writes columns [0, ncols_out) (zeros past K); packed

@@ -13,10 +13,11 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libw8a8_gfx950.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 F32, F16, BF16, I32, I8 = 0, 1, 2, 3, 4
 EPI_I32, EPI_DEQUANT, EPI_SILU_MUL, EPI_SILU_MUL_Q8 = 0, 1, 2, 3
+EPI_REQUANT, EPI_DEQUANT_BF16_EXACT = 4, 5
 ROWS_AS_IS, ROWS_INTERLEAVE_HALVES = 0, 1
 
 OK = 0
@@ -42,6 +43,9 @@ EXPORTED_SYMBOLS = (
     "w8a8_gemm_i32",
     "w8a8_linear",
     "w8a8_linear_i8in",
+    "w8a8_linear_i8in_requant",
+    "w8a8_requantize_i32",
+    "w8a8_dequant_i32_bf16",
 )
 
 _lock = threading.Lock()
@@ -66,6 +70,10 @@ _SIGNATURES = {
                            _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
     "w8a8_linear_i8in": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _int, _vp, _int, _i64, _f32,
                                 _int, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "w8a8_linear_i8in_requant": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                                        _i64, _vp, _i64, _vp]),
+    "w8a8_requantize_i32": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "w8a8_dequant_i32_bf16": (_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
 }
 
 

@@ -139,6 +139,16 @@ def _out_cols(epilogue: int, n: int) -> int:
     return n // 2 if epilogue in (_lib.EPI_SILU_MUL, _lib.EPI_SILU_MUL_Q8) else n
 
 
+def _default_out_dtype(epilogue: int, x_dtype: torch.dtype) -> torch.dtype:
+    if epilogue == _lib.EPI_SILU_MUL_Q8:
+        return torch.int8
+    if epilogue == _lib.EPI_I32:
+        return torch.int32
+    if epilogue == _lib.EPI_DEQUANT_BF16_EXACT:
+        return torch.bfloat16
+    return x_dtype
+
+
 def linear_dynamic(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
                    bias: torch.Tensor | None, n: int, *, epilogue: int = _lib.EPI_DEQUANT,
                    out_dtype: torch.dtype | None = None, y_scale: float = 0.0,
@@ -149,8 +159,7 @@ def linear_dynamic(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tenso
     x2, ldx = _rows_view(x)
     m, k = x2.shape
     if out_dtype is None:
-        out_dtype = torch.int8 if epilogue == _lib.EPI_SILU_MUL_Q8 else (
-            torch.int32 if epilogue == _lib.EPI_I32 else x.dtype)
+        out_dtype = _default_out_dtype(epilogue, x.dtype)
     if inter_dtype is None:
         inter_dtype = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.float16
     cols = _out_cols(epilogue, n)
@@ -174,10 +183,12 @@ def linear_dynamic(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tenso
 
 def linear_i8in(xq: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor,
                 w_scale: torch.Tensor, bias: torch.Tensor | None, n: int, *,
-                epilogue: int = _lib.EPI_DEQUANT, out_dtype: torch.dtype = torch.float16,
+                epilogue: int = _lib.EPI_DEQUANT, out_dtype: torch.dtype | None = None,
                 y_scale: float = 0.0, inter_dtype: torch.dtype = torch.float16) -> torch.Tensor:
     """W8A8 linear on already-quantized activations with per-row scales."""
     device = _lib.require_cuda(xq, x_scale, w_packed, w_scale, bias)
+    if out_dtype is None:
+        out_dtype = _default_out_dtype(epilogue, torch.float16)
     x2, ldq = _rows_view(xq)
     m, k = x2.shape
     s = x_scale.detach().to(dtype=torch.float32).reshape(-1)

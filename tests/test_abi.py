@@ -22,7 +22,7 @@ def declared_symbols() -> list[str]:
 def test_header_declarations_are_exported():
     lib = _lib.load()
     names = declared_symbols()
-    assert len(names) == 11
+    assert len(names) == 14
     for name in names:
         assert hasattr(lib, name), name
     assert sorted(_lib.EXPORTED_SYMBOLS) == names
@@ -77,6 +77,41 @@ def test_invalid_arguments_return_status_without_launch():
     # empty problems are valid no-ops
     assert lib.w8a8_linear(None, _lib.F16, 64, None, None, None, _lib.EPI_DEQUANT, None,
                            _lib.F16, 16, 0.0, _lib.F16, 0, 16, 64, None, None, 0, None) == _lib.OK
+
+
+def test_integer_epilogue_arguments_rejected_without_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    # the integer requant needs int8 activations with a static scale
+    assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_REQUANT, fake,
+                           _lib.I8, 16, 0.0, _lib.F16, 9, 16, 64, None, fake, 1 << 20,
+                           None) == _lib.ERR_DTYPE
+    assert lib.w8a8_linear_i8in(fake, 64, fake, fake, fake, None, _lib.EPI_REQUANT, fake,
+                                _lib.I8, 16, 0.0, _lib.F16, 9, 16, 64, fake, 1 << 20,
+                                None) == _lib.ERR_DTYPE
+    # the single-rounding bf16 dequant has a bfloat16 output and no bias
+    assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, fake, _lib.EPI_DEQUANT_BF16_EXACT,
+                           fake, _lib.BF16, 16, 0.0, _lib.F16, 9, 16, 64, None, fake, 1 << 20,
+                           None) == _lib.ERR_DTYPE
+    assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_DEQUANT_BF16_EXACT,
+                           fake, _lib.F16, 16, 0.0, _lib.F16, 9, 16, 64, None, fake, 1 << 20,
+                           None) == _lib.ERR_DTYPE
+    # fused requant linear: null multiplier, short workspace, int8 output only
+    assert lib.w8a8_linear_i8in_requant(fake, 64, fake, None, fake, None, fake, 16, 2, 16, 64,
+                                        fake, 1 << 20, None) == _lib.ERR_NULL
+    assert lib.w8a8_linear_i8in_requant(fake, 64, fake, fake, fake, None, fake, 16, 2, 16, 64,
+                                        fake, 10, None) == _lib.ERR_WORKSPACE
+    assert lib.w8a8_linear_i8in_requant(fake, 64, fake, fake, fake, ctypes.c_void_p(0x1002),
+                                        fake, 16, 2, 16, 64, fake, 1 << 20,
+                                        None) == _lib.ERR_ALIGN
+    # elementwise epilogues
+    assert lib.w8a8_requantize_i32(fake, 8, None, fake, fake, fake, 16, 2, 16,
+                                   None) == _lib.ERR_SHAPE
+    assert lib.w8a8_requantize_i32(fake, 16, None, fake, None, fake, 16, 2, 16,
+                                   None) == _lib.ERR_NULL
+    assert lib.w8a8_dequant_i32_bf16(fake, 16, fake, fake, ctypes.c_void_p(0x1001), 16, 2, 16,
+                                     None) == _lib.ERR_ALIGN
+    assert lib.w8a8_dequant_i32_bf16(None, 16, None, None, None, 16, 0, 16, None) == _lib.OK
 
 
 def test_status_errors_map_to_python_exceptions():

@@ -1,0 +1,219 @@
+"""Hardware-model integer contracts: a17 INT32 -> A8 requantization and a18
+INT32 x FP16 x FP16 -> BF16 single-rounding dequantization.
+
+CPU: the host-side scale compiler against the oracle and the reference's
+asserted compile case.  GPU: the elementwise kernels against the reference's
+locked vectors and the oracle, and the fused product epilogues (GEMV and GEMM
+paths) against the oracle applied to the exact int32 product.  Bar: bit-exact.
+"""
+from __future__ import annotations
+
+import json
+import random
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import w8a8_oracle as O
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "reference_vectors.json").read_text())
+
+
+def note(msg: str) -> None:
+    import sys
+    sys.__stderr__.write(f"[gpu-case] {msg}\n")
+    sys.__stderr__.flush()
+
+
+# ------------------------------------------------------------------ CPU
+def test_compile_matches_oracle_and_reference_assertion():
+    from nanopointllm_amd import integer_epilogues as E
+
+    kat = GOLDEN["requant_locked"]["asserted_compile"]
+    c = E.compile_fp16_requant_scale(kat["activation_scale"], kat["weight_scale"],
+                                     kat["output_scale"])
+    assert c.relative_error < kat["relative_error_below"]
+    rng = random.Random(11)
+    for _ in range(3000):
+        a, w, o = (10 ** rng.uniform(-4, 1) for _ in range(3))
+        mine = E.compile_fp16_requant_scale(a, w, o)
+        mult, shift, ratio, rel = O.compile_fp16_requant_scale(a, w, o)
+        assert (mine.multiplier, mine.right_shift) == (mult, shift)
+        assert mine.exact_ratio == ratio and mine.relative_error == rel
+        assert 0 < mine.multiplier < 2 ** 32 and 0 <= mine.right_shift <= 63
+    with pytest.raises(ValueError, match="positive finite"):
+        E.compile_fp16_requant_scale(0.0, 1.0, 1.0)
+    with pytest.raises(ValueError, match="positive and finite"):
+        E.compile_requant_ratio(float("inf"))
+
+
+# ------------------------------------------------------------------ GPU
+def _requant_ref(acc, bias, mult, shift):
+    m, n = acc.shape
+    out = np.empty((m, n), np.int8)
+    for i in range(m):
+        for j in range(n):
+            out[i, j] = O.requantize_int32(int(acc[i, j]), int(bias[j]), int(mult[j]),
+                                           int(shift[j]))
+    return out
+
+
+def _bf16_ref(acc, sa_bits, sw_bits):
+    m, n = acc.shape
+    out = np.empty((m, n), np.uint16)
+    for i in range(m):
+        for j in range(n):
+            out[i, j] = O.dequantize_int32_to_bf16(int(acc[i, j]), int(sa_bits[i]),
+                                                   int(sw_bits[j]))
+    return out
+
+
+def _u32_as_i32(values) -> torch.Tensor:
+    return torch.from_numpy(np.asarray(values, np.uint32).view(np.int32))
+
+
+@pytest.mark.gpu
+def test_requantize_locked_vectors_and_random(cuda):
+    from nanopointllm_amd import integer_epilogues as E
+
+    vec = np.array(GOLDEN["requant_locked"]["vectors"], dtype=np.int64)
+    acc = vec[:, 0].astype(np.int32).reshape(1, -1)
+    bias, mult, shift = vec[:, 1].astype(np.int32), vec[:, 2], vec[:, 3].astype(np.int32)
+    note("requantize_i32 locked vectors")
+    got = E.requantize_int32(torch.from_numpy(acc).to(cuda), torch.from_numpy(bias).to(cuda),
+                             _u32_as_i32(mult).to(cuda), torch.from_numpy(shift).to(cuda))
+    got = got.cpu().numpy()[0]
+    assert got[3:7].tolist() == GOLDEN["requant_locked"]["asserted_outputs_3_7"]
+    assert got[7:9].tolist() == GOLDEN["requant_locked"]["asserted_outputs_7_9"]
+    np.testing.assert_array_equal(got, _requant_ref(acc, bias, mult, shift)[0])
+
+    rng = np.random.default_rng(7)
+    m, n = 37, 67
+    acc = rng.integers(-2 ** 31, 2 ** 31, (m, n), dtype=np.int64).astype(np.int32)
+    acc[:, :20] = rng.integers(-70000, 70000, (m, 20))
+    bias = rng.integers(-2 ** 31, 2 ** 31, n, dtype=np.int64).astype(np.int32)
+    bias[::3] = rng.integers(-500, 500, bias[::3].size)
+    mult = rng.integers(0, 2 ** 32, n, dtype=np.uint64).astype(np.uint32)
+    shift = rng.integers(0, 64, n).astype(np.int32)
+    note("requantize_i32 random")
+    got = E.requantize_int32(torch.from_numpy(acc).to(cuda), torch.from_numpy(bias).to(cuda),
+                             _u32_as_i32(mult).to(cuda), torch.from_numpy(shift).to(cuda))
+    np.testing.assert_array_equal(got.cpu().numpy(), _requant_ref(acc, bias, mult, shift))
+    # no bias
+    got = E.requantize_int32(torch.from_numpy(acc).to(cuda), None, _u32_as_i32(mult).to(cuda),
+                             torch.from_numpy(shift).to(cuda))
+    np.testing.assert_array_equal(got.cpu().numpy(),
+                                  _requant_ref(acc, np.zeros(n, np.int32), mult, shift))
+
+
+@pytest.mark.gpu
+def test_dequant_bf16_locked_vectors_and_random(cuda):
+    from nanopointllm_amd import integer_epilogues as E
+
+    vec = GOLDEN["bf16_dequant_locked"]["vectors"]
+    k = len(vec)
+    # vector i on the diagonal: row scale sa_i, column scale sw_i
+    acc = np.zeros((k, k), np.int32)
+    for i, (a, _, _) in enumerate(vec):
+        acc[i, :] = a
+    sa = np.array([v[1] for v in vec], np.uint16)
+    sw = np.array([v[2] for v in vec], np.uint16)
+    note("dequant_i32_bf16 locked vectors")
+    got = E.dequantize_int32_to_bf16(torch.from_numpy(acc).to(cuda),
+                                     torch.from_numpy(sa.view(np.int16)).to(cuda),
+                                     torch.from_numpy(sw.view(np.int16)).to(cuda))
+    bits = got.cpu().view(torch.int16).numpy().view(np.uint16)
+    diag = np.diag(bits)
+    assert diag[:3].tolist() == GOLDEN["bf16_dequant_locked"]["asserted_outputs_0_3"]
+    assert int(diag[6]) == GOLDEN["bf16_dequant_locked"]["asserted_output_6"]
+    np.testing.assert_array_equal(bits, _bf16_ref(acc, sa, sw))
+
+    rng = np.random.default_rng(20261002)
+    m, n = 33, 70
+    acc = rng.integers(-2 ** 31, 2 ** 31, (m, n), dtype=np.int64).astype(np.int32)
+    acc[:, ::5] = rng.integers(-300, 300, (m, acc[:, ::5].shape[1]))
+    finite = lambda size: np.array([b for b in rng.integers(0, 1 << 16, 4 * size)
+                                    if (b >> 10) & 0x1F != 0x1F][:size], np.uint16)
+    sa, sw = finite(m), finite(n)
+    sw[:4] = [1, 2, 0x8001, 0x7BFF]                       # subnormal and largest scales
+    note("dequant_i32_bf16 random")
+    got = E.dequantize_int32_to_bf16(torch.from_numpy(acc).to(cuda),
+                                     torch.from_numpy(sa.view(np.int16)).to(cuda),
+                                     torch.from_numpy(sw.view(np.int16)).to(cuda))
+    np.testing.assert_array_equal(got.cpu().view(torch.int16).numpy().view(np.uint16),
+                                  _bf16_ref(acc, sa, sw))
+
+
+def _weights(n, k, seed):
+    from nanopointllm_amd import workloads as W
+
+    _, q, s = O.per_output_weight_qdq(W.linear_weight(n, k, seed=seed).float().numpy())
+    return q, s
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 8, 40, 100, 300])
+def test_linear_i8in_requant_fused(cuda, m):
+    """int8-in linear with the integer requant epilogue (GEMV for m <= 64,
+    GEMM above) against requantize_int32 of the exact int32 product."""
+    from nanopointllm_amd import integer_epilogues as E, w8a8
+
+    n, k = 200, 1000
+    q, s = _weights(n, k, seed=m)
+    xq = torch.randint(-127, 128, (m, k), generator=torch.Generator().manual_seed(m),
+                       dtype=torch.int8)
+    act_scale, out_scale = 0.02, 0.5
+    comp = [O.compile_fp16_requant_scale(act_scale, float(w), out_scale) for w in s]
+    mult = np.array([c[0] for c in comp], np.uint32)
+    shift = np.array([c[1] for c in comp], np.int32)
+    bias = np.random.default_rng(m).integers(-3000, 3000, n).astype(np.int32)
+    wp = w8a8.pack_rows(torch.from_numpy(q).to(cuda))
+    note(f"linear_i8in_requant m={m}")
+    y = E.linear_i8in_requant(xq.to(cuda), wp, _u32_as_i32(mult).to(cuda),
+                              torch.from_numpy(shift).to(cuda), torch.from_numpy(bias).to(cuda),
+                              n)
+    acc = O.int32_matmul_f64(xq.numpy(), q)
+    np.testing.assert_array_equal(y.cpu().numpy(), _requant_ref(acc, bias, mult, shift))
+
+    # the module: same compile on the GPU-quantized weights
+    lin = torch.nn.Linear(k, n, bias=False)
+    from nanopointllm_amd import workloads as W
+    lin.weight.data = W.linear_weight(n, k, seed=m).to(cuda)
+    mod = E.StaticA8RequantLinear(lin, act_scale, out_scale)
+    ym = mod(xq.to(cuda)).cpu().numpy()
+    mm, ss = E.compile_per_output(act_scale, mod.weight_scale, out_scale)
+    np.testing.assert_array_equal(ym, _requant_ref(acc, np.zeros(n, np.int32),
+                                                   mm.cpu().numpy().view(np.uint32),
+                                                   ss.cpu().numpy()))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("m", [1, 8, 64, 65, 200])
+def test_linear_bf16_exact_epilogue(cuda, m):
+    """Dynamic per-token linear and int8-in linear with the single-rounding
+    bf16 epilogue against dequantize_int32_to_bf16 of the exact product."""
+    from nanopointllm_amd import _lib, w8a8
+
+    n, k = 96, 700
+    q, s = _weights(n, k, seed=100 + m)
+    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(m)) * 3).to(torch.float16)
+    wp = w8a8.pack_rows(torch.from_numpy(q).to(cuda))
+    note(f"bf16 exact epilogue m={m}")
+    y = w8a8.linear_dynamic(x.to(cuda), wp, torch.from_numpy(s).to(cuda), None, n,
+                            epilogue=_lib.EPI_DEQUANT_BF16_EXACT)
+    assert y.dtype == torch.bfloat16
+    xq, sx = O.dynamic_per_token_quant(x.float().numpy())
+    acc = O.int32_matmul_f64(xq, q)
+    sa = sx[:, 0].astype(np.float16).view(np.uint16)
+    sw = s.astype(np.float16).view(np.uint16)
+    exp = _bf16_ref(acc, sa, sw)
+    np.testing.assert_array_equal(y.cpu().view(torch.int16).numpy().view(np.uint16), exp)
+    y8 = w8a8.linear_i8in(torch.from_numpy(xq).to(cuda), torch.from_numpy(sx[:, 0]).to(cuda), wp,
+                          torch.from_numpy(s).to(cuda), None, n,
+                          epilogue=_lib.EPI_DEQUANT_BF16_EXACT)
+    np.testing.assert_array_equal(y8.cpu().view(torch.int16).numpy().view(np.uint16), exp)
+    with pytest.raises(ValueError):
+        w8a8.linear_dynamic(x.to(cuda), wp, torch.from_numpy(s).to(cuda),
+                            torch.zeros(n, device=cuda), n, epilogue=_lib.EPI_DEQUANT_BF16_EXACT)
