@@ -183,6 +183,30 @@ int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
                      int64_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Activation prologue fused into the quantization, one pass per row of x
+ * (F16/BF16 [m, ldx]), each step optional:
+ *   residual add   s = x + residual (x's dtype), written to residual_out
+ *                  (LightweightRMSNorm.residual_norm, lightweight_runner.py:247-257);
+ *   RMSNorm        y = w * dtype(f32(s) / sqrt(mean(f32(s)^2) + eps)) with
+ *                  norm_weight [k] of x's dtype or F32 (norm_weight_dtype); an
+ *                  F32 weight keeps y in binary32 (lightweight_runner.py:239-245);
+ *   smooth divide  y = dtype(y / smooth[k]), smooth of x's dtype (the
+ *                  SmoothQuant input transform, w8a8.py:351-359);
+ *   quantization   per-row dynamic scale (w8a8.py:106-115), or the one
+ *                  static_scale (w8a8.py:94-103): q int8 [m, ldq] (k columns),
+ *                  scales_out [m] (nullable with a static scale).
+ * x_out (nullable, [m, ld_x_out], x's dtype or F32 as y) receives y.  The
+ * binary32 sum of squares is summed in the kernel's order; every other step
+ * is exactly rounded.  k <= 32768.
+ */
+int w8a8_prologue_quant(const void* x, int x_dtype, int64_t ldx, const void* residual,
+                        int64_t ld_residual, void* residual_out, int64_t ld_residual_out,
+                        const void* norm_weight, int norm_weight_dtype, float eps,
+                        const void* smooth, const float* static_scale, int64_t m, int64_t k,
+                        int8_t* q, int64_t ldq, float* scales_out, void* x_out,
+                        int64_t ld_x_out, hipStream_t stream);
+
+/*
  * Static-A8 linear with the hardware model's integer requantization
  * (architecture_simulator/gtsu_cycle/requant.py:62-119): xq int8 [m, ldq]
  * (activations quantized with one static scale), y int8 [m, ldy] =

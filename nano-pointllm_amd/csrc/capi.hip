@@ -305,6 +305,35 @@ int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
   return status_of(run_product(op, stream));
 }
 
+int w8a8_prologue_quant(const void* x, int x_dtype, int64_t ldx, const void* residual,
+                        int64_t ld_residual, void* residual_out, int64_t ld_residual_out,
+                        const void* norm_weight, int norm_weight_dtype, float eps,
+                        const void* smooth, const float* static_scale, int64_t m, int64_t k,
+                        int8_t* q, int64_t ldq, float* scales_out, void* x_out,
+                        int64_t ld_x_out, hipStream_t stream) {
+  if (!half_dtype(x_dtype)) return W8A8_ERR_DTYPE;
+  const bool w32 = norm_weight != nullptr && norm_weight_dtype == kF32;
+  if (norm_weight != nullptr && norm_weight_dtype != x_dtype && !w32) return W8A8_ERR_DTYPE;
+  if (m < 0 || k < 0 || k > prologue_max_k() || m > INT32_MAX) return W8A8_ERR_SHAPE;
+  if (m == 0 || k == 0) return W8A8_OK;
+  if (x == nullptr || q == nullptr) return W8A8_ERR_NULL;
+  if (residual != nullptr && residual_out == nullptr) return W8A8_ERR_NULL;
+  if (static_scale == nullptr && scales_out == nullptr) return W8A8_ERR_NULL;
+  if (ldx < k || ldq < k) return W8A8_ERR_SHAPE;
+  if (residual != nullptr && (ld_residual < k || ld_residual_out < k)) return W8A8_ERR_SHAPE;
+  if (x_out != nullptr && ld_x_out < k) return W8A8_ERR_SHAPE;
+  if (!(eps >= 0.0f)) return W8A8_ERR_SHAPE;
+  const uintptr_t xs = static_cast<uintptr_t>(elem_size(x_dtype));
+  if (!aligned(x, xs) || !aligned(residual, xs) || !aligned(residual_out, xs) ||
+      !aligned(smooth, xs) || !aligned(norm_weight, w32 ? 4 : xs) || !aligned(static_scale, 4) ||
+      !aligned(scales_out, 4) || !aligned(x_out, w32 ? 4 : xs))
+    return W8A8_ERR_ALIGN;
+  return status_of(launch_prologue_quant(x, x_dtype, ldx, residual, ld_residual, residual_out,
+                                         ld_residual_out, norm_weight, norm_weight_dtype, eps,
+                                         smooth, static_scale, m, k, q, ldq, scales_out, x_out,
+                                         ld_x_out, stream));
+}
+
 int w8a8_linear_i8in_requant(const int8_t* xq, int64_t ldq, const int8_t* w_packed,
                              const uint32_t* multiplier, const int32_t* right_shift,
                              const int32_t* bias_i32, int8_t* y, int64_t ldy, int64_t m,

@@ -1,0 +1,220 @@
+// Fused activation prologue of the W8A8 linear: one pass over each row of x
+//   [residual add] -> [RMSNorm] -> [SmoothQuant divide] -> int8 quantization
+// producing the int8 row and its scale for the int8-in GEMV / GEMM.
+//
+//   residual add   summed = x + residual in the input dtype, also written out
+//                  (LightweightRMSNorm.residual_norm,
+//                  nanopointllm/llama/lightweight_runner.py:247-257)
+//   RMSNorm        y = weight * dtype(f32(x) * 1/sqrt(mean(f32(x)^2) + eps))
+//                  (LightweightRMSNorm.forward, lightweight_runner.py:239-245):
+//                  the product is rounded to the input dtype when the weight
+//                  has that dtype and kept in binary32 for a binary32 weight,
+//                  as torch's type promotion does
+//   smooth divide  y = dtype(f32(y) / f32(smooth[k]))  (the SmoothQuant input
+//                  transform, nanopointllm/compression/w8a8.py:351-359)
+//   quantization   per-token dynamic scale (w8a8.py:46-50, 106-115) or one
+//                  static scale (w8a8.py:94-103), quantize_symmetric
+//                  (w8a8.py:33-43)
+//
+// One workgroup per row; each thread keeps REG chunks of 8 elements in
+// registers between the reductions (sum of squares, absmax) and the writes,
+// so x is read once.  The sum of squares is a binary32 sum in the kernel's
+// own order (per thread, then a wavefront butterfly, then across wavefronts);
+// every other step is an exactly rounded elementwise operation.
+#include "w8a8_internal.h"
+
+namespace w8a8 {
+
+namespace {
+
+constexpr int kProThreads = 512;
+
+struct PrologueParams {
+  const void* x;
+  int64_t ldx;
+  const void* residual;
+  int64_t ld_res;
+  void* residual_out;
+  int64_t ld_res_out;
+  const void* norm_weight;  // TW [K] or null
+  float eps;
+  const void* smooth;       // TX [K] or null
+  const float* static_scale;  // one value, or null for a per-row scale
+  int64_t M;
+  int64_t K;
+  int8_t* q;
+  int64_t ldq;
+  float* scales_out;
+  void* x_out;  // TY [M, ld_xout] or null
+  int64_t ld_xout;
+};
+
+__device__ inline bool aligned16(const void* p) {
+  return (reinterpret_cast<uintptr_t>(p) & 15u) == 0;
+}
+
+template <typename T>
+__device__ inline float round_to(float v) {
+  return to_f32(from_f32<T>(v));
+}
+
+// Sum over the workgroup of one float per thread (every thread gets it).
+template <bool MAX>
+__device__ inline float block_reduce(float v, float* red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float o = __shfl_xor(v, off);
+    v = MAX ? fmaxf(v, o) : v + o;
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  __syncthreads();  // red[] may still be read from a previous reduction
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float r = red[0];
+#pragma unroll
+  for (int w = 1; w < kProThreads / 64; ++w) r = MAX ? fmaxf(r, red[w]) : r + red[w];
+  return r;
+}
+
+// TX: input / residual / smooth dtype (binary16 or bfloat16).  TW: RMSNorm
+// weight dtype (TX or float); TY = the row's dtype after the prologue (TX,
+// or float when TW is float).
+template <typename TX, typename TW, int REG>
+__global__ __launch_bounds__(kProThreads) void prologue_quant_kernel(PrologueParams p) {
+  using TY = TW;
+  __shared__ float red[kProThreads / 64];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int64_t K = p.K;
+  const TX* xr = static_cast<const TX*>(p.x) + row * p.ldx;
+
+  float v[REG][8];
+#pragma unroll
+  for (int c = 0; c < REG; ++c) {
+    const int64_t k0 = (tid + static_cast<int64_t>(c) * kProThreads) * 8;
+    const int valid = static_cast<int>(K - k0 < 8 ? (K - k0 > 0 ? K - k0 : 0) : 8);
+    load8(xr + k0, v[c], aligned16(xr + k0), valid);
+    if (p.residual != nullptr && valid > 0) {
+      const TX* rr = static_cast<const TX*>(p.residual) + row * p.ld_res + k0;
+      TX* ro = static_cast<TX*>(p.residual_out) + row * p.ld_res_out + k0;
+      float rv[8];
+      load8(rr, rv, aligned16(rr), valid);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (j < valid) {
+          const TX s = from_f32<TX>(v[c][j] + rv[j]);
+          ro[j] = s;
+          v[c][j] = to_f32(s);
+        }
+      }
+    }
+  }
+
+  if (p.norm_weight != nullptr) {
+    float ss = 0.0f;
+#pragma unroll
+    for (int c = 0; c < REG; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss = __fadd_rn(ss, __fmul_rn(v[c][j], v[c][j]));
+    ss = block_reduce<false>(ss, red);
+    const float var = ss / static_cast<float>(K);
+    const float rr = 1.0f / sqrtf(__fadd_rn(var, p.eps));
+    const TW* w = static_cast<const TW*>(p.norm_weight);
+#pragma unroll
+    for (int c = 0; c < REG; ++c) {
+      const int64_t k0 = (tid + static_cast<int64_t>(c) * kProThreads) * 8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (k0 + j < K) {
+          const float xn = round_to<TX>(__fmul_rn(v[c][j], rr));
+          v[c][j] = round_to<TY>(__fmul_rn(to_f32(w[k0 + j]), xn));
+        }
+      }
+    }
+  }
+
+  if (p.smooth != nullptr) {
+    const TX* sm = static_cast<const TX*>(p.smooth);
+#pragma unroll
+    for (int c = 0; c < REG; ++c) {
+      const int64_t k0 = (tid + static_cast<int64_t>(c) * kProThreads) * 8;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (k0 + j < K) v[c][j] = round_to<TY>(v[c][j] / to_f32(sm[k0 + j]));
+      }
+    }
+  }
+
+  float s;
+  if (p.static_scale != nullptr) {
+    s = *p.static_scale;
+  } else {
+    float amax = 0.0f;
+#pragma unroll
+    for (int c = 0; c < REG; ++c)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[c][j]));
+    s = scale_from_absmax(block_reduce<true>(amax, red));
+  }
+  const float r = 1.0f / s;
+  // The division-free quantizer needs 16-bit values and a binary16 scale.
+  const bool fast = sizeof(TY) == 2 && __half2float(__float2half_rn(s)) == s;
+  if (tid == 0 && p.scales_out != nullptr) p.scales_out[row] = s;
+
+#pragma unroll
+  for (int c = 0; c < REG; ++c) {
+    const int64_t k0 = (tid + static_cast<int64_t>(c) * kProThreads) * 8;
+    if (k0 >= K) continue;
+    int8_t* qr = p.q + row * p.ldq + k0;
+    TY* xo = p.x_out != nullptr ? static_cast<TY*>(p.x_out) + row * p.ld_xout + k0 : nullptr;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (k0 + j < K) {
+        qr[j] = static_cast<int8_t>(fast ? quant1_h(v[c][j], s, r) : quant1(v[c][j], s));
+        if (xo != nullptr) xo[j] = from_f32<TY>(v[c][j]);
+      }
+    }
+  }
+}
+
+template <typename TX, typename TW>
+hipError_t launch_reg(const PrologueParams& p, hipStream_t st) {
+  const int64_t per_pass = static_cast<int64_t>(kProThreads) * 8;
+  const dim3 grid(static_cast<unsigned>(p.M)), block(kProThreads);
+  if (p.K <= per_pass)
+    hipLaunchKernelGGL((prologue_quant_kernel<TX, TW, 1>), grid, block, 0, st, p);
+  else if (p.K <= 2 * per_pass)
+    hipLaunchKernelGGL((prologue_quant_kernel<TX, TW, 2>), grid, block, 0, st, p);
+  else if (p.K <= 4 * per_pass)
+    hipLaunchKernelGGL((prologue_quant_kernel<TX, TW, 4>), grid, block, 0, st, p);
+  else if (p.K <= 8 * per_pass)
+    hipLaunchKernelGGL((prologue_quant_kernel<TX, TW, 8>), grid, block, 0, st, p);
+  else
+    return hipErrorInvalidValue;
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int64_t prologue_max_k() { return static_cast<int64_t>(kProThreads) * 8 * 8; }
+
+hipError_t launch_prologue_quant(const void* x, int x_dtype, int64_t ldx, const void* residual,
+                                 int64_t ld_res, void* residual_out, int64_t ld_res_out,
+                                 const void* norm_weight, int w_dtype, float eps,
+                                 const void* smooth, const float* static_scale, int64_t M,
+                                 int64_t K, int8_t* q, int64_t ldq, float* scales_out,
+                                 void* x_out, int64_t ld_xout, hipStream_t st) {
+  PrologueParams p{x,          ldx, residual, ld_res, residual_out, ld_res_out, norm_weight,
+                   eps,        smooth, static_scale, M, K, q, ldq, scales_out, x_out,
+                   ld_xout};
+  if (M == 0 || K == 0) return hipSuccess;
+  const bool w32 = norm_weight != nullptr && w_dtype == kF32;
+  if (x_dtype == kF16)
+    return w32 ? launch_reg<__half, float>(p, st) : launch_reg<__half, __half>(p, st);
+  if (x_dtype == kBF16)
+    return w32 ? launch_reg<__hip_bfloat16, float>(p, st)
+               : launch_reg<__hip_bfloat16, __hip_bfloat16>(p, st);
+  return hipErrorInvalidValue;
+}
+
+}  // namespace w8a8

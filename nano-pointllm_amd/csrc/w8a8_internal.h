@@ -38,6 +38,21 @@ struct LinearOperands {
   int epi;
 };
 
+// Activation prologue (prologue.hip): per row of 16-bit x, optional
+// residual add (written to residual_out), RMSNorm with a weight of x's dtype
+// or F32 (w_dtype), division by a per-channel smooth scale of x's dtype, then
+// int8 quantization with a per-row dynamic or one static scale.  Row-major
+// q [M, ldq] (K columns), scales_out [M] (nullable), x_out [M, ld_xout]
+// (nullable) receives the rows before quantization (x's dtype, or F32 with
+// an F32 RMSNorm weight).  K <= prologue_max_k().
+int64_t prologue_max_k();
+hipError_t launch_prologue_quant(const void* x, int x_dtype, int64_t ldx, const void* residual,
+                                 int64_t ld_res, void* residual_out, int64_t ld_res_out,
+                                 const void* norm_weight, int w_dtype, float eps,
+                                 const void* smooth, const float* static_scale, int64_t M,
+                                 int64_t K, int8_t* q, int64_t ldq, float* scales_out,
+                                 void* x_out, int64_t ld_xout, hipStream_t st);
+
 // Elementwise epilogues over caller int32 accumulators acc[m, ld_acc]:
 // requant1 per element with per-column multiplier / shift / bias (nullable)
 // into int8 y, or dequant_bf16_exact with binary16 scale bit patterns

@@ -44,6 +44,7 @@ EXPORTED_SYMBOLS = (
     "w8a8_linear",
     "w8a8_linear_i8in",
     "w8a8_linear_i8in_requant",
+    "w8a8_prologue_quant",
     "w8a8_requantize_i32",
     "w8a8_dequant_i32_bf16",
 )
@@ -72,6 +73,8 @@ _SIGNATURES = {
                                 _int, _i64, _i64, _i64, _vp, _i64, _vp]),
     "w8a8_linear_i8in_requant": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                         _i64, _vp, _i64, _vp]),
+    "w8a8_prologue_quant": (_int, [_vp, _int, _i64, _vp, _i64, _vp, _i64, _vp, _int, _f32, _vp,
+                                   _vp, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp]),
     "w8a8_requantize_i32": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "w8a8_dequant_i32_bf16": (_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
 }

@@ -24,7 +24,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from .linear import W8A8GateUpSiluMul, W8A8Linear, W8A8MLP, W8A8PackedQKV
+from .linear import W8A8GateUpSiluMul, W8A8Linear, W8A8MLP, W8A8PackedQKV, W8A8RMSNormQuant
 
 _ATTN_LINEARS = ("q_proj", "k_proj", "v_proj", "o_proj")
 _MLP_LINEARS = ("gate_proj", "up_proj", "down_proj")
@@ -116,3 +116,33 @@ def packed_mlp_decode(hidden_states: torch.Tensor, mlp: W8A8MLP) -> torch.Tensor
 def gateup_silu_mul(hidden_states: torch.Tensor, gate_up: W8A8GateUpSiluMul) -> torch.Tensor:
     """Packed gate/up projection followed by ``act_fn(gate) * up``."""
     return gate_up(hidden_states)
+
+
+def rmsnorm_packed_qkv_decode(hidden_states: torch.Tensor, norm: nn.Module, qkv: W8A8PackedQKV
+                              ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``_rmsnorm_staged_packed_qkv_decode`` (llama/paged_attention.py:283-305):
+    RMSNorm of ``hidden_states[0]`` fused with its per-token quantization (one
+    kernel), then the packed QKV product on the int8 rows.  Returns q, k, v
+    views like the reference."""
+    rows = hidden_states[0] if hidden_states.dim() == 3 else hidden_states
+    if not rows.is_contiguous():
+        rows = rows.contiguous()
+    xq, sx = W8A8RMSNormQuant(norm)(rows)
+    return qkv.project_i8(xq, sx, out_dtype=rows.dtype)
+
+
+def residual_rmsnorm_mlp_decode(hidden_states: torch.Tensor, residual: torch.Tensor,
+                                norm: nn.Module, mlp: W8A8MLP
+                                ) -> tuple[torch.Tensor, torch.Tensor]:
+    """``post_attention_layernorm.residual_norm`` followed by the packed MLP
+    (llama/lightweight_runner.py:247-257, 320-383): the residual add, RMSNorm
+    and per-token quantization are one kernel; returns ``(residual, mlp_out)``
+    with the reference's ``[1, B, H]`` staging for 3-D inputs."""
+    three_d = hidden_states.dim() == 3
+    rows = hidden_states[0] if three_d else hidden_states
+    res = residual[0] if three_d else residual
+    summed, xq, sx = W8A8RMSNormQuant(norm).residual_norm(rows.contiguous(), res.contiguous())
+    out = mlp.forward_i8(xq, sx, out_dtype=rows.dtype)
+    if three_d:
+        return summed.unsqueeze(0), out.unsqueeze(0)
+    return summed, out

@@ -13,6 +13,9 @@ and replaces one of the reference's dense call sites:
   (``LightweightMLP`` packed branch, llama/lightweight_runner.py:320-358) in one
   kernel, with the interleaved weight layout of ``_pack_gateup_tensors``
   (:81-92).
+* :class:`W8A8RMSNormQuant`      - ``LightweightRMSNorm`` (:225-257) fused with the
+  per-token quantization of its output (the int8 rows feed the packed QKV /
+  MLP through ``project_i8`` / ``forward_i8``).
 * :class:`W8A8MLP`               - gate/up + SiLU*mul + down
   (``LightweightMLP.forward``, :320-383), optionally as an int8 chain where the
   gate/up epilogue requantizes ``h`` with a static (calibrated) scale and the
@@ -141,7 +144,16 @@ class W8A8PackedQKV(nn.Module):
                 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """``_project_qkv_decode_packed`` (paged_attention.py:97-115) semantics."""
         staged = hidden_states[0] if hidden_states.dim() == 3 else hidden_states
-        qkv = self.linear(staged)
+        return self._split(self.linear(staged))
+
+    def project_i8(self, xq: torch.Tensor, x_scale: torch.Tensor, *,
+                   out_dtype: torch.dtype = torch.float16
+                   ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """As :meth:`project` for int8 rows with per-row scales (the output of
+        the fused RMSNorm + quantization prologue)."""
+        return self._split(self.linear.forward_i8(xq, x_scale, out_dtype=out_dtype))
+
+    def _split(self, qkv: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         q_size = self.num_heads * self.head_dim
         kv_size = self.num_kv_heads * self.head_dim
         q, k, v = torch.split(qkv, (q_size, kv_size, kv_size), dim=-1)
@@ -183,6 +195,20 @@ class W8A8GateUpSiluMul(nn.Module):
         return _w.linear_dynamic(x, p.packed, p.scale, p.bias, p.out_features,
                                  epilogue=_lib.EPI_SILU_MUL_Q8, y_scale=h_scale)
 
+    def forward_i8(self, xq: torch.Tensor, x_scale: torch.Tensor, *,
+                   out_dtype: torch.dtype = torch.float16,
+                   h_scale: float | None = None) -> torch.Tensor:
+        """``SiLU(g) * u`` from int8 rows with per-row scales; with ``h_scale``
+        the result is requantized to int8 as in :meth:`forward_q8`."""
+        p = self.weight_q
+        if h_scale is None:
+            return _w.linear_i8in(xq, x_scale, p.packed, p.scale, p.bias, p.out_features,
+                                  epilogue=_lib.EPI_SILU_MUL, out_dtype=out_dtype,
+                                  inter_dtype=out_dtype)
+        return _w.linear_i8in(xq, x_scale, p.packed, p.scale, p.bias, p.out_features,
+                              epilogue=_lib.EPI_SILU_MUL_Q8, out_dtype=torch.int8,
+                              y_scale=h_scale, inter_dtype=out_dtype)
+
     def accumulators(self, x: torch.Tensor) -> torch.Tensor:
         """int32 accumulators in packed (interleaved) column order."""
         p = self.weight_q
@@ -213,3 +239,39 @@ class W8A8MLP(nn.Module):
         hq = self.gate_up.forward_q8(x, self.h_scale)
         s = torch.full((1,), self.h_scale, dtype=torch.float32, device=x.device)
         return self.down.forward_i8(hq, s, out_dtype=x.dtype)
+
+    def forward_i8(self, xq: torch.Tensor, x_scale: torch.Tensor, *,
+                   out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+        """The MLP on int8 rows with per-row scales (the output of the fused
+        residual-add + RMSNorm + quantization prologue)."""
+        if self.h_scale is None:
+            return self.down(self.gate_up.forward_i8(xq, x_scale, out_dtype=out_dtype))
+        hq = self.gate_up.forward_i8(xq, x_scale, out_dtype=out_dtype, h_scale=self.h_scale)
+        s = torch.full((1,), self.h_scale, dtype=torch.float32, device=xq.device)
+        return self.down.forward_i8(hq, s, out_dtype=out_dtype)
+
+
+class W8A8RMSNormQuant(nn.Module):
+    """``LightweightRMSNorm`` (lightweight_runner.py:225-257) fused with the
+    per-token int8 quantization of its output, for norms whose only consumer
+    is a W8A8 projection (input_layernorm -> packed QKV,
+    post_attention_layernorm -> packed gate/up).
+
+    ``forward(h) -> (xq, s_x)``; ``residual_norm(h, r) -> (h + r, xq, s_x)``.
+    The weight keeps the norm's dtype: a binary32 weight promotes the
+    normalized rows to binary32 before quantization, as torch does.
+    """
+
+    def __init__(self, norm: nn.Module) -> None:
+        super().__init__()
+        self.weight = norm.weight
+        self.variance_epsilon = float(getattr(norm, "variance_epsilon",
+                                              getattr(norm, "eps", 1.0e-6)))
+
+    def forward(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        return _w.rmsnorm_quant(hidden_states, self.weight, self.variance_epsilon)
+
+    def residual_norm(self, hidden_states: torch.Tensor, residual: torch.Tensor
+                      ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        return _w.rmsnorm_quant(hidden_states, self.weight, self.variance_epsilon,
+                                residual=residual)

@@ -9,7 +9,7 @@ and the trivial elementwise QDQ reconstruction (``q * s``).
 from __future__ import annotations
 
 from dataclasses import asdict, dataclass
-from typing import Any
+from typing import Any, NamedTuple
 
 import torch
 
@@ -208,6 +208,96 @@ def linear_i8in(xq: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor,
             float(y_scale), _lib.dtype_code(inter_dtype), m, n, k, ws.data_ptr(), ws.numel(),
             _lib.stream_handle(device)), "w8a8_linear_i8in")
     return y.reshape(*xq.shape[:-1], cols)
+
+
+class PrologueOutput(NamedTuple):
+    q: torch.Tensor                  # int8 [..., K]
+    scale: torch.Tensor              # f32 [...] per row (dynamic) or the static scale
+    residual: torch.Tensor | None    # x + residual, when a residual was given
+    rows: torch.Tensor | None        # the rows before quantization, when asked for
+
+
+def prologue_quant(x: torch.Tensor, *, norm_weight: torch.Tensor | None = None,
+                   eps: float = 1e-6, residual: torch.Tensor | None = None,
+                   smooth: torch.Tensor | None = None,
+                   static_scale: torch.Tensor | float | None = None,
+                   return_rows: bool = False) -> PrologueOutput:
+    """One pass per row of 16-bit ``x``: [x + residual] -> [RMSNorm with
+    ``norm_weight``] -> [/ ``smooth``] -> int8 quantization (per-row dynamic
+    scale, or ``static_scale``).  Each step follows its reference formula
+    (lightweight_runner.py:239-257, w8a8.py:351-359, 94-115)."""
+    device = _lib.require_cuda(x, norm_weight, residual, smooth)
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("the activation prologue takes float16 / bfloat16 rows")
+    x2, ldx = _rows_view(x)
+    m, k = x2.shape
+    res2 = res_out = None
+    ld_res = 0
+    if residual is not None:
+        if residual.shape != x.shape or residual.dtype != x.dtype:
+            raise ValueError("residual must match the hidden states' shape and dtype")
+        res2, ld_res = _rows_view(residual)
+        res_out = torch.empty((m, k), dtype=x.dtype, device=device)
+    w = None
+    w_code = _lib.dtype_code(x.dtype)
+    if norm_weight is not None:
+        w = norm_weight.detach().reshape(-1)
+        if w.numel() != k:
+            raise ValueError("RMSNorm weight must have one value per hidden channel")
+        if w.dtype not in (x.dtype, torch.float32):
+            w = w.to(x.dtype)
+        w = w.contiguous()
+        w_code = _lib.dtype_code(w.dtype)
+    sm = None
+    if smooth is not None:
+        sm = smooth.detach().reshape(-1).to(device=device, dtype=x.dtype).contiguous()
+        if sm.numel() != k:
+            raise ValueError("smoothing scales must have one value per input channel")
+    st = None
+    if static_scale is not None:
+        st = torch.as_tensor(static_scale, dtype=torch.float32, device=device).reshape(1)
+        if not bool(st[0] > 0):
+            raise ValueError("quantization scale must be positive")
+    q = torch.empty((m, k), dtype=torch.int8, device=device)
+    scales = torch.empty((m,), dtype=torch.float32, device=device) if st is None else None
+    rows = None
+    if return_rows:
+        rows_dtype = torch.float32 if (w is not None and w.dtype == torch.float32) else x.dtype
+        rows = torch.empty((m, k), dtype=rows_dtype, device=device)
+    if m and k:
+        _lib.check(_lib.load().w8a8_prologue_quant(
+            x2.data_ptr(), _lib.dtype_code(x.dtype), ldx, _lib.ptr(res2), ld_res,
+            _lib.ptr(res_out), k, _lib.ptr(w), w_code, float(eps), _lib.ptr(sm), _lib.ptr(st),
+            m, k, q.data_ptr(), k, _lib.ptr(scales), _lib.ptr(rows), k,
+            _lib.stream_handle(device)), "w8a8_prologue_quant")
+    lead = x.shape[:-1]
+    return PrologueOutput(
+        q.reshape(*lead, k),
+        scales.reshape(lead) if scales is not None else st.reshape(()),
+        None if res_out is None else res_out.reshape(x.shape),
+        None if rows is None else rows.reshape(*lead, k))
+
+
+def rmsnorm_quant(hidden_states: torch.Tensor, norm_weight: torch.Tensor, eps: float, *,
+                  residual: torch.Tensor | None = None):
+    """``LightweightRMSNorm`` (lightweight_runner.py:239-257) fused with the
+    per-token int8 quantization of its output.  Returns ``(xq, s_x)``, or
+    ``(summed, xq, s_x)`` with a residual, like ``residual_norm``."""
+    out = prologue_quant(hidden_states, norm_weight=norm_weight, eps=eps, residual=residual)
+    if residual is None:
+        return out.q, out.scale
+    return out.residual, out.q, out.scale
+
+
+def smoothquant_activation_qdq(values: torch.Tensor, smoothing: torch.Tensor, *,
+                               static_scale: torch.Tensor | float | None = None,
+                               ) -> tuple[torch.Tensor, torch.Tensor]:
+    """The SmoothQuant input hook's replacement (w8a8.py:351-362) on the GPU:
+    ``values / smoothing`` then static or per-token dynamic QDQ.  Returns
+    ``(qdq values, scale)``."""
+    out = prologue_quant(values, smooth=smoothing, static_scale=static_scale)
+    s = out.scale if static_scale is not None else out.scale.unsqueeze(-1)
+    return (out.q.float() * s).to(values.dtype), s
 
 
 # ------------------------------------------- reference-named contract functions

@@ -37,6 +37,15 @@ How each function is pinned (tests/test_oracle.py):
   (architecture_simulator/tests/test_gtsu_cycle.py:690-721).
 * ``pack_gateup_rows`` / ``pack_qkv_rows`` - packed == unpacked invariants
   (tests/test_lightweight_runner.py:132-200).
+* ``residual_add`` / ``smooth_divide`` - numpy's and torch's own 16-bit
+  arithmetic (convert to binary32, operate, round once) on random and
+  boundary values.
+* ``rmsnorm`` - a float64 restatement within one 16-bit ulp; bit equality on
+  inputs whose binary32 sum of squares is exact in any order; planted
+  mistakes (eps outside the square root, sum instead of mean, weight before
+  the rounding) fail.  The binary32 summation order of torch's CPU ``mean``
+  is not pinned: GPU parity for the normalization is by tolerance, and the
+  quantization of the GPU's own normalized rows is bit-exact.
 """
 from __future__ import annotations
 
@@ -378,6 +387,47 @@ def dequantize_int32_to_bf16(acc: int, sa_bits: int, sw_bits: int) -> int:
     if unbiased > 127:
         return (sign << 15) | 0x7F80
     return (sign << 15) | ((unbiased + 127) << 7) | (sig - 128)
+
+
+# --------------------------------------------------------------------------
+# activation prologue: residual add, RMSNorm, SmoothQuant divide
+# --------------------------------------------------------------------------
+def round16(values, dtype: str) -> np.ndarray:
+    """Round binary32 values to ``"f16"`` / ``"bf16"`` (RNE) and back."""
+    v = np.asarray(values, dtype=np.float32)
+    if dtype == "f16":
+        return v.astype(np.float16).astype(np.float32)
+    if dtype == "bf16":
+        return bf16_bits_to_f32(f32_to_bf16_bits(v)).reshape(v.shape)
+    raise ValueError(f"unsupported 16-bit dtype: {dtype}")
+
+
+def residual_add(hidden, residual, dtype: str) -> np.ndarray:
+    """``summed = hidden_states + residual`` on 16-bit tensors
+    (``LightweightRMSNorm.residual_norm``, llama/lightweight_runner.py:256)."""
+    return round16(np.asarray(hidden, np.float32) + np.asarray(residual, np.float32), dtype)
+
+
+def rmsnorm(hidden, weight, eps: float, dtype: str, *, weight_f32: bool = False) -> np.ndarray:
+    """``LightweightRMSNorm.forward`` (llama/lightweight_runner.py:239-245).
+
+    ``x = f32(h); x = x * rsqrt(mean(x**2) + eps); y = weight * x.to(dtype)``.
+    A 16-bit weight rounds ``y`` to ``dtype``; a binary32 weight promotes it
+    to binary32 (torch's type promotion).
+    """
+    x = np.asarray(hidden, np.float32)
+    var = np.sum(x * x, axis=-1, keepdims=True, dtype=np.float32) / np.float32(x.shape[-1])
+    r = np.float32(1.0) / np.sqrt(var + np.float32(eps))
+    xn = round16(x * r, dtype)
+    y = np.asarray(weight, np.float32) * xn
+    return y.astype(np.float32) if weight_f32 else round16(y, dtype)
+
+
+def smooth_divide(values, smoothing, dtype: str | None) -> np.ndarray:
+    """``values / smoothing.to(values.dtype)`` of the SmoothQuant input hook
+    (compression/w8a8.py:351-359); ``dtype`` None keeps binary32 values."""
+    out = np.asarray(values, np.float32) / np.asarray(smoothing, np.float32)
+    return out.astype(np.float32) if dtype is None else round16(out, dtype)
 
 
 # --------------------------------------------------------------------------

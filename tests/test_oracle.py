@@ -359,3 +359,93 @@ def test_tensor_error_metrics():
     e = O.tensor_error(ref, cand)
     assert math.isclose(e["max_abs"], 0.5)
     assert math.isclose(e["mean_abs"], (0.5 + 1e-9) / 3, rel_tol=1e-6)
+
+
+# ------------------------------------------------ activation prologue (f3/f4)
+def _ulp_distance16(a: np.ndarray, b: np.ndarray, dtype: str) -> np.ndarray:
+    """|a - b| in units in the last place of the 16-bit dtype (values are
+    exactly representable in it)."""
+    if dtype == "f16":
+        ia = a.astype(np.float16).view(np.int16).astype(np.int64)
+        ib = b.astype(np.float16).view(np.int16).astype(np.int64)
+    else:
+        ia = O.f32_to_bf16_bits(a).view(np.int16).astype(np.int64)
+        ib = O.f32_to_bf16_bits(b).view(np.int16).astype(np.int64)
+    key = lambda i: np.where(i < 0, -(i & 0x7FFF), i)
+    return np.abs(key(ia) - key(ib))
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_residual_add_and_smooth_divide_match_16bit_arithmetic(dtype):
+    import torch
+
+    rng = np.random.default_rng(1)
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    a = torch.from_numpy(rng.standard_normal(5000).astype(np.float32) * 30).to(tdt)
+    b = torch.from_numpy(rng.standard_normal(5000).astype(np.float32) * 0.01).to(tdt)
+    s = torch.from_numpy(np.exp(rng.uniform(-5, 5, 5000)).astype(np.float32)).to(tdt)
+    an, bn, sn = a.float().numpy(), b.float().numpy(), s.float().numpy()
+    np.testing.assert_array_equal(O.residual_add(an, bn, dtype), (a + b).float().numpy())
+    np.testing.assert_array_equal(O.smooth_divide(an, sn, dtype), (a / s).float().numpy())
+    np.testing.assert_array_equal(O.smooth_divide(an, sn, None), (a.float() / s.float()).numpy())
+
+
+def _rmsnorm_f64(x, w, eps, dtype):
+    """Float64 closed form rounded once to the 16-bit dtype per step the
+    reference rounds (x.to(dtype), then weight * x in dtype)."""
+    x64 = np.asarray(x, np.float64)
+    r = 1.0 / np.sqrt((x64 * x64).mean(axis=-1, keepdims=True) + eps)
+    xn = O.round16((x64 * r).astype(np.float32), dtype)
+    return O.round16(np.asarray(w, np.float64) * xn, dtype)
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_rmsnorm_within_one_ulp_of_float64_and_planted_mistakes_fail(dtype):
+    rng = np.random.default_rng(2)
+    x = O.round16(rng.standard_normal((6, 4096)).astype(np.float32) * 3, dtype)
+    x[0, :8] *= 60
+    w = O.round16(rng.uniform(0.2, 2.0, 4096).astype(np.float32), dtype)
+    eps = 1e-6
+    y = O.rmsnorm(x, w, eps, dtype)
+    ref = _rmsnorm_f64(x, w, eps, dtype)
+    # Only the binary32 rsqrt factor differs from the float64 chain, which
+    # flips a 16-bit rounding on very few elements.
+    assert _ulp_distance16(y, ref, dtype).max() <= 1
+    assert np.mean(y == ref) > 0.999
+
+    def eps_outside(x, w):
+        x = np.asarray(x, np.float32)
+        r = np.float32(1) / (np.sqrt(np.sum(x * x, -1, keepdims=True, dtype=np.float32)
+                                     / np.float32(x.shape[-1])) + np.float32(eps))
+        return O.round16(w * O.round16(x * r, dtype), dtype)
+
+    def sum_not_mean(x, w):
+        x = np.asarray(x, np.float32)
+        r = np.float32(1) / np.sqrt(np.sum(x * x, -1, keepdims=True, dtype=np.float32)
+                                    + np.float32(eps))
+        return O.round16(w * O.round16(x * r, dtype), dtype)
+
+    def weight_before_rounding(x, w):
+        x = np.asarray(x, np.float32)
+        r = np.float32(1) / np.sqrt(np.sum(x * x, -1, keepdims=True, dtype=np.float32)
+                                    / np.float32(x.shape[-1]) + np.float32(eps))
+        return O.round16(w * (x * r), dtype)
+
+    assert _ulp_distance16(sum_not_mean(x, w), ref, dtype).max() > 1
+    assert np.mean(weight_before_rounding(x, w) == ref) < 0.99
+    # eps placement only shows on rows whose mean square is near eps
+    xs = O.round16(np.full((1, 64), 1e-3, np.float32), dtype)
+    assert _ulp_distance16(eps_outside(xs, w[:64]), _rmsnorm_f64(xs, w[:64], eps, dtype),
+                           dtype).max() > 1
+    assert _ulp_distance16(O.rmsnorm(xs, w[:64], eps, dtype),
+                           _rmsnorm_f64(xs, w[:64], eps, dtype), dtype).max() <= 1
+
+
+def test_rmsnorm_binary32_weight_promotes_and_unit_weight_normalises():
+    rng = np.random.default_rng(3)
+    x = O.round16(rng.standard_normal((3, 1000)).astype(np.float32), "f16")
+    w32 = rng.uniform(0.5, 1.5, 1000).astype(np.float32)
+    y = O.rmsnorm(x, w32, 1e-6, "f16", weight_f32=True)
+    xn = O.rmsnorm(x, np.ones(1000, np.float32), 1e-6, "f16")
+    np.testing.assert_array_equal(y, w32 * xn)            # no 16-bit rounding of the product
+    np.testing.assert_allclose(np.mean(xn.astype(np.float64) ** 2, axis=-1), 1.0, rtol=2e-3)
