@@ -88,22 +88,43 @@ def _linear_parts(module: nn.Module) -> tuple[torch.Tensor, torch.Tensor | None]
 
 
 class W8A8Linear(nn.Module):
-    """``F.linear(x, W, b)`` with dynamic per-token A8 and per-output W8."""
+    """``F.linear(x, W, b)`` with A8 activations and per-output W8.
 
-    def __init__(self, weight: PackedW8A8Weight) -> None:
+    By default activations are quantized per token (dynamic).  A SmoothQuant
+    ``smooth`` vector [K] (the input smoothing scales of
+    ``apply_smoothquant_transform``, w8a8.py:373-414, applied to the weight
+    before it was quantized) makes the forward divide x by it first, and a
+    ``static_scale`` replaces the per-token scale (static A8, w8a8.py:94-103):
+    both run fused in the activation prologue kernel before the int8-in
+    product.
+    """
+
+    def __init__(self, weight: PackedW8A8Weight, *, smooth: torch.Tensor | None = None,
+                 static_scale: float | None = None) -> None:
         super().__init__()
         self.weight_q = weight
         self.in_features = weight.in_features
         self.out_features = weight.out_features
+        if smooth is not None and smooth.numel() != weight.in_features:
+            raise ValueError("smoothing scales must have one value per input channel")
+        if static_scale is not None and not static_scale > 0:
+            raise ValueError("quantization scale must be positive")
+        self.register_buffer("smooth", None if smooth is None else smooth.detach().reshape(-1))
+        self.static_scale = None if static_scale is None else float(static_scale)
 
     @classmethod
-    def from_linear(cls, linear: nn.Module) -> "W8A8Linear":
+    def from_linear(cls, linear: nn.Module, *, smooth: torch.Tensor | None = None,
+                    static_scale: float | None = None) -> "W8A8Linear":
         w, b = _linear_parts(linear)
-        return cls(PackedW8A8Weight.from_float(w, b))
+        return cls(PackedW8A8Weight.from_float(w, b), smooth=smooth, static_scale=static_scale)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         p = self.weight_q
-        return _w.linear_dynamic(x, p.packed, p.scale, p.bias, p.out_features)
+        if self.smooth is None and self.static_scale is None:
+            return _w.linear_dynamic(x, p.packed, p.scale, p.bias, p.out_features)
+        out = _w.prologue_quant(x, smooth=self.smooth, static_scale=self.static_scale)
+        return _w.linear_i8in(out.q, out.scale.reshape(-1), p.packed, p.scale, p.bias,
+                              p.out_features, out_dtype=x.dtype)
 
     def forward_i8(self, xq: torch.Tensor, x_scale: torch.Tensor,
                    out_dtype: torch.dtype = torch.float16) -> torch.Tensor:

@@ -358,6 +358,113 @@ def per_output_weight_qdq(weight: torch.Tensor
     return deq.to(weight.dtype), q.reshape_as(weight), scales
 
 
+def groupwise_weight_qdq(weight: torch.Tensor, *, group_size: int = 128
+                         ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """``groupwise_weight_qdq`` (w8a8.py:65-91): one scale per row and group of
+    ``group_size`` input columns (the last group may be shorter).  Returns
+    (dequant, int8, f32 scales [rows, groups]).  Each group is a strided
+    [rows, group] view quantized per row by the HIP kernel."""
+    if weight.dim() < 2:
+        raise ValueError("groupwise W8 expects at least two weight dimensions")
+    if group_size <= 0:
+        raise ValueError("group_size must be positive")
+    device = _lib.require_cuda(weight)
+    rows = weight.shape[0]
+    flat = weight.detach().reshape(rows, -1)
+    cols = flat.shape[1]
+    groups = (cols + group_size - 1) // group_size
+    q = torch.empty((rows, cols), dtype=torch.int8, device=device)
+    deq = torch.empty((rows, cols), dtype=weight.dtype, device=device)
+    scales = torch.empty((rows, groups), dtype=torch.float32, device=device)
+    full = cols // group_size
+    if full:
+        body = flat[:, : full * group_size].float().reshape(rows * full, group_size)
+        qb, sb = quant_rows(body)
+        q[:, : full * group_size] = qb.reshape(rows, full * group_size)
+        scales[:, :full] = sb.reshape(rows, full)
+    if full < groups:
+        qt, st = quant_rows(flat[:, full * group_size:].float())
+        q[:, full * group_size:] = qt
+        scales[:, full] = st
+    per_col = scales.repeat_interleave(group_size, dim=1)[:, :cols]
+    deq.copy_((q.float() * per_col).to(weight.dtype))
+    return deq.reshape(weight.shape), q.reshape(weight.shape), scales
+
+
+def tensor_error(reference: torch.Tensor, candidate: torch.Tensor) -> dict[str, float]:
+    """``_tensor_error`` (w8a8.py:254-262)."""
+    difference = candidate.float() - reference.float()
+    denominator = reference.float().abs().clamp_min(1e-8)
+    return {
+        "rmse": float(difference.square().mean().sqrt().item()),
+        "max_abs": float(difference.abs().max().item()),
+        "mean_abs": float(difference.abs().mean().item()),
+        "mean_relative_abs": float((difference.abs() / denominator).mean().item()),
+    }
+
+
+def compare_linear_bf16_qdq_integer(values: torch.Tensor, weight: torch.Tensor, *,
+                                    activation_scale: torch.Tensor,
+                                    bias: torch.Tensor | None = None) -> dict[str, Any]:
+    """``compare_linear_bf16_qdq_integer`` (w8a8.py:142-214) with the integer
+    path on the HIP kernels: native bf16, bf16 after QDQ, fp32 QDQ and the true
+    int32 path, the same report keys and metrics.  The float paths use torch
+    linears on the GPU in the reference's dtypes."""
+    if values.shape[-1] != weight.shape[1] or weight.dim() != 2:
+        raise ValueError("linear input/weight shapes do not match")
+    if weight.shape[1] * CONTRACT.symmetric_max ** 2 >= 1 << 31:
+        raise OverflowError("worst-case dot product exceeds signed INT32")
+    device = _lib.require_cuda(values, weight)
+    x = values.detach().float()
+    w = weight.detach().float()
+    b = None if bias is None else bias.detach().float().to(device)
+    scale = torch.as_tensor(activation_scale, device=device).detach().float()
+    qactivation = quantize_symmetric(x, scale)
+    dequant_weight, _, _ = per_output_weight_qdq(w)
+    dequant_activation = qactivation.float() * scale
+    out_shape = (*values.shape[:-1], weight.shape[0])
+
+    def linear(a, wt, bb):
+        # 2-D products only (plain matrix multiplies, no batched bf16 calls).
+        return torch.nn.functional.linear(a.reshape(-1, a.shape[-1]), wt, bb).reshape(out_shape)
+
+    fp32_reference = linear(x, w, b)
+    qdq_fp32 = linear(dequant_activation, dequant_weight, b)
+    bf16 = torch.bfloat16
+    bf16_reference = linear(x.to(bf16), w.to(bf16), None if b is None else b.to(bf16)).float()
+    qdq_bf16 = linear(dequant_activation.to(bf16), dequant_weight.to(bf16),
+                      None if b is None else b.to(bf16)).float()
+    integer, accumulator = integer_linear_per_output(x, w, activation_scale=scale, bias=b)
+    return {
+        "source_device": str(values.device),
+        "arithmetic_contract": {
+            "activation_quantization": "symmetric_per_tensor_int8",
+            "activation_scale_storage": CONTRACT.scale_storage,
+            "weight_quantization": "symmetric_per_output_int8",
+            "weight_scale_storage": CONTRACT.scale_storage,
+            "accumulation": CONTRACT.accumulator,
+            "dequantization_arithmetic": "float32",
+            "bias_present": b is not None,
+            "bias_application": CONTRACT.bias if b is not None else "none",
+            "output_dtype": "float32",
+        },
+        "shape": {"input": list(values.shape), "weight": list(weight.shape),
+                  "output": list(integer.shape)},
+        "accumulator_dtype": str(accumulator.dtype),
+        "accumulator_min": int(accumulator.min().item()),
+        "accumulator_max": int(accumulator.max().item()),
+        "worst_case_accumulator_bound": weight.shape[1] * CONTRACT.symmetric_max ** 2,
+        "int32_safe": True,
+        "metrics": {
+            "bf16_vs_fp32": tensor_error(fp32_reference, bf16_reference),
+            "qdq_bf16_vs_qdq_fp32": tensor_error(qdq_fp32, qdq_bf16),
+            "integer_vs_qdq_fp32": tensor_error(qdq_fp32, integer),
+            "integer_vs_qdq_bf16": tensor_error(qdq_bf16, integer),
+            "integer_vs_fp32": tensor_error(fp32_reference, integer),
+        },
+    }
+
+
 def integer_linear_per_output(values: torch.Tensor, weight: torch.Tensor, *,
                               activation_scale: torch.Tensor,
                               bias: torch.Tensor | None = None

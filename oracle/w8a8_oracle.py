@@ -37,6 +37,9 @@ How each function is pinned (tests/test_oracle.py):
   (architecture_simulator/tests/test_gtsu_cycle.py:690-721).
 * ``pack_gateup_rows`` / ``pack_qkv_rows`` - packed == unpacked invariants
   (tests/test_lightweight_runner.py:132-200).
+* ``groupwise_weight_qdq`` - two closed forms: a group of at least K columns
+  is ``per_output_weight_qdq``; a group of one column maps every weight with
+  |w| >= 127 * 2**-14 to +-127 and every smaller one to rint(w * 2**14).
 * ``residual_add`` / ``smooth_divide`` - numpy's and torch's own 16-bit
   arithmetic (convert to binary32, operate, round once) on random and
   boundary values.
@@ -88,6 +91,28 @@ def quantize_symmetric(values, scale) -> np.ndarray:
     v = np.asarray(values).astype(np.float32)
     q = np.rint(v / s)
     return np.clip(q, SYMMETRIC_MIN, SYMMETRIC_MAX).astype(np.int8)
+
+
+def groupwise_weight_qdq(weight, group_size: int = 128):
+    """``groupwise_weight_qdq`` (nanopointllm/compression/w8a8.py:65-91): one
+    scale per row and group of ``group_size`` columns (the last group may be
+    shorter).  Returns (dequant f32, int8, scales f32 [rows, groups])."""
+    w = np.asarray(weight, dtype=np.float32)
+    rows = w.shape[0]
+    flat = w.reshape(rows, -1)
+    cols = flat.shape[1]
+    groups = (cols + group_size - 1) // group_size
+    q = np.empty(flat.shape, np.int8)
+    deq = np.empty(flat.shape, np.float32)
+    scales = np.empty((rows, groups), np.float32)
+    for g in range(groups):
+        part = flat[:, g * group_size: min(cols, (g + 1) * group_size)]
+        s = scale_from_absmax(np.abs(part).max(axis=1))
+        q[:, g * group_size: g * group_size + part.shape[1]] = quantize_symmetric(part, s[:, None])
+        deq[:, g * group_size: g * group_size + part.shape[1]] = (
+            q[:, g * group_size: g * group_size + part.shape[1]].astype(np.float32) * s[:, None])
+        scales[:, g] = s
+    return deq.reshape(w.shape), q.reshape(w.shape), scales
 
 
 def static_activation_scale(absmax) -> np.ndarray:

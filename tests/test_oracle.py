@@ -449,3 +449,24 @@ def test_rmsnorm_binary32_weight_promotes_and_unit_weight_normalises():
     xn = O.rmsnorm(x, np.ones(1000, np.float32), 1e-6, "f16")
     np.testing.assert_array_equal(y, w32 * xn)            # no 16-bit rounding of the product
     np.testing.assert_allclose(np.mean(xn.astype(np.float64) ** 2, axis=-1), 1.0, rtol=2e-3)
+
+
+def test_groupwise_weight_qdq_closed_forms():
+    rng = np.random.default_rng(4)
+    w = (rng.standard_normal((9, 300)) * 0.05).astype(np.float32)
+    deq, q, s = O.groupwise_weight_qdq(w, group_size=1000)
+    pdeq, pq, ps = O.per_output_weight_qdq(w)
+    np.testing.assert_array_equal(q, pq)
+    np.testing.assert_array_equal(s[:, 0], ps)
+    np.testing.assert_array_equal(deq, pdeq)
+    deq1, q1, s1 = O.groupwise_weight_qdq(w, group_size=1)
+    assert s1.shape == (9, 300)
+    # |w| >= 127 * 2**-14 keeps the scale unclamped: every such weight maps to
+    # +-127; below it the scale clamps to 2**-14 and q = rint(w * 2**14).
+    big = np.abs(w) >= 127 * 2.0 ** -14
+    np.testing.assert_array_equal(np.abs(q1[big]), 127)
+    np.testing.assert_array_equal(q1[~big], np.rint(w[~big].astype(np.float64) * 2 ** 14))
+    np.testing.assert_array_equal(s1, O.scale_from_absmax(np.abs(w)))
+    _, q128, s128 = O.groupwise_weight_qdq(w, group_size=128)       # 128 + 128 + 44
+    assert s128.shape == (9, 3)
+    np.testing.assert_array_equal(q128[:, 256:], O.per_output_weight_qdq(w[:, 256:])[1])
