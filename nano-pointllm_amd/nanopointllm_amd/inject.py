@@ -44,13 +44,18 @@ def _attn_geometry(attn: nn.Module, q_proj: nn.Module) -> tuple[int, int, int]:
 
 
 def inject_w8a8(hf_model: nn.Module, *, h_scales: dict[int, float] | None = None,
-                pack: bool = True) -> dict[str, int]:
+                pack: bool = True, weight_cache=None, verify_source: bool = False
+                ) -> dict[str, int]:
     """Replace the decoder layers' projections with W8A8 modules (in place).
 
     ``h_scales`` optionally maps a layer index to a calibrated static scale for
     the SiLU*mul output, which turns that layer's packed MLP into the int8
-    chain (gate/up writes int8, down consumes it).  Returns counts of replaced
-    modules.  The model's weights must live on the GPU.
+    chain (gate/up writes int8, down consumes it).  ``weight_cache`` is a
+    directory of pre-quantized, pre-packed weights (``weight_cache.py``):
+    entries present are loaded (checksummed; ``verify_source`` also checks
+    them against the model's weights), missing ones are built and stored.
+    Returns counts of replaced modules.  The model's weights must live on the
+    GPU.
     """
     layers = hf_model.model.layers
     counts = {"linear": 0, "packed_qkv": 0, "packed_mlp": 0}
@@ -59,26 +64,33 @@ def inject_w8a8(hf_model: nn.Module, *, h_scales: dict[int, float] | None = None
         mlp = getattr(layer, "mlp", None)
         if attn is not None and all(hasattr(attn, n) for n in _ATTN_LINEARS):
             q, k, v = attn.q_proj, attn.k_proj, attn.v_proj
+            prefix = f"layers.{idx}.self_attn."
+            cache = dict(weight_cache=weight_cache, verify_source=verify_source)
             if pack and not isinstance(q, W8A8Linear):
                 heads, kv_heads, head_dim = _attn_geometry(attn, q)
                 attn.w8a8_qkv = W8A8PackedQKV(q, k, v, num_heads=heads, num_kv_heads=kv_heads,
-                                              head_dim=head_dim)
+                                              head_dim=head_dim, cache_key=prefix + "packed_qkv",
+                                              **cache)
                 counts["packed_qkv"] += 1
             for name in _ATTN_LINEARS:
                 mod = getattr(attn, name)
                 if not isinstance(mod, W8A8Linear):
-                    setattr(attn, name, W8A8Linear.from_linear(mod))
+                    setattr(attn, name, W8A8Linear.from_linear(mod, cache_key=prefix + name,
+                                                               **cache))
                     counts["linear"] += 1
         if mlp is not None and all(hasattr(mlp, n) for n in _MLP_LINEARS):
             g, u, d = mlp.gate_proj, mlp.up_proj, mlp.down_proj
+            prefix = f"layers.{idx}.mlp."
+            cache = dict(weight_cache=weight_cache, verify_source=verify_source)
             if pack and not isinstance(g, W8A8Linear):
                 scale = None if h_scales is None else h_scales.get(idx)
-                mlp.w8a8_mlp = W8A8MLP(g, u, d, h_scale=scale)
+                mlp.w8a8_mlp = W8A8MLP(g, u, d, h_scale=scale, cache_prefix=prefix, **cache)
                 counts["packed_mlp"] += 1
             for name in _MLP_LINEARS:
                 mod = getattr(mlp, name)
                 if not isinstance(mod, W8A8Linear):
-                    setattr(mlp, name, W8A8Linear.from_linear(mod))
+                    setattr(mlp, name, W8A8Linear.from_linear(mod, cache_key=prefix + name,
+                                                              **cache))
                     counts["linear"] += 1
     return counts
 

@@ -78,6 +78,14 @@ class PackedW8A8Weight:
         return cls.from_int8(q, s, bias, layout=layout)
 
 
+def _packed(build, source: torch.Tensor, weight_cache, cache_key: str, verify_source: bool):
+    if weight_cache is None:
+        return build()
+    from . import weight_cache as _wc
+    return _wc.cached(weight_cache, cache_key, build, source=source,
+                      verify_source=verify_source, device=source.device)
+
+
 def _interleave_halves(v: torch.Tensor) -> torch.Tensor:
     half = v.numel() // 2
     return torch.stack([v[:half], v[half:]], dim=1).reshape(-1)
@@ -114,9 +122,14 @@ class W8A8Linear(nn.Module):
 
     @classmethod
     def from_linear(cls, linear: nn.Module, *, smooth: torch.Tensor | None = None,
-                    static_scale: float | None = None) -> "W8A8Linear":
+                    static_scale: float | None = None, weight_cache=None, cache_key: str = "",
+                    verify_source: bool = False) -> "W8A8Linear":
+        """Quantize and pack ``linear``'s weight, or load it from the packed
+        weight cache directory ``weight_cache`` under ``cache_key``."""
         w, b = _linear_parts(linear)
-        return cls(PackedW8A8Weight.from_float(w, b), smooth=smooth, static_scale=static_scale)
+        packed = _packed(lambda: PackedW8A8Weight.from_float(w, b), w, weight_cache, cache_key,
+                         verify_source)
+        return cls(packed, smooth=smooth, static_scale=static_scale)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         p = self.weight_q
@@ -144,7 +157,8 @@ class W8A8PackedQKV(nn.Module):
     """Packed ``[Wq; Wk; Wv]`` projection (paged_attention.py:1242-1262)."""
 
     def __init__(self, q_proj: nn.Module, k_proj: nn.Module, v_proj: nn.Module, *,
-                 num_heads: int, num_kv_heads: int, head_dim: int) -> None:
+                 num_heads: int, num_kv_heads: int, head_dim: int, weight_cache=None,
+                 cache_key: str = "packed_qkv", verify_source: bool = False) -> None:
         super().__init__()
         parts = [_linear_parts(m) for m in (q_proj, k_proj, v_proj)]
         weight = torch.cat([w for w, _ in parts], dim=0)
@@ -153,7 +167,8 @@ class W8A8PackedQKV(nn.Module):
         else:
             bias = torch.cat([b if b is not None else w.new_zeros(w.shape[0])
                               for w, b in parts], dim=0)
-        self.linear = W8A8Linear(PackedW8A8Weight.from_float(weight, bias))
+        self.linear = W8A8Linear(_packed(lambda: PackedW8A8Weight.from_float(weight, bias),
+                                         weight, weight_cache, cache_key, verify_source))
         self.num_heads = num_heads
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
@@ -192,7 +207,8 @@ class W8A8GateUpSiluMul(nn.Module):
     (lightweight_runner.py:344-358).
     """
 
-    def __init__(self, gate_proj: nn.Module, up_proj: nn.Module) -> None:
+    def __init__(self, gate_proj: nn.Module, up_proj: nn.Module, *, weight_cache=None,
+                 cache_key: str = "packed_gate_up", verify_source: bool = False) -> None:
         super().__init__()
         (wg, bg), (wu, bu) = _linear_parts(gate_proj), _linear_parts(up_proj)
         weight = torch.cat([wg, wu], dim=0)
@@ -201,8 +217,9 @@ class W8A8GateUpSiluMul(nn.Module):
         else:
             bias = torch.cat([bg if bg is not None else wg.new_zeros(wg.shape[0]),
                               bu if bu is not None else wu.new_zeros(wu.shape[0])])
-        self.weight_q = PackedW8A8Weight.from_float(
-            weight, bias, layout=_lib.ROWS_INTERLEAVE_HALVES)
+        self.weight_q = _packed(
+            lambda: PackedW8A8Weight.from_float(weight, bias, layout=_lib.ROWS_INTERLEAVE_HALVES),
+            weight, weight_cache, cache_key, verify_source)
         self.intermediate = wg.shape[0]
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -248,10 +265,15 @@ class W8A8MLP(nn.Module):
     """
 
     def __init__(self, gate_proj: nn.Module, up_proj: nn.Module, down_proj: nn.Module, *,
-                 h_scale: float | None = None) -> None:
+                 h_scale: float | None = None, weight_cache=None, cache_prefix: str = "",
+                 verify_source: bool = False) -> None:
         super().__init__()
-        self.gate_up = W8A8GateUpSiluMul(gate_proj, up_proj)
-        self.down = W8A8Linear.from_linear(down_proj)
+        self.gate_up = W8A8GateUpSiluMul(gate_proj, up_proj, weight_cache=weight_cache,
+                                         cache_key=cache_prefix + "packed_gate_up",
+                                         verify_source=verify_source)
+        self.down = W8A8Linear.from_linear(down_proj, weight_cache=weight_cache,
+                                           cache_key=cache_prefix + "down_proj",
+                                           verify_source=verify_source)
         self.h_scale = h_scale
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -9,8 +9,9 @@ bytes, sha256}``.  The manifest is written with ``indent=2, sort_keys=True``
 and a trailing newline so a package written here hashes identically to one
 written by the reference.
 
-Host-side file I/O only (numpy + hashlib); :func:`to_device_weight` hands
-the int8 weight to the GPU kernels.
+The per-token variant (``PACKAGE_TYPE_PER_TOKEN``) keeps every file and key
+and stores one activation scale per row.  Host-side file I/O only (numpy +
+hashlib); :func:`to_device_weight` hands the int8 weight to the GPU kernels.
 """
 from __future__ import annotations
 
@@ -24,6 +25,10 @@ import numpy as np
 
 SCHEMA_VERSION = "1.0"
 PACKAGE_TYPE = "smoothquant_static_a8_per_output_w8_linear"
+# Per-token variant: the same files, with activation_scale.fp16 holding one
+# scale per activation row ([m]) - the dynamic per-token contract
+# (w8a8.py:106-115) that the reference's package cannot express.
+PACKAGE_TYPE_PER_TOKEN = "smoothquant_dynamic_per_token_a8_per_output_w8_linear"
 
 _FILES = {
     "activation": "activation.int8",
@@ -72,6 +77,21 @@ class QuantizedLinearTensors:
     def k(self) -> int:
         return int(self.weight.shape[1])
 
+    @property
+    def per_token(self) -> bool:
+        return self.metadata.get("package_type") == PACKAGE_TYPE_PER_TOKEN
+
+    def output_golden(self) -> np.ndarray:
+        """The binary32 linear output of the package's integer contract:
+        ``f32(acc) * s_a * s_w (+ bias)`` with s_a per tensor or per row."""
+        acc = self.integer_golden().astype(np.float32)
+        sa = self.activation_scale.astype(np.float32)
+        out = acc * (sa[:, None] if self.per_token else sa[0])
+        out = out * self.weight_scale.astype(np.float32)[None, :]
+        if self.bias is not None:
+            out = out + self.bias.astype(np.float32)[None, :]
+        return out.astype(np.float32)
+
     def integer_golden(self) -> np.ndarray:
         """Host int32 accumulators ``activation @ weight.T`` (exact)."""
         a = self.activation.astype(np.int64)
@@ -90,8 +110,12 @@ def _as_array(values, dtype: np.dtype, name: str, ndim: int) -> np.ndarray:
 
 def write_quantized_linear_package(directory, *, activation, weight, activation_scale,
                                    weight_scale, smooth_scale, output_scale=None, bias=None,
-                                   provenance: dict[str, Any] | None = None) -> dict[str, Any]:
-    """Write a schema-1.0 package and return its manifest."""
+                                   provenance: dict[str, Any] | None = None,
+                                   per_token: bool = False) -> dict[str, Any]:
+    """Write a schema-1.0 package and return its manifest.
+
+    ``per_token`` writes the per-token variant (``PACKAGE_TYPE_PER_TOKEN``):
+    ``activation_scale`` then holds one scale per activation row."""
     root = Path(directory)
     root.mkdir(parents=True, exist_ok=True)
     act = _as_array(activation, _I8, "activation", 2)
@@ -99,7 +123,9 @@ def write_quantized_linear_package(directory, *, activation, weight, activation_
     if act.shape[1] != wgt.shape[1]:
         raise ValueError("activation and weight K dimensions differ")
     a_scale = _as_array(np.asarray(activation_scale).reshape(-1), _F16, "activation_scale", 1)
-    if a_scale.shape != (1,):
+    if per_token and a_scale.shape != (act.shape[0],):
+        raise ValueError("activation_scale must contain one FP16 value per activation row")
+    if not per_token and a_scale.shape != (1,):
         raise ValueError("activation_scale must contain exactly one FP16 value")
     w_scale = _as_array(weight_scale, _F16, "weight_scale", 1)
     s_scale = _as_array(smooth_scale, _F16, "smooth_scale", 1)
@@ -140,15 +166,22 @@ def write_quantized_linear_package(directory, *, activation, weight, activation_
         }
     manifest = {
         "schema_version": SCHEMA_VERSION,
-        "package_type": PACKAGE_TYPE,
+        "package_type": PACKAGE_TYPE_PER_TOKEN if per_token else PACKAGE_TYPE,
         "shape": {"m": int(act.shape[0]), "n": int(wgt.shape[0]), "k": int(wgt.shape[1])},
-        "numerical_contract": dict(_NUMERICAL_CONTRACT),
+        "numerical_contract": _contract(per_token),
         "tensors": entries,
         "provenance": provenance or {},
     }
     (root / "metadata.json").write_text(json.dumps(manifest, indent=2, sort_keys=True) + "\n",
                                         encoding="utf-8")
     return manifest
+
+
+def _contract(per_token: bool) -> dict[str, str]:
+    contract = dict(_NUMERICAL_CONTRACT)
+    if per_token:
+        contract["activation"] = "symmetric_per_token_int8[-127,127]"
+    return contract
 
 
 def _read_entry(root: Path, name: str, entry: dict[str, Any]) -> np.ndarray:
@@ -170,6 +203,10 @@ def load_quantized_linear_package(directory) -> QuantizedLinearTensors:
     manifest = json.loads((root / "metadata.json").read_text(encoding="utf-8"))
     if manifest.get("schema_version") != SCHEMA_VERSION:
         raise ValueError("unsupported quantized tensor package schema")
+    package_type = manifest.get("package_type", PACKAGE_TYPE)
+    if package_type not in (PACKAGE_TYPE, PACKAGE_TYPE_PER_TOKEN):
+        raise ValueError(f"unsupported quantized tensor package type: {package_type}")
+    per_token = package_type == PACKAGE_TYPE_PER_TOKEN
     entries = manifest.get("tensors", {})
     missing = sorted(set(_REQUIRED) - set(entries))
     if missing:
@@ -181,8 +218,9 @@ def load_quantized_linear_package(directory) -> QuantizedLinearTensors:
         raise ValueError("activation shape does not match package shape")
     if arrays["weight"].shape != (n, k):
         raise ValueError("weight shape does not match package shape")
-    if arrays["activation_scale"].shape != (1,):
-        raise ValueError("activation_scale shape must be [1]")
+    if arrays["activation_scale"].shape != ((m,) if per_token else (1,)):
+        raise ValueError("activation_scale shape must be [m]" if per_token
+                         else "activation_scale shape must be [1]")
     if arrays["weight_scale"].shape != (n,):
         raise ValueError("weight_scale shape does not match N")
     if arrays["smooth_scale"].shape != (k,):

@@ -85,3 +85,41 @@ def test_rejects_bad_scales_and_truncation(tmp_path):
     (tmp_path / "activation.int8").write_bytes(b"\x00")
     with pytest.raises(ValueError, match="byte count mismatch"):
         load_quantized_linear_package(tmp_path)
+
+
+def test_per_token_variant_round_trip_and_golden(tmp_path):
+    """Per-token package type: the same files and keys, one activation scale
+    per row; the output golden applies each row's scale."""
+    from nanopointllm_amd.package import PACKAGE_TYPE_PER_TOKEN
+
+    sa = np.array([0.125, 0.5], np.float16)
+    manifest = _write(tmp_path, activation_scale=sa, per_token=True)
+    assert manifest["package_type"] == PACKAGE_TYPE_PER_TOKEN
+    assert manifest["numerical_contract"]["activation"] == "symmetric_per_token_int8[-127,127]"
+    assert manifest["tensors"]["activation_scale"]["shape"] == [2]
+    pkg = load_quantized_linear_package(tmp_path)
+    assert pkg.per_token
+    acc = np.array(PKG["derived_integer_golden"], np.float32)
+    ws = np.array(PKG["weight_scale"], np.float16).astype(np.float32)
+    exp = (acc * sa.astype(np.float32)[:, None]) * ws[None, :]
+    np.testing.assert_array_equal(pkg.output_golden(), exp.astype(np.float32))
+    # a static package's golden uses its single scale
+    static_dir = tmp_path / "static"
+    _write(static_dir)
+    spkg = load_quantized_linear_package(static_dir)
+    assert not spkg.per_token
+    np.testing.assert_array_equal(
+        spkg.output_golden(),
+        ((acc * np.float32(np.float16(PKG["activation_scale"]))) * ws[None, :]).astype(np.float32))
+
+
+def test_per_token_variant_rejects_wrong_scale_count_and_unknown_type(tmp_path):
+    with pytest.raises(ValueError, match="one FP16 value per activation row"):
+        _write(tmp_path, activation_scale=np.array([0.1], np.float16), per_token=True)
+    _write(tmp_path / "ok", activation_scale=np.array([0.1, 0.2], np.float16), per_token=True)
+    meta_path = tmp_path / "ok" / "metadata.json"
+    meta = json.loads(meta_path.read_text())
+    meta["package_type"] = "something_else"
+    meta_path.write_text(json.dumps(meta, indent=2, sort_keys=True) + "\n")
+    with pytest.raises(ValueError, match="unsupported quantized tensor package type"):
+        load_quantized_linear_package(tmp_path / "ok")
