@@ -55,12 +55,12 @@ __device__ inline void store8(int8_t* __restrict__ q, int64_t row, int64_t k0, i
 // row-major int8 row or as the row's slots of the packed tiles.  For packed
 // output the grid covers ceil(rows/16)*16 rows and every row writes all
 // ceil(K/64)*64 columns, so tile padding is zero-filled.
-template <typename TX, bool PACKED, bool DYNAMIC, int REG>
-__global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
+template <typename TX, bool PACKED, bool DYNAMIC, int REG, int NT>
+__global__ __launch_bounds__(NT) void quant_rows_kernel(
     const TX* __restrict__ x, int64_t ldx, int64_t rows, int64_t K, int vec_in,
     const float* __restrict__ scale_in, int64_t scale_stride, int8_t* __restrict__ q,
     int64_t ldq, int64_t ncols_out, int vec_out, int64_t KB, float* __restrict__ scales_out) {
-  __shared__ float red[kQuantThreads / 64];
+  __shared__ float red[NT / 64];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const bool live = row < rows;
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
   if constexpr (REG > 0) {
 #pragma unroll
     for (int c = 0; c < REG; ++c) {
-      const int64_t k0 = (tid + static_cast<int64_t>(c) * kQuantThreads) * 8;
+      const int64_t k0 = (tid + static_cast<int64_t>(c) * NT) * 8;
       const int64_t rem = K - k0;
       if (live && rem > 0) {
         load8(xr + k0, v[c], vec_in != 0, static_cast<int>(rem < 8 ? rem : 8));
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
 #pragma unroll
         for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(v[c][j]));
     } else if (live) {
-      for (int64_t c = tid; c < nchunk_in; c += kQuantThreads) {
+      for (int64_t c = tid; c < nchunk_in; c += NT) {
         float t[8];
         const int64_t k0 = c * 8;
         load8(xr + k0, t, vec_in != 0, static_cast<int>(K - k0 < 8 ? K - k0 : 8));
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
     __syncthreads();
     amax = red[0];
 #pragma unroll
-    for (int w = 1; w < kQuantThreads / 64; ++w) amax = fmaxf(amax, red[w]);
+    for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, red[w]);
     s = scale_from_absmax(amax);
   } else {
     if (live) s = scale_in[row * scale_stride];
@@ -118,7 +118,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
   if constexpr (REG > 0) {
 #pragma unroll
     for (int c = 0; c < REG; ++c) {
-      const int64_t chunk = tid + static_cast<int64_t>(c) * kQuantThreads;
+      const int64_t chunk = tid + static_cast<int64_t>(c) * NT;
       if (chunk < nchunk_out) {
         const int64_t k0 = chunk * 8;
         int32_t qi[8];
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(kQuantThreads) void quant_rows_kernel(
       }
     }
   } else {
-    for (int64_t c = tid; c < nchunk_out; c += kQuantThreads) {
+    for (int64_t c = tid; c < nchunk_out; c += NT) {
       const int64_t k0 = c * 8;
       const int64_t rem = K - k0;
       const int valid = live ? static_cast<int>(rem <= 0 ? 0 : (rem < 8 ? rem : 8)) : 0;
@@ -213,37 +213,62 @@ __global__ __launch_bounds__(256) void pad_rows_kernel(const int8_t* __restrict_
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline bool aligned8(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 7u) == 0; }
 
-template <typename TX, bool PACKED, bool DYN, int REG>
-void quant_launch_reg(dim3 g, dim3 b, hipStream_t st, const TX* x, int64_t ldx, int64_t rows,
+template <typename TX, bool PACKED, bool DYN, int REG, int NT>
+void quant_launch_reg(dim3 g, hipStream_t st, const TX* x, int64_t ldx, int64_t rows,
                       int64_t K, int vec_in, const float* scale_in, int64_t scale_stride,
                       int8_t* q, int64_t ldq, int64_t ncols_out, int vec_out, int64_t KB,
                       float* scales_out) {
-  hipLaunchKernelGGL((quant_rows_kernel<TX, PACKED, DYN, REG>), g, b, 0, st, x, ldx, rows, K,
-                     vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+  hipLaunchKernelGGL((quant_rows_kernel<TX, PACKED, DYN, REG, NT>), g, dim3(NT), 0, st, x, ldx,
+                     rows, K, vec_in, scale_in, scale_stride, q, ldq, ncols_out, vec_out, KB,
+                     scales_out);
 }
 
+template <typename TX, bool PACKED, bool DYN, int NT>
+void quant_launch_nt(dim3 g, hipStream_t st, int64_t chunks, const TX* x, int64_t ldx,
+                     int64_t rows, int64_t K, int vec_in, const float* scale_in,
+                     int64_t scale_stride, int8_t* q, int64_t ldq, int64_t ncols_out,
+                     int vec_out, int64_t KB, float* scales_out) {
+  const int64_t per = ceil_div(chunks, NT);
+#define W8A8_QUANT_REG(R)                                                                     \
+  quant_launch_reg<TX, PACKED, DYN, R, NT>(g, st, x, ldx, rows, K, vec_in, scale_in,          \
+                                           scale_stride, q, ldq, ncols_out, vec_out, KB,      \
+                                           scales_out)
+  if (per <= 1)
+    W8A8_QUANT_REG(1);
+  else if (per <= 2)
+    W8A8_QUANT_REG(2);
+  else if (per <= 4)
+    W8A8_QUANT_REG(4);
+  else if (per <= kRegChunksMax)
+    W8A8_QUANT_REG(kRegChunksMax);
+  else
+    W8A8_QUANT_REG(0);
+#undef W8A8_QUANT_REG
+}
+
+// Few rows (decode) leave most of the GPU idle, so each row's latency is what
+// counts: wide rows then get up to 1024 threads (16 wavefronts share each
+// CU's SIMDs and hide each other's load latency).  Many rows keep 256
+// threads per row.
 template <typename TX, bool PACKED, bool DYN>
-void quant_launch(dim3 g, dim3 b, hipStream_t st, int64_t chunks, const TX* x, int64_t ldx,
+void quant_launch(dim3 g, hipStream_t st, int64_t chunks, const TX* x, int64_t ldx,
                   int64_t rows, int64_t K, int vec_in, const float* scale_in,
                   int64_t scale_stride, int8_t* q, int64_t ldq, int64_t ncols_out, int vec_out,
                   int64_t KB, float* scales_out) {
-  const int64_t per = ceil_div(chunks, kQuantThreads);
-  if (per <= 1)
-    quant_launch_reg<TX, PACKED, DYN, 1>(g, b, st, x, ldx, rows, K, vec_in, scale_in,
-                                         scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
-  else if (per <= 2)
-    quant_launch_reg<TX, PACKED, DYN, 2>(g, b, st, x, ldx, rows, K, vec_in, scale_in,
-                                         scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
-  else if (per <= 4)
-    quant_launch_reg<TX, PACKED, DYN, 4>(g, b, st, x, ldx, rows, K, vec_in, scale_in,
-                                         scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
-  else if (per <= kRegChunksMax)
-    quant_launch_reg<TX, PACKED, DYN, kRegChunksMax>(g, b, st, x, ldx, rows, K, vec_in, scale_in,
-                                                     scale_stride, q, ldq, ncols_out, vec_out,
-                                                     KB, scales_out);
-  else
-    quant_launch_reg<TX, PACKED, DYN, 0>(g, b, st, x, ldx, rows, K, vec_in, scale_in,
-                                         scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
+  if constexpr (!PACKED) {
+    if (rows <= kGemvMaxRows && chunks > kQuantThreads) {
+      if (chunks > 2 * kQuantThreads)
+        return quant_launch_nt<TX, PACKED, DYN, 4 * kQuantThreads>(
+            g, st, chunks, x, ldx, rows, K, vec_in, scale_in, scale_stride, q, ldq, ncols_out,
+            vec_out, KB, scales_out);
+      return quant_launch_nt<TX, PACKED, DYN, 2 * kQuantThreads>(
+          g, st, chunks, x, ldx, rows, K, vec_in, scale_in, scale_stride, q, ldq, ncols_out,
+          vec_out, KB, scales_out);
+    }
+  }
+  quant_launch_nt<TX, PACKED, DYN, kQuantThreads>(g, st, chunks, x, ldx, rows, K, vec_in,
+                                                  scale_in, scale_stride, q, ldq, ncols_out,
+                                                  vec_out, KB, scales_out);
 }
 
 template <typename TX>
@@ -257,20 +282,20 @@ hipError_t quant_dispatch(const TX* x, int64_t ldx, int64_t rows, int64_t K,
   if (grid == 0) return hipSuccess;
   const int64_t chunks = packed ? KB * 8 : ceil_div(ncols_out > K ? ncols_out : K, 8);
   const bool dyn = scale_in == nullptr;
-  dim3 g(static_cast<unsigned>(grid)), b(kQuantThreads);
+  dim3 g(static_cast<unsigned>(grid));
   if (packed) {
     if (dyn)
-      quant_launch<TX, true, true>(g, b, st, chunks, x, ldx, rows, K, vec_in, scale_in,
+      quant_launch<TX, true, true>(g, st, chunks, x, ldx, rows, K, vec_in, scale_in,
                                    scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
     else
-      quant_launch<TX, true, false>(g, b, st, chunks, x, ldx, rows, K, vec_in, scale_in,
+      quant_launch<TX, true, false>(g, st, chunks, x, ldx, rows, K, vec_in, scale_in,
                                     scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
   } else {
     if (dyn)
-      quant_launch<TX, false, true>(g, b, st, chunks, x, ldx, rows, K, vec_in, scale_in,
+      quant_launch<TX, false, true>(g, st, chunks, x, ldx, rows, K, vec_in, scale_in,
                                     scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
     else
-      quant_launch<TX, false, false>(g, b, st, chunks, x, ldx, rows, K, vec_in, scale_in,
+      quant_launch<TX, false, false>(g, st, chunks, x, ldx, rows, K, vec_in, scale_in,
                                      scale_stride, q, ldq, ncols_out, vec_out, KB, scales_out);
   }
   return hipGetLastError();
