@@ -39,7 +39,6 @@ constexpr int kFusedCH = 4;
 constexpr int kBufferWord3 = 0x00020000;
 constexpr int kCacheNT = 2;
 constexpr int kBlockBytes = 1024;
-constexpr int kFusedRing = 3;  // register buffers (the main loop is unrolled by 3)
 constexpr int kFusedMaxRows = 8;
 constexpr int kFusedMaxKB = 192;  // K <= 12288
 constexpr int kFusedMaxBlocks = 64;  // 16-row output blocks per workgroup
@@ -136,8 +135,13 @@ __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
   }
 }
 
-template <int EPI, typename TX, typename TY, typename TH>
+// NCH: 16-byte x chunks each thread holds while quantizing (sized to the
+// shape, so small shapes keep their registers for the ring).  RING: register
+// buffers of the weight stream; RING - 1 steps are in flight, including
+// during the quantization prologue.
+template <int EPI, typename TX, typename TY, typename TH, int NCH, int RING>
 __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p) {
+  static_assert(NCH <= kFusedMaxChunks && RING >= 2, "fused kernel shape");
   // A fragments: [kb][g][row < 8][16 bytes]
   __shared__ __attribute__((aligned(16))) int8_t a_lds[kFusedMaxKB * 512];
   __shared__ int32_t red[2][kFusedWaves][256];
@@ -197,7 +201,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
     lc = wrap ? 0 : nc;
   };
 
-  i32x4 r0[kFusedCH], r1[kFusedCH], r2[kFusedCH];
+  i32x4 rb[RING][kFusedCH];
 
   // ---------------------------------------------------------- quantize x
   // Rows are spread over power-of-two groups of TPR >= 128 threads.
@@ -209,9 +213,9 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   const bool row_live = row < M;
   const uint16_t* xr =
       static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(row_live ? row : 0) * p.ldx;
-  u32x4 raw[kFusedMaxChunks];
+  u32x4 raw[NCH];
 #pragma unroll
-  for (int i = 0; i < kFusedMaxChunks; ++i) {
+  for (int i = 0; i < NCH; ++i) {
     const int c = j0 + i * tpr;
     if (row_live && c < nchunk && c * 8 < p.K) {
       raw[i] = *reinterpret_cast<const u32x4*>(xr + static_cast<int64_t>(c) * 8);
@@ -234,8 +238,8 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   }
   // The first weight loads go out after x and the operands (which they do not
   // depend on), so they stream while x is quantized.
-  issue(r0);
-  issue(r1);
+#pragma unroll
+  for (int u = 0; u < RING - 1; ++u) issue(rb[u]);
   if constexpr (EPI != kEpiI32) {
     if (op_j < n_mine) {
       ops_lds[op_j * 32 + (tid & 15)] = op_s;
@@ -244,7 +248,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   }
   uint32_t am = 0;
 #pragma unroll
-  for (int i = 0; i < kFusedMaxChunks; ++i) {
+  for (int i = 0; i < NCH; ++i) {
 #pragma unroll
     for (int q = 0; q < 4; ++q) am = max(am, max(abs_lo(raw[i][q]), abs_hi(raw[i][q])));
   }
@@ -265,14 +269,22 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
     const float s = row_s[row];
     const float r = 1.0f / s;
 #pragma unroll
-    for (int i = 0; i < kFusedMaxChunks; ++i) {
+    for (int i = 0; i < NCH; ++i) {
       const int c = j0 + i * tpr;
       if (c < nchunk) {
-        int32_t qi[8];
+        float xv[8];
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          qi[2 * q] = quant1_h(bits_to_f32<TX>(raw[i][q] & 0xffffu), s, r);
-          qi[2 * q + 1] = quant1_h(bits_to_f32<TX>(raw[i][q] >> 16), s, r);
+          xv[2 * q] = bits_to_f32<TX>(raw[i][q] & 0xffffu);
+          xv[2 * q + 1] = bits_to_f32<TX>(raw[i][q] >> 16);
+        }
+        int32_t qi[8];
+        if constexpr (NCH <= 4) {
+          quant8_dyn(xv, s, r, qi);
+        } else {
+          // Many chunks per thread leave no registers for the fast path.
+#pragma unroll
+          for (int j = 0; j < 8; ++j) qi[j] = quant1_h(xv[j], s, r);
         }
         const int k = c * 8;
         const int off = (((k >> 6) * 4 + ((k & 63) >> 4)) * 8 + row) * 16 + (k & 15);
@@ -316,10 +328,9 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
     j += last ? 1 : 0;
     c = last ? 0 : c + 1;
   };
-  for (int t = 0; t < total; t += kFusedRing) {
-    step(r0, r2, t);
-    step(r1, r0, t + 1);
-    step(r2, r1, t + 2);
+  for (int t = 0; t < total; t += RING) {
+#pragma unroll
+    for (int u = 0; u < RING; ++u) step(rb[u], rb[(u + RING - 1) % RING], t + u);
   }
 }
 
@@ -339,8 +350,18 @@ int cu_count() {
 
 template <int EPI, typename TX, typename TY, typename TH>
 hipError_t launch_f(const FusedParams& p, hipStream_t st) {
-  hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH>), dim3(p.G), dim3(kFusedThreads), 0, st,
-                     p);
+  // x chunks per thread: rows spread over 1024 / mpad(M) threads each.
+  const int mpad = p.M <= 1 ? 1 : (p.M <= 2 ? 2 : (p.M <= 4 ? 4 : 8));
+  const int per_thread = static_cast<int>(ceil_div(static_cast<int64_t>(p.KB) * 8,
+                                                   kFusedThreads / mpad));
+  const dim3 grid(p.G), block(kFusedThreads);
+  if (per_thread <= 2)
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 2, 3>), grid, block, 0, st, p);
+  else if (per_thread <= 4)
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 4, 3>), grid, block, 0, st, p);
+  else
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, kFusedMaxChunks, 3>), grid, block, 0,
+                       st, p);
   return hipGetLastError();
 }
 

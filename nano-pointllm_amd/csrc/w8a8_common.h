@@ -127,6 +127,28 @@ __device__ inline int32_t quant1_h(float x, float s, float r) {
   return static_cast<int32_t>(q);
 }
 
+// Quantizes 8 values with a dynamic row scale s (scale_from_absmax of the
+// row's |x|max, so |x / s| <= 127.07) and r = 1/s, exactly and faster than
+// quant1_h: rint(x * r) already rounds x / s correctly (ties to even) unless
+// x * r lies within 2^-15 of a half-integer, since |x*r - x/s| <= 127.07 *
+// 2^-23 < 2^-16 and x*r - rint(x*r) is exact.  When any lane of the
+// wavefront holds such a value the 8 values are redone with quant1_h (a
+// wave-uniform branch).  No clamp is needed: |rint(x * r)| <= 127.
+__device__ inline void quant8_dyn(const float (&x)[8], float s, float r, int32_t (&q)[8]) {
+  float dev = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float y = x[j] * r;
+    const float t = __builtin_rintf(y);
+    dev = fmaxf(dev, fabsf(y - t));
+    q[j] = static_cast<int32_t>(t);
+  }
+  if (__any(dev >= 0.5f - 0x1p-15f)) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = quant1_h(x[j], s, r);
+  }
+}
+
 __device__ inline uint32_t pack4_i8(int32_t a, int32_t b, int32_t c, int32_t d) {
   return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
          ((static_cast<uint32_t>(c) & 0xffu) << 16) | ((static_cast<uint32_t>(d) & 0xffu) << 24);

@@ -337,6 +337,31 @@ def test_fused_decode_path(cuda, m, n, k):
     np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
 
 
+@pytest.mark.parametrize("m", [1, 3, 8])
+def test_fused_decode_exact_ties(cuda, m):
+    """Integer activations with |x|max = 254 give s = 2, so half the values
+    are exact ties x/s = n + 1/2: the fused kernel's quantizer takes its exact
+    fallback on almost every chunk and must still round ties to even."""
+    from nanopointllm_amd import _lib, w8a8
+
+    n, k = 12288, 4096
+    g = torch.Generator().manual_seed(m)
+    x = torch.randint(-254, 255, (m, k), generator=g).float()
+    x[:, 0] = 254.0
+    x = x.to(torch.float16)
+    _, qw, sw = weight_q(n, k, seed=n + 3)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    swt = torch.from_numpy(sw).to(cuda)
+    note(f"fused decode ties m={m}")
+    rc, acc, sx = _linear_without_workspace(x.to(cuda), wp, swt, None, n, _lib.EPI_I32,
+                                            torch.int32)
+    assert rc == 0
+    xq, esx = O.dynamic_per_token_quant(x.float().numpy())
+    assert float(esx[0, 0]) == 2.0
+    np.testing.assert_array_equal(sx.cpu().numpy(), esx[:, 0])
+    np.testing.assert_array_equal(acc.cpu().numpy(), O.int32_matmul_f64(xq, qw))
+
+
 def test_fused_path_not_taken_for_small_shapes(cuda):
     """O-sized and tiny projections go through quantization + GEMV (they need a
     workspace) and give the same results."""
