@@ -12,7 +12,8 @@ once in a HIP graph and replayed.  Inputs are resident in HBM before timing.
 
 `value` = algorithmic HBM bytes of the step / step time (GB/s), with bytes =
 N*K + 2N + 2MK + 2M*N_out per linear.  The `roofline` object is for the
-dominant kernel (the packed gate/up GEMV with fused SiLU*mul), timed with HIP
+dominant kernel (the packed gate/up linear: per-token quantization, int8 GEMV and
+SiLU*mul in one kernel at M <= 8), timed with HIP
 events on the stream it is launched on.  `cpu_baseline` times the numpy
 restatement of the reference CPU integer path on a bounded sample (rank 0,
 N=1 only).  `extra` carries per-projection decode GB/s at M=1,4,8 and the
@@ -38,7 +39,7 @@ HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
 INT8_PEAK_TOPS = 5000.0      # MI355X dense int8 MFMA
 # Per-launch HBM traffic of the gate/up GEMV, from rocprofv3 FETCH_SIZE /
 # WRITE_SIZE runs of `bench.py --profile-gateup`, scaled by a copy kernel.
-TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_gateup_m8_traffic.json"
+TRAFFIC_SUMMARY = ROOT / "profiles" / "gemv_fused_gateup_m8_traffic.json"
 CALIBRATION_COPY_BYTES = 256 << 20
 
 
@@ -57,7 +58,7 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU sample")
     ap.add_argument("--profile-gateup", action="store_true",
-                    help="only the counter-calibration copy and the gate/up GEMV loop "
+                    help="only the counter-calibration copy and the gate/up linear loop "
                          "(the region rocprofv3 --pmc runs measure)")
     return ap.parse_args()
 
@@ -139,42 +140,54 @@ def event_time_ms(fn, reps: int) -> float:
 
 
 def gateup_kernel_roofline(layers, m: int, device) -> dict:
-    """Average duration of the gate/up GEMV kernel alone (int8-in, fused SiLU*mul)."""
+    """Average duration of the step's dominant launch, the packed gate/up
+    linear (binary16 x, fused SiLU*mul), over 32 layers x 20 repetitions,
+    bracketed by HIP events on the stream the kernels run on.  At decode sizes
+    it is one kernel (quantization fused into the GEMV); otherwise the
+    quantization and the GEMV launch are both counted."""
     import torch
 
     from nanopointllm_amd import _lib, w8a8, workloads as W
 
     spec = {p.name: p for p in W.PROJECTIONS}["gateup"]
-    xq, sx = w8a8.quant_rows(layers[0].x["gateup"])
+    x = layers[0].x["gateup"]
     outs = [torch.empty(m, spec.n // 2, dtype=torch.float16, device=device) for _ in layers]
-    ws = torch.empty(w8a8.workspace_bytes(m, spec.k), dtype=torch.uint8, device=device)
     lib = _lib.load()
     stream = _lib.stream_handle(device)
-    args = []
-    for layer, y in zip(layers, outs):
+
+    def call_args(layer, y, ws):
         p = layer.weights["gateup"]
-        args.append((xq.data_ptr(), spec.k, sx.data_ptr(), p.packed.data_ptr(), p.scale.data_ptr(),
-                     None, _lib.EPI_SILU_MUL, y.data_ptr(), _lib.F16, spec.n // 2, 0.0, _lib.F16,
-                     m, spec.n, spec.k, ws.data_ptr(), ws.numel(), stream))
+        return (x.data_ptr(), _lib.F16, spec.k, p.packed.data_ptr(), p.scale.data_ptr(), None,
+                _lib.EPI_SILU_MUL, y.data_ptr(), _lib.F16, spec.n // 2, 0.0, _lib.F16, m, spec.n,
+                spec.k, None, None if ws is None else ws.data_ptr(),
+                0 if ws is None else ws.numel(), stream)
+
+    ws = None
+    fused = lib.w8a8_linear(*call_args(layers[0], outs[0], None)) == _lib.OK
+    if not fused:
+        ws = torch.empty(w8a8.workspace_bytes(m, spec.k), dtype=torch.uint8, device=device)
+    args = [call_args(layer, y, ws) for layer, y in zip(layers, outs)]
 
     def run_all():
         for a in args:
-            rc = lib.w8a8_linear_i8in(*a)
+            rc = lib.w8a8_linear(*a)
             if rc:
-                _lib.check(rc, "w8a8_linear_i8in")
+                _lib.check(rc, "w8a8_linear")
 
     reps = 20
     ms = event_time_ms(run_all, reps) / len(args)
-    nbytes = W.algorithmic_bytes(m, spec.n, spec.k, silu=True, int8_in=True)
+    nbytes = W.algorithmic_bytes(m, spec.n, spec.k, silu=True)
     achieved = nbytes / (ms * 1e-3) / 1e9
     traffic = None
     if TRAFFIC_SUMMARY.exists():
         t = json.loads(TRAFFIC_SUMMARY.read_text())
-        if t.get("m") == m:
+        if t.get("m") == m and fused:
             traffic = t["hbm_bytes_per_launch"]
+    kernel = ("gemv_fused_kernel (packed gate/up: per-token quantization + int8 GEMV + "
+              "SiLU*mul, one launch)" if fused else
+              "quant_rows_kernel + gemv_kernel (packed gate/up, SiLU*mul)")
     return {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-            "kernel": "gemv_kernel (packed gate/up, SiLU*mul epilogue, int8 in)",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "kernel": kernel,
             "avg_launch_us": round(ms * 1e3, 3), "algorithmic_bytes_per_launch": nbytes}
 
 
