@@ -1,0 +1,166 @@
+"""A LLaMA decoder stack on the W8A8 kernels, in the shape of the reference's
+``LightweightLlamaLayer`` / ``LightweightLlamaRunner``
+(nanopointllm/llama/lightweight_runner.py:421-737).
+
+Per layer, every projection runs on int8 and every norm feeding one is fused
+with the quantization of its output:
+
+1. ``input_layernorm`` + per-token int8 quantization - one kernel
+   (``_rmsnorm_staged_packed_qkv_decode``, llama/paged_attention.py:283-305);
+2. packed ``[Wq; Wk; Wv]`` projection on the int8 rows, for decode and for
+   prefill alike (the reference's prefill runs three projections,
+   paged_attention.py:1349-1352; one packed product is the same numbers,
+   since quantization is per token and per output row);
+3. the attention core, supplied by the caller (rotary, KV cache and the
+   attention kernel are not part of the W8A8 path):
+   ``core(q [T, H, D], k [T, Hkv, D], v [T, Hkv, D], layer_index, state)``
+   returns the context ``[T, H * D]``;
+4. ``o_proj`` as a W8A8 linear (paged_attention.py:1376, 1488);
+5. residual add + ``post_attention_layernorm`` + int8 quantization - one
+   kernel (``residual_norm``, lightweight_runner.py:247-257);
+6. packed gate/up with the SiLU*mul epilogue, then down (binary16 ``h``, or
+   the int8 chain with a calibrated ``h`` scale) (lightweight_runner.py:320-383);
+7. the final residual add in the activation dtype, as the reference does.
+
+The stack is inference-only (no autograd).  Nothing on it synchronizes with
+the host or allocates outside torch's allocator, so a decode step can be
+captured into a HIP graph;
+:class:`DecodeGraphBucket` follows the reference's strict capture/replay
+wrapper (nanopointllm/engine/cuda_graph.py:17-52).
+"""
+from __future__ import annotations
+
+from typing import Any, Callable
+
+import torch
+import torch.nn as nn
+
+from .inject import inject_w8a8
+from .linear import W8A8Linear, W8A8MLP, W8A8PackedQKV, W8A8RMSNormQuant
+
+AttentionCore = Callable[[torch.Tensor, torch.Tensor, torch.Tensor, int, Any], torch.Tensor]
+
+
+def _rows(hidden_states: torch.Tensor) -> torch.Tensor:
+    """``[1, T, hidden]`` (the reference's flattened-token layout) or
+    ``[T, hidden]`` -> contiguous ``[T, hidden]``."""
+    if hidden_states.dim() == 3:
+        if hidden_states.shape[0] != 1:
+            raise ValueError("hidden states must be [1, tokens, hidden] or [tokens, hidden]")
+        hidden_states = hidden_states[0]
+    if hidden_states.dim() != 2:
+        raise ValueError("hidden states must be [1, tokens, hidden] or [tokens, hidden]")
+    return hidden_states if hidden_states.is_contiguous() else hidden_states.contiguous()
+
+
+class W8A8LlamaLayer(nn.Module):
+    """One decoder layer (lightweight_runner.py:421-560) on W8A8 projections.
+
+    ``hf_layer`` must already carry the W8A8 modules of :func:`inject_w8a8`
+    (``self_attn.w8a8_qkv``, a W8A8 ``self_attn.o_proj``, ``mlp.w8a8_mlp``).
+    """
+
+    def __init__(self, hf_layer: nn.Module, layer_index: int, attention_core: AttentionCore
+                 ) -> None:
+        super().__init__()
+        attn, mlp = hf_layer.self_attn, hf_layer.mlp
+        qkv = getattr(attn, "w8a8_qkv", None)
+        w8a8_mlp = getattr(mlp, "w8a8_mlp", None)
+        if not isinstance(qkv, W8A8PackedQKV) or not isinstance(attn.o_proj, W8A8Linear) \
+                or not isinstance(w8a8_mlp, W8A8MLP):
+            raise ValueError(f"layer {layer_index} has no W8A8 modules; run inject_w8a8 first")
+        self.layer_index = layer_index
+        self.input_layernorm = W8A8RMSNormQuant(hf_layer.input_layernorm)
+        self.post_attention_layernorm = W8A8RMSNormQuant(hf_layer.post_attention_layernorm)
+        self.qkv = qkv
+        self.o_proj = attn.o_proj
+        self.mlp = w8a8_mlp
+        self.attention_core = attention_core
+
+    @torch.no_grad()
+    def forward(self, hidden_states: torch.Tensor, attention_state: Any = None) -> torch.Tensor:
+        rows = _rows(hidden_states)
+        xq, sx = self.input_layernorm(rows)
+        q, k, v = self.qkv.project_i8(xq, sx, out_dtype=rows.dtype)
+        context = self.attention_core(q, k, v, self.layer_index, attention_state)
+        attn_out = self.o_proj(context)
+        residual, xq, sx = self.post_attention_layernorm.residual_norm(attn_out, rows)
+        out = residual + self.mlp.forward_i8(xq, sx, out_dtype=rows.dtype)
+        return out.unsqueeze(0) if hidden_states.dim() == 3 else out
+
+
+class W8A8LlamaRunner(nn.Module):
+    """``LightweightLlamaRunner`` (lightweight_runner.py:563-737) with W8A8
+    decoder layers: ``embed_tokens`` -> layers -> ``norm`` -> ``lm_head``.
+
+    The final norm and the LM head stay in the model's dtype (the LM head is
+    not a W8A8 linear in the reference either).  ``inject`` installs the W8A8
+    modules first (``h_scales`` and ``weight_cache`` as in :func:`inject_w8a8`).
+    """
+
+    def __init__(self, hf_model: nn.Module, attention_core: AttentionCore, *,
+                 inject: bool = True, h_scales: dict[int, float] | None = None,
+                 weight_cache=None) -> None:
+        super().__init__()
+        if inject:
+            inject_w8a8(hf_model, h_scales=h_scales, weight_cache=weight_cache)
+        model = hf_model.model if hasattr(hf_model, "model") else hf_model
+        self.hf_model = hf_model
+        self.embed_tokens = model.embed_tokens
+        self.layers = nn.ModuleList([W8A8LlamaLayer(layer, i, attention_core)
+                                     for i, layer in enumerate(model.layers)])
+        self.norm = model.norm
+        self.lm_head = hf_model.lm_head
+
+    @torch.no_grad()
+    def forward(self, input_ids: torch.Tensor | None = None, *,
+                inputs_embeds: torch.Tensor | None = None,
+                attention_state: Any = None) -> torch.Tensor:
+        if inputs_embeds is None:
+            if input_ids is None:
+                raise ValueError("input_ids or inputs_embeds is required")
+            hidden_states = self.embed_tokens(input_ids)
+        else:
+            hidden_states = inputs_embeds
+        for layer in self.layers:
+            hidden_states = layer(hidden_states, attention_state)
+        return self.lm_head(self.norm(hidden_states))
+
+
+class DecodeGraphBucket:
+    """Strict capture / replay of one fixed-shape decode step
+    (nanopointllm/engine/cuda_graph.py:17-52): ``capture(forward)`` warms the
+    kernels up twice, captures one call and returns its static output;
+    ``replay()`` reruns the captured kernels on whatever the static inputs
+    hold.  Errors propagate; there is no eager fallback."""
+
+    def __init__(self, device: torch.device | str = "cuda") -> None:
+        self.device = torch.device(device)
+        self.graph: torch.cuda.CUDAGraph | None = None
+        self.static_output: torch.Tensor | None = None
+
+    @property
+    def captured(self) -> bool:
+        return self.graph is not None
+
+    def capture(self, forward: Callable[[], torch.Tensor]) -> torch.Tensor:
+        if self.device.type != "cuda" or not torch.cuda.is_available():
+            raise RuntimeError("decode graph capture needs a GPU")
+        side = torch.cuda.Stream(self.device)
+        side.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                forward()
+        torch.cuda.current_stream(self.device).wait_stream(side)
+        torch.cuda.synchronize(self.device)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            out = forward()
+        self.graph, self.static_output = graph, out
+        return out
+
+    def replay(self) -> torch.Tensor:
+        if self.graph is None:
+            raise RuntimeError("decode graph bucket has not been captured")
+        self.graph.replay()
+        return self.static_output

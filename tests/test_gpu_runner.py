@@ -1,0 +1,268 @@
+"""The W8A8 decoder stack (runner.py) in the shape of LightweightLlamaRunner
+(nanopointllm/llama/lightweight_runner.py:421-737).
+
+Bars:
+* packed QKV on the prologue's int8 rows equals the three separate W8A8
+  projections, bit for bit (prefill uses the packed product instead of
+  paged_attention.py:1349-1352);
+* the runner equals the chain of its primitives bit for bit, and the same
+  rows give the same bits whether they run as one prefill batch (MFMA GEMM),
+  in decode chunks of 8 (GEMV) or one by one (fused decode kernel) when the
+  attention core is row-local;
+* every replay of a captured decode step equals the eager step for the same
+  input, with eager work and synchronizations between the replays;
+* end to end, the logits stay within the int8 quantization error of a dense
+  binary32 model with the same weights and attention (relative Frobenius
+  error below 5%, cosine above 0.998); a wiring mistake (missing residual,
+  k and v swapped) is far outside that.
+"""
+from __future__ import annotations
+
+import copy
+import sys
+
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+pytestmark = pytest.mark.gpu
+
+
+def note(msg):
+    sys.__stderr__.write(f"[gpu-case] {msg}\n")
+    sys.__stderr__.flush()
+
+
+class _RMSNorm(nn.Module):
+    """LightweightRMSNorm's formula (lightweight_runner.py:239-245)."""
+
+    def __init__(self, hidden, eps=1e-6):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden))
+        self.variance_epsilon = eps
+
+    def forward(self, x):
+        dtype = x.dtype
+        h = x.float()
+        var = h.pow(2).mean(-1, keepdim=True)
+        h = h * torch.rsqrt(var + self.variance_epsilon)
+        return self.weight * h.to(dtype)
+
+
+class _Attn(nn.Module):
+    def __init__(self, hidden, heads, kv_heads):
+        super().__init__()
+        self.num_heads, self.num_key_value_heads = heads, kv_heads
+        self.head_dim = hidden // heads
+        self.q_proj = nn.Linear(hidden, hidden, bias=False)
+        self.k_proj = nn.Linear(hidden, kv_heads * self.head_dim, bias=False)
+        self.v_proj = nn.Linear(hidden, kv_heads * self.head_dim, bias=False)
+        self.o_proj = nn.Linear(hidden, hidden, bias=False)
+
+
+class _MLP(nn.Module):
+    def __init__(self, hidden, inter):
+        super().__init__()
+        self.gate_proj = nn.Linear(hidden, inter, bias=False)
+        self.up_proj = nn.Linear(hidden, inter, bias=False)
+        self.down_proj = nn.Linear(inter, hidden, bias=False)
+
+
+class _Layer(nn.Module):
+    def __init__(self, hidden, heads, kv_heads, inter):
+        super().__init__()
+        self.input_layernorm = _RMSNorm(hidden)
+        self.self_attn = _Attn(hidden, heads, kv_heads)
+        self.post_attention_layernorm = _RMSNorm(hidden)
+        self.mlp = _MLP(hidden, inter)
+
+
+class _FakeLlama(nn.Module):
+    def __init__(self, hidden, heads, kv_heads, inter, vocab, layers):
+        super().__init__()
+        self.model = nn.Module()
+        self.model.embed_tokens = nn.Embedding(vocab, hidden)
+        self.model.layers = nn.ModuleList([_Layer(hidden, heads, kv_heads, inter)
+                                           for _ in range(layers)])
+        self.model.norm = _RMSNorm(hidden)
+        self.lm_head = nn.Linear(hidden, vocab, bias=False)
+
+
+def _model(cuda, *, hidden=256, heads=4, kv_heads=2, inter=384, vocab=512, layers=2, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    m = _FakeLlama(hidden, heads, kv_heads, inter, vocab, layers)
+    with torch.no_grad():
+        for name, p in m.named_parameters():
+            if name.endswith("norm.weight") or "layernorm" in name:
+                p.copy_(1.0 + 0.1 * torch.randn(p.shape, generator=g))
+            elif "embed" in name:
+                p.copy_(torch.randn(p.shape, generator=g))
+            else:
+                p.copy_(torch.randn(p.shape, generator=g) / p.shape[-1] ** 0.5)
+    return m.to(device=cuda, dtype=torch.float16)
+
+
+def _expand_kv(t, heads):
+    return t.repeat_interleave(heads // t.shape[1], dim=1)
+
+
+def causal_core(q, k, v, layer_index, state):
+    """Dense causal attention over the T rows, in binary32 with contiguous
+    2-D-per-head products, cast back to the activation dtype."""
+    t, heads, d = q.shape
+    qf = q.float().permute(1, 0, 2).contiguous()
+    kf = _expand_kv(k.float(), heads).permute(1, 2, 0).contiguous()      # [H, D, T]
+    vf = _expand_kv(v.float(), heads).permute(1, 0, 2).contiguous()
+    scores = torch.matmul(qf, kf) / d ** 0.5
+    mask = torch.ones(t, t, dtype=torch.bool, device=q.device).triu(1)
+    probs = scores.masked_fill(mask, float("-inf")).softmax(-1)
+    return torch.matmul(probs, vf).permute(1, 0, 2).reshape(t, heads * d).to(q.dtype)
+
+
+def rowlocal_core(q, k, v, layer_index, state):
+    """A row-local stand-in for attention: each row's context depends on its
+    own q, k and v only (so rows can be split across launches)."""
+    t, heads, d = q.shape
+    return (q + 0.5 * _expand_kv(k, heads) - _expand_kv(v, heads)).reshape(t, heads * d)
+
+
+def _dense_reference(weights, input_ids, core, heads):
+    """The same decoder in binary32 with the unquantized weights."""
+    W = {k: v.float() for k, v in weights.items()}
+
+    def norm(x, w):
+        return w * (x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + 1e-6))
+
+    x = W["model.embed_tokens.weight"][input_ids[0]]
+    i = 0
+    while f"model.layers.{i}.self_attn.q_proj.weight" in W:
+        p = f"model.layers.{i}."
+        h = norm(x, W[p + "input_layernorm.weight"])
+        q = (h @ W[p + "self_attn.q_proj.weight"].t()).view(h.shape[0], heads, -1)
+        k = (h @ W[p + "self_attn.k_proj.weight"].t()).view(h.shape[0], -1, q.shape[-1])
+        v = (h @ W[p + "self_attn.v_proj.weight"].t()).view(h.shape[0], -1, q.shape[-1])
+        x = x + core(q, k, v, i, None) @ W[p + "self_attn.o_proj.weight"].t()
+        h = norm(x, W[p + "post_attention_layernorm.weight"])
+        act = F.silu(h @ W[p + "mlp.gate_proj.weight"].t()) * (h @ W[p + "mlp.up_proj.weight"].t())
+        x = x + act @ W[p + "mlp.down_proj.weight"].t()
+        i += 1
+    return norm(x, W["model.norm.weight"]) @ W["lm_head.weight"].t()
+
+
+def _runner(model, core, **kw):
+    from nanopointllm_amd.runner import W8A8LlamaRunner
+    return W8A8LlamaRunner(model, core, **kw)
+
+
+@pytest.mark.parametrize("tokens", [5, 96])
+def test_packed_qkv_equals_three_projections(cuda, tokens):
+    from nanopointllm_amd import w8a8
+    from nanopointllm_amd.inject import inject_w8a8
+
+    model = _model(cuda)
+    inject_w8a8(model)
+    attn = model.model.layers[0].self_attn
+    x = torch.randn(tokens, 256, generator=torch.Generator().manual_seed(tokens)).half().to(cuda)
+    note(f"packed QKV vs q/k/v projections, T={tokens}")
+    xq, sx = w8a8.rmsnorm_quant(x, model.model.layers[0].input_layernorm.weight, 1e-6)
+    q, k, v = attn.w8a8_qkv.project_i8(xq, sx, out_dtype=torch.float16)
+    for packed, proj in ((q, attn.q_proj), (k, attn.k_proj), (v, attn.v_proj)):
+        sep = proj.forward_i8(xq, sx, out_dtype=torch.float16)
+        assert torch.equal(packed.reshape(tokens, -1), sep)
+
+
+@pytest.mark.parametrize("tokens", [3, 96])
+def test_runner_is_the_chain_of_its_primitives(cuda, tokens):
+    from nanopointllm_amd import w8a8
+
+    model = _model(cuda)
+    runner = _runner(model, causal_core)
+    ids = torch.randint(0, 512, (1, tokens), generator=torch.Generator().manual_seed(1)).to(cuda)
+    note(f"runner vs primitive chain, T={tokens}")
+    logits = runner(ids)
+    x = model.model.embed_tokens(ids)[0]
+    for i, layer in enumerate(model.model.layers):
+        xq, sx = w8a8.rmsnorm_quant(x, layer.input_layernorm.weight, 1e-6)
+        q, k, v = layer.self_attn.w8a8_qkv.project_i8(xq, sx, out_dtype=torch.float16)
+        a = layer.self_attn.o_proj(causal_core(q, k, v, i, None))
+        r, xq, sx = w8a8.rmsnorm_quant(a, layer.post_attention_layernorm.weight, 1e-6, residual=x)
+        x = r + layer.mlp.w8a8_mlp.forward_i8(xq, sx, out_dtype=torch.float16)
+    expect = model.lm_head(model.model.norm(x))
+    assert logits.shape == (1, tokens, 512)
+    assert torch.equal(logits[0], expect)
+
+
+@pytest.mark.parametrize("h_scale", [None, 0.05])
+def test_runner_within_quantization_error_of_dense_fp32(cuda, h_scale):
+    model = _model(cuda)
+    weights = {k: v.detach().clone() for k, v in model.state_dict().items()}
+    h_scales = None if h_scale is None else {0: h_scale, 1: h_scale}
+    runner = _runner(model, causal_core, h_scales=h_scales)
+    ids = torch.randint(0, 512, (1, 40), generator=torch.Generator().manual_seed(2)).to(cuda)
+    note(f"runner vs dense fp32, h_scale={h_scale}")
+    got = runner(ids)[0].float()
+    ref = _dense_reference(weights, ids, causal_core, heads=4)
+    rel = float((got - ref).norm() / ref.norm())
+    cos = float(F.cosine_similarity(got.flatten(), ref.flatten(), dim=0))
+    note(f"  rel {rel:.4f} cos {cos:.5f}")
+    assert rel < 0.05 and cos > 0.998
+
+    def swapped(q, k, v, i, s):
+        return causal_core(q, v, k, i, s)
+    bad = _dense_reference(weights, ids, swapped, heads=4)
+    assert float((bad - ref).norm() / ref.norm()) > 0.2     # the bar separates wiring mistakes
+
+
+@pytest.fixture(scope="module")
+def llama7b_layer(cuda):
+    """One decoder layer at LLaMA-7B sizes (hidden 4096, 32 heads, MLP
+    11008), so decode rows take the GEMV and fused decode kernels."""
+    return _model(cuda, hidden=4096, heads=32, kv_heads=32, inter=11008, vocab=256, layers=1,
+                  seed=7)
+
+
+def test_rows_give_the_same_bits_on_every_kernel_path(cuda, llama7b_layer):
+    model = copy.deepcopy(llama7b_layer)
+    runner = _runner(model, rowlocal_core)
+    x = torch.randn(1, 96, 4096, generator=torch.Generator().manual_seed(3)).half().to(cuda)
+    note("runner rows: prefill GEMM vs decode chunks of 8 vs single rows")
+    whole = runner(inputs_embeds=x)
+    chunks = torch.cat([runner(inputs_embeds=x[:, i:i + 8]) for i in range(0, 96, 8)], dim=1)
+    assert torch.equal(whole, chunks)
+    singles = torch.cat([runner(inputs_embeds=x[:, i:i + 1]) for i in range(0, 12)], dim=1)
+    assert torch.equal(whole[:, :12], singles)
+
+
+@pytest.mark.parametrize("rows", [1, 8])
+def test_decode_graph_replays_match_eager(cuda, llama7b_layer, rows):
+    from nanopointllm_amd.runner import DecodeGraphBucket
+
+    model = copy.deepcopy(llama7b_layer)
+    runner = _runner(model, rowlocal_core, h_scales={0: 0.02} if rows == 8 else None)
+    g = torch.Generator().manual_seed(rows)
+    inputs = [torch.randn(1, rows, 4096, generator=g).half().to(cuda) for _ in range(3)]
+    eager = [runner(inputs_embeds=x).clone() for x in inputs]
+    static = torch.zeros_like(inputs[0])
+    bucket = DecodeGraphBucket(cuda)
+    note(f"capture decode step, rows={rows}")
+    out = bucket.capture(lambda: runner(inputs_embeds=static))
+    for rep in range(2):
+        for x, e in zip(inputs, eager):
+            static.copy_(x)
+            got = bucket.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(got, e), f"replay {rep} differs from eager"
+            # eager work between replays
+            runner(inputs_embeds=inputs[0])
+    assert out is bucket.static_output
+
+
+def test_layer_requires_injection(cuda):
+    from nanopointllm_amd.runner import W8A8LlamaLayer
+
+    model = _model(cuda)
+    with pytest.raises(ValueError, match="inject_w8a8"):
+        W8A8LlamaLayer(model.model.layers[0], 0, causal_core)
+    with pytest.raises(ValueError, match="input_ids or inputs_embeds"):
+        _runner(model, causal_core)()
