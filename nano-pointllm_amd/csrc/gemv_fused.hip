@@ -34,6 +34,8 @@ namespace {
 constexpr int kFusedWaves = 16;
 constexpr int kFusedThreads = kFusedWaves * 64;
 constexpr int kFusedCH = 4;
+// Weight ring steps issued before x is quantized (the others follow it).
+constexpr int kFusedPreSteps = 1;
 // Raw buffer loads: descriptor word 3 of gfx9 (32-bit data format), the
 // nontemporal cache policy and the bytes of one 16 x 64 packed k-block.
 constexpr int kBufferWord3 = 0x00020000;
@@ -141,7 +143,8 @@ __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
 // during the quantization prologue.
 template <int EPI, typename TX, typename TY, typename TH, int NCH, int RING>
 __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p) {
-  static_assert(NCH <= kFusedMaxChunks && RING >= 2, "fused kernel shape");
+  static_assert(NCH <= kFusedMaxChunks && RING >= 2 && kFusedPreSteps < RING,
+                "fused kernel shape");
   // A fragments: [kb][g][row < 8][16 bytes]
   __shared__ __attribute__((aligned(16))) int8_t a_lds[kFusedMaxKB * 512];
   __shared__ int32_t red[2][kFusedWaves][256];
@@ -236,16 +239,6 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       if (p.bias != nullptr) op_b = p.bias[n];
     }
   }
-  // The first weight loads go out after x and the operands (which they do not
-  // depend on), so they stream while x is quantized.
-#pragma unroll
-  for (int u = 0; u < RING - 1; ++u) issue(rb[u]);
-  if constexpr (EPI != kEpiI32) {
-    if (op_j < n_mine) {
-      ops_lds[op_j * 32 + (tid & 15)] = op_s;
-      ops_lds[op_j * 32 + 16 + (tid & 15)] = op_b;
-    }
-  }
   uint32_t am = 0;
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
@@ -254,6 +247,21 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   }
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) am = max(am, static_cast<uint32_t>(__shfl_xor(static_cast<int>(am), off)));
+  // The first weight loads go out once x has arrived (the absmax above waits
+  // for it) and stream while x is quantized.  Only kFusedPreSteps steps go out
+  // before the quantization: a wave that issues more loads than the CU's
+  // memory pipeline holds stalls at the issue, which holds up the barriers of
+  // the quantization and with them the whole workgroup.  The rest of the ring
+  // is issued once the quantization is done.
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int u = 0; u < kFusedPreSteps; ++u) issue(rb[u]);
+  if constexpr (EPI != kEpiI32) {
+    if (op_j < n_mine) {
+      ops_lds[op_j * 32 + (tid & 15)] = op_s;
+      ops_lds[op_j * 32 + 16 + (tid & 15)] = op_b;
+    }
+  }
   if (lane == 0) amax_w[wave] = am;
   __syncthreads();
   if (tid < M) {
@@ -293,6 +301,8 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       }
     }
   }
+#pragma unroll
+  for (int u = kFusedPreSteps; u < RING - 1; ++u) issue(rb[u]);
   __syncthreads();
 
   // ------------------------------------------------------- stream weights
