@@ -7,8 +7,9 @@
 //
 // Design: a persistent grid of one 16-wavefront workgroup per CU.
 //   1. Each thread loads its x chunks and one epilogue operand (a weight scale
-//      or bias of this workgroup's output blocks, kept in LDS), then each
-//      wavefront issues its first weight loads (they do not depend on x).
+//      or bias of this workgroup's output blocks, kept in LDS); once x has
+//      arrived each wavefront issues its first step of weight loads (they do
+//      not depend on x).
 //   2. While those are in flight the workgroup quantizes all M rows of x into
 //      LDS (row absmax on the raw 16-bit patterns, binary16 scale, the
 //      division-free exact quantizer), laid out as half MFMA A fragments:
@@ -139,8 +140,8 @@ __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
 
 // NCH: 16-byte x chunks each thread holds while quantizing (sized to the
 // shape, so small shapes keep their registers for the ring).  RING: register
-// buffers of the weight stream; RING - 1 steps are in flight, including
-// during the quantization prologue.
+// buffers of the weight stream; RING - 1 steps are in flight in the main
+// loop, kFusedPreSteps of them during the quantization.
 template <int EPI, typename TX, typename TY, typename TH, int NCH, int RING>
 __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p) {
   static_assert(NCH <= kFusedMaxChunks && RING >= 2 && kFusedPreSteps < RING,
