@@ -221,6 +221,7 @@ hipError_t launch_gemv(const LinearOperands& op, hipStream_t st) {
   p.KB = static_cast<int>(ceil_div(op.K, kTileK));
   const int64_t nblocks = ceil_div(op.N, kTileRows);
   if (op.M <= 0 || nblocks == 0) return hipSuccess;
+  if (fused_gemv_i8_supported(op.M, op.N, op.K, op.lda, op.epi)) return launch_gemv_fused_i8(op, st);
   switch (op.epi) {
     case kEpiI32:
       return launch_mt<kEpiI32, int32_t, float>(p, nblocks, st);

@@ -26,6 +26,8 @@
 // Quantizing x once per CU costs M*K*~10 VALU ops per CU; for decode shapes
 // that hides behind the weight loads already in flight, and it saves the
 // separate quantization launch and its round trip through memory.
+#include <type_traits>
+
 #include "w8a8_internal.h"
 
 namespace w8a8 {
@@ -44,6 +46,7 @@ constexpr int kCacheNT = 2;
 constexpr int kBlockBytes = 1024;
 constexpr int kFusedMaxRows = 8;
 constexpr int kFusedMaxKB = 192;  // K <= 12288
+constexpr int kFusedI8MinKB = 129;  // int8 x: K > 8192
 constexpr int kFusedMaxBlocks = 64;  // 16-row output blocks per workgroup
 static_assert(kFusedMaxBlocks * 16 == kFusedThreads, "one epilogue operand per thread");
 // Max 16-byte x chunks a thread holds during quantization (1 row: 12288/8/1024).
@@ -58,6 +61,7 @@ struct FusedParams {
   void* y;
   int64_t ldy;
   float* sx_out;
+  const float* sx_in;  // int8 x: its per-row scales
   float out_scale;
   int M;
   int N;
@@ -146,6 +150,9 @@ template <int EPI, typename TX, typename TY, typename TH, int NCH, int RING>
 __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p) {
   static_assert(NCH <= kFusedMaxChunks && RING >= 2 && kFusedPreSteps < RING,
                 "fused kernel shape");
+  // TX = int8_t: x comes quantized, with per-row scales (no quantization).
+  constexpr bool kI8 = std::is_same<TX, int8_t>::value;
+  static_assert(kFusedMaxKB * 4 <= kFusedThreads, "one int8 x chunk per thread and row");
   // A fragments: [kb][g][row < 8][16 bytes]
   __shared__ __attribute__((aligned(16))) int8_t a_lds[kFusedMaxKB * 512];
   __shared__ int32_t red[2][kFusedWaves][256];
@@ -207,6 +214,72 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
 
   i32x4 rb[RING][kFusedCH];
 
+  // The epilogue operands of all this workgroup's blocks (n_mine <= 64, one
+  // per thread) go to LDS up front: vmcnt counts loads in issue order, so a
+  // scale loaded at epilogue time would wait for every weight load in flight.
+  float op_s = 0.0f, op_b = 0.0f;
+  const int op_j = tid >> 4;
+  auto load_ops = [&]() {
+    if constexpr (EPI != kEpiI32) {
+      const int64_t n =
+          (static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(op_j) * p.G) * 16 + (tid & 15);
+      if (op_j < n_mine && n < p.N) {
+        op_s = p.sw[n];
+        if (p.bias != nullptr) op_b = p.bias[n];
+      }
+    }
+  };
+  auto store_ops = [&]() {
+    if constexpr (EPI != kEpiI32) {
+      if (op_j < n_mine) {
+        ops_lds[op_j * 32 + (tid & 15)] = op_s;
+        ops_lds[op_j * 32 + 16 + (tid & 15)] = op_b;
+      }
+    }
+  };
+
+  if constexpr (kI8) {
+    // ------------------------------------------------ stage int8 x in LDS
+    // x is int8 [M, ldx] (M * ldx < 2^30), rows 16-byte aligned and readable
+    // (zero past K) up to KB*64 bytes, with per-row scales: each 16-byte
+    // chunk goes straight to its slot of the A fragments.  A row has
+    // KB*4 <= 768 chunks, so a thread takes at most one chunk of each row.
+    // Branch-free buffer loads: the descriptor range ends after row M-1's
+    // KB*64 bytes, so rows past M read zeros without a memory access (and a
+    // conditional load here would let the compiler wait on each load in turn).
+    const int cpr = KB * 4;
+    const bool chunk_live = tid < cpr;
+    const int xrec = __builtin_amdgcn_readfirstlane(static_cast<int>((M - 1) * p.ldx) + KB * 64);
+    const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(p.x), 0, xrec, kBufferWord3);
+    const int ldx = static_cast<int>(p.ldx);
+    i32x4 v[kFusedMaxRows];
+#pragma unroll
+    for (int r = 0; r < kFusedMaxRows; ++r) {
+      v[r] = __builtin_bit_cast(
+          i32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, r * ldx + tid * 16, 0, 0));
+    }
+    load_ops();
+    float sxr = 0.0f;
+    // The int32 epilogue has no scales (and may be given none).
+    if constexpr (EPI != kEpiI32) {
+      if (tid < M) sxr = p.sx_in[tid];
+    }
+    // With nothing to compute on x, the weight stream starts right behind
+    // the x loads; the LDS stores below wait for x only.
+#pragma unroll
+    for (int u = 0; u < RING - 1; ++u) issue(rb[u]);
+    __builtin_amdgcn_sched_barrier(0);
+    if (tid < M) row_s[tid] = sxr;
+    const int k = tid * 16;
+    const int off0 = ((k >> 6) * 4 + ((k & 63) >> 4)) * 8 * 16;
+#pragma unroll
+    for (int r = 0; r < kFusedMaxRows; ++r) {
+      if (r < M && chunk_live) *reinterpret_cast<i32x4*>(a_lds + off0 + r * 16) = v[r];
+    }
+    store_ops();
+    __syncthreads();
+  } else {
   // ---------------------------------------------------------- quantize x
   // Rows are spread over power-of-two groups of TPR >= 128 threads.
   const int mpad = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
@@ -227,19 +300,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       raw[i] = u32x4{0u, 0u, 0u, 0u};
     }
   }
-  // The epilogue operands of all this workgroup's blocks (n_mine <= 64, one
-  // per thread) go to LDS up front: vmcnt counts loads in issue order, so a
-  // scale loaded at epilogue time would wait for every weight load in flight.
-  float op_s = 0.0f, op_b = 0.0f;
-  const int op_j = tid >> 4;
-  if constexpr (EPI != kEpiI32) {
-    const int64_t n =
-        (static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(op_j) * p.G) * 16 + (tid & 15);
-    if (op_j < n_mine && n < p.N) {
-      op_s = p.sw[n];
-      if (p.bias != nullptr) op_b = p.bias[n];
-    }
-  }
+  load_ops();
   uint32_t am = 0;
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
@@ -257,12 +318,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int u = 0; u < kFusedPreSteps; ++u) issue(rb[u]);
-  if constexpr (EPI != kEpiI32) {
-    if (op_j < n_mine) {
-      ops_lds[op_j * 32 + (tid & 15)] = op_s;
-      ops_lds[op_j * 32 + 16 + (tid & 15)] = op_b;
-    }
-  }
+  store_ops();
   if (lane == 0) amax_w[wave] = am;
   __syncthreads();
   if (tid < M) {
@@ -305,6 +361,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
 #pragma unroll
   for (int u = kFusedPreSteps; u < RING - 1; ++u) issue(rb[u]);
   __syncthreads();
+  }
 
   // ------------------------------------------------------- stream weights
   const bool a_live = li < M;
@@ -366,7 +423,9 @@ hipError_t launch_f(const FusedParams& p, hipStream_t st) {
   const int per_thread = static_cast<int>(ceil_div(static_cast<int64_t>(p.KB) * 8,
                                                    kFusedThreads / mpad));
   const dim3 grid(p.G), block(kFusedThreads);
-  if (per_thread <= 2)
+  if constexpr (std::is_same<TX, int8_t>::value) {
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 1, 3>), grid, block, 0, st, p);
+  } else if (per_thread <= 2)
     hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 2, 3>), grid, block, 0, st, p);
   else if (per_thread <= 4)
     hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 4, 3>), grid, block, 0, st, p);
@@ -434,6 +493,7 @@ hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const Line
   p.y = op.y;
   p.ldy = op.ldy;
   p.sx_out = sx_out;
+  p.sx_in = nullptr;
   p.out_scale = op.out_scale;
   p.M = static_cast<int>(op.M);
   p.N = static_cast<int>(op.N);
@@ -445,6 +505,47 @@ hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const Line
   if (x_dtype == kF16) return dispatch_f<__half>(p, op.epi, op.y_dtype, op.h_dtype, st);
   if (x_dtype == kBF16) return dispatch_f<__hip_bfloat16>(p, op.epi, op.y_dtype, op.h_dtype, st);
   return hipErrorInvalidValue;
+}
+
+// int8 activations (already quantized, per-row scales): the same persistent
+// weight stream without the quantization.  It pays where each wavefront
+// streams several ring steps per block: for K > 8192 it beats gemv_kernel
+// (LLaMA-7B down at M = 1..8: 10.7-10.9 us against 11.2-11.7 us per launch),
+// while for K = 4096 the staging of x before the first step costs more than
+// the stream gains (O at M = 8: 7.1 against 5.3 us; the x loads wait behind
+// every CU's first weight requests).  Also M <= 8, K <= 12288, at most 64
+// output blocks per workgroup, rows of at most 2^30 / M bytes, and the
+// dequant / SiLU*mul / int8-requant epilogues.
+bool fused_gemv_i8_supported(int64_t M, int64_t N, int64_t K, int64_t lda, int epi) {
+  const int64_t kb = ceil_div(K, kTileK);
+  if (!(M >= 1 && M <= kFusedMaxRows && kb >= kFusedI8MinKB && kb <= kFusedMaxKB &&
+        epi <= kEpiSiluQ8 && lda >= kb * kTileK && M * lda < (int64_t{1} << 30)))
+    return false;
+  const int64_t nb = ceil_div(N, kTileRows);
+  const int64_t g = nb < cu_count() ? nb : cu_count();
+  return nb >= 1 && ceil_div(nb, g) <= kFusedMaxBlocks;
+}
+
+hipError_t launch_gemv_fused_i8(const LinearOperands& op, hipStream_t st) {
+  FusedParams p;
+  p.x = op.a;
+  p.ldx = op.lda;
+  p.w = reinterpret_cast<const i32x4*>(op.w);
+  p.sw = op.sw;
+  p.bias = op.bias;
+  p.y = op.y;
+  p.ldy = op.ldy;
+  p.sx_out = nullptr;
+  p.sx_in = op.sx;
+  p.out_scale = op.out_scale;
+  p.M = static_cast<int>(op.M);
+  p.N = static_cast<int>(op.N);
+  p.K = static_cast<int>(op.K);
+  p.KB = static_cast<int>(ceil_div(op.K, kTileK));
+  p.NB = static_cast<int>(ceil_div(op.N, kTileRows));
+  p.G = static_cast<int>(p.NB < cu_count() ? p.NB : cu_count());
+  if (p.NB == 0 || p.M == 0) return hipSuccess;
+  return dispatch_f<int8_t>(p, op.epi, op.y_dtype, op.h_dtype, st);
 }
 
 }  // namespace w8a8

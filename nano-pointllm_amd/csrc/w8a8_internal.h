@@ -92,6 +92,10 @@ constexpr int64_t kGemvMaxRows = 64;
 // N <= 1024 * CUs, and enough weight bytes per CU to hide the quantization.
 bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
                           int64_t K);
+// The fused kernel's weight stream on int8 activations (op.a row-major as for
+// the GEMV, op.sx per-row scales); decode shapes only.
+bool fused_gemv_i8_supported(int64_t M, int64_t N, int64_t K, int64_t lda, int epi);
+hipError_t launch_gemv_fused_i8(const LinearOperands& op, hipStream_t st);
 hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const LinearOperands& op,
                              float* sx_out, hipStream_t st);
 
