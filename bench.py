@@ -56,7 +56,7 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-extra", action="store_true", help="skip the per-projection sweeps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-layers", type=int, default=2, help="layers in the CPU sample")
+    ap.add_argument("--cpu-layers", type=int, default=16, help="layers in the CPU sample (~10 s)")
     ap.add_argument("--profile-gateup", action="store_true",
                     help="only the counter-calibration copy and the gate/up linear loop "
                          "(the region rocprofv3 --pmc runs measure)")
