@@ -17,6 +17,8 @@ MLP chain (``inject_w8a8(h_scales=...)``).
   reference's report (w8a8.py:417-447).
 * :func:`apply_smoothquant_transform` - exact ``x/s, W*s`` smoothing and the
   post-transform static scales (w8a8.py:370-414).
+* :func:`smoothquant_hardware_report` - storage and foldability of the
+  smoothing vectors (w8a8.py:217-251).
 """
 from __future__ import annotations
 
@@ -219,6 +221,48 @@ def apply_smoothquant_transform(modules: dict[str, nn.Module],
         activation_scales[name] = _w.static_activation_scale(post_absmax,
                                                              device=weight.device).cpu()
     return input_scales, activation_scales
+
+
+_SHARED_INPUT_STATUS = (
+    (("q_proj", "k_proj", "v_proj"), "not_foldable_independently_shared_qkv_input"),
+    (("gate_proj", "up_proj"), "not_foldable_independently_shared_gate_up_input"),
+)
+
+
+def smoothquant_hardware_report(modules: dict[str, nn.Module],
+                                input_smoothing_scales: dict[str, torch.Tensor]
+                                ) -> dict[str, Any]:
+    """Storage and foldability of independent per-module smoothing vectors
+    (w8a8.py:217-251), in the reference's report format.
+
+    Q/K/V and gate/up read one shared producer output, so a vector per module
+    cannot be folded into that producer; any other module needs its producer's
+    fan-out and residual path checked first.  Every vector is stored as
+    binary16 and divided at run time (here inside the activation prologue)."""
+    rows: dict[str, dict[str, Any]] = {}
+    total = 0
+    for name, module in modules.items():
+        channels = int(input_smoothing_scales[name].numel())
+        total += channels
+        status = next((s for parts, s in _SHARED_INPUT_STATUS if any(p in name for p in parts)),
+                      "requires_producer_fanout_and_residual_proof")
+        rows[name] = {
+            "channels": channels,
+            "storage_bytes_fp16": channels * 2,
+            "current_runtime_channelwise_divide": True,
+            "offline_fold_status": status,
+            "module_type": type(module).__name__,
+        }
+    return {
+        "scheme": "independent_per_module_smoothing_vectors",
+        "vector_count": len(rows),
+        "total_scale_values": total,
+        "total_storage_bytes_fp16": total * 2,
+        "runtime_overhead_zero": False,
+        "reason": ("independent Q/K/V and Gate/Up vectors cannot all fold into their "
+                   "single shared producer; joint-group smoothing is required"),
+        "modules": rows,
+    }
 
 
 def calibrate_h_scales(model: nn.Module, run: Callable[[], Any]) -> dict[int, float]:

@@ -199,3 +199,85 @@ def test_calibrate_h_scales_feeds_the_int8_chain(cuda):
         mlp.h_scale = s
         out = packed_mlp_decode(batches[0], mlp)
         assert out.shape == (1, 4, 256) and torch.isfinite(out.float()).all()
+
+
+# ------------------------------------ the reference's own calibration tests
+# (tests/test_w8a8_contract.py:79-160), on the GPU path.
+def test_sequential_activation_qdq_propagates_to_later_layer(cuda):
+    from nanopointllm_amd import calibration as C, w8a8
+
+    model = nn.Sequential(nn.Linear(4, 4, bias=False), nn.Linear(4, 2, bias=False)).to(cuda)
+    modules = {"first": model[0], "second": model[1]}
+    values = torch.tensor([[0.03, -0.7, 1.1, 4.3]], device=cuda)
+    note("sequential QDQ propagation")
+    with C.ActivationAbsmaxCollector(modules) as collector:
+        baseline = model(values)
+    scales = collector.static_scales()
+    captured = []
+    handle = model[1].register_forward_pre_hook(
+        lambda _m, inputs: captured.append(inputs[0].detach().clone()))
+    try:
+        with C.SequentialActivationQDQ(modules, mode="static", static_scales=scales):
+            candidate = model(values)
+    finally:
+        handle.remove()
+    first_q = w8a8.static_activation_qdq(values, scales["first"].to(cuda))
+    np.testing.assert_array_equal(
+        first_q.cpu().numpy(),
+        O.quantize_symmetric(values.cpu().numpy(), scales["first"].numpy()).astype(np.float32)
+        * scales["first"].numpy())
+    torch.testing.assert_close(captured[0], model[0](first_q))
+    assert not torch.equal(candidate, baseline)
+
+
+def test_apply_weight_qdq_changes_all_selected_modules(cuda):
+    from nanopointllm_amd import calibration as C
+
+    model = nn.Sequential(nn.Linear(7, 5), nn.Linear(5, 3)).to(cuda)
+    originals = [m.weight.detach().clone() for m in model]
+    note("apply_weight_qdq group 4")
+    report = C.apply_weight_qdq({"first": model[0], "second": model[1]}, granularity="group",
+                                group_size=4)
+    assert set(report) == {"first", "second"}
+    assert all(not torch.equal(m.weight, w) for m, w in zip(model, originals))
+    for m, w in zip(model, originals):
+        np.testing.assert_array_equal(m.weight.detach().cpu().numpy(),
+                                      O.groupwise_weight_qdq(w.cpu().numpy(), 4)[0])
+
+
+def test_smoothquant_transform_is_exact_before_qdq_for_linear_and_conv(cuda):
+    from nanopointllm_amd import calibration as C
+
+    torch.manual_seed(8)
+    linear = nn.Linear(5, 3).to(cuda)
+    x = torch.randn(2, 4, 5, device=cuda)
+    ref = linear(x)
+    note("smoothquant linear + conv")
+    with C.ActivationAbsmaxCollector({"linear": linear}) as col:
+        linear(x)
+    smoothing, act = C.apply_smoothquant_transform({"linear": linear}, col.channel_absmax,
+                                                   alpha=0.5)
+    torch.testing.assert_close(linear(x / smoothing["linear"].to(cuda)), ref, rtol=2e-3,
+                               atol=2e-3)
+    assert act["linear"].numel() == 1
+    conv = nn.Conv1d(4, 6, 1).to(cuda)
+    xc = torch.randn(2, 4, 7, device=cuda)
+    refc = conv(xc)
+    with C.ActivationAbsmaxCollector({"conv": conv}) as col:
+        conv(xc)
+    np.testing.assert_array_equal(col.channel_absmax["conv"].numpy(),
+                                  xc.abs().amax(dim=(0, 2)).cpu().numpy())
+    smoothing, _ = C.apply_smoothquant_transform({"conv": conv}, col.channel_absmax, alpha=0.5)
+    torch.testing.assert_close(conv(xc / smoothing["conv"].to(cuda).reshape(1, 4, 1)), refc,
+                               rtol=2e-3, atol=2e-3)
+
+
+def test_invalid_contract_arguments_fail_closed(cuda):
+    from nanopointllm_amd import calibration as C, w8a8
+
+    with pytest.raises(ValueError, match="positive"):
+        w8a8.quantize_symmetric(torch.ones(1, device=cuda), torch.tensor(0.0, device=cuda))
+    with pytest.raises(ValueError, match="group_size"):
+        w8a8.groupwise_weight_qdq(torch.ones(2, 2, device=cuda), group_size=0)
+    with pytest.raises(ValueError, match="alpha"):
+        C.apply_smoothquant_transform({}, {}, alpha=1.1)
