@@ -396,8 +396,9 @@ def _unpack_rows(packed, rows: int, k: int):
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
-        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the W8A8 path "
-              "is single-GPU; sharding is described in DESIGN.md).", file=sys.stderr)
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported: the W8A8 "
+              "linear path runs on one GPU, and its throughput is the one GPU's.",
+              file=sys.stderr)
         return 2
     import torch
 
