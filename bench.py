@@ -60,7 +60,38 @@ def parse_args():
     ap.add_argument("--profile-gateup", action="store_true",
                     help="only the counter-calibration copy and the gate/up linear loop "
                          "(the region rocprofv3 --pmc runs measure)")
+    ap.add_argument("--profile-gemm", action="store_true",
+                    help="only the prefill GEMM: packed gate/up (22016 x 4096, SiLU*mul) on "
+                         "560 rows of int8 activations, 4 layers x 5 repetitions, after the "
+                         "counter-calibration copy (the region rocprofv3 --pmc runs of the "
+                         "GEMM measure)")
     return ap.parse_args()
+
+
+def profile_gemm(device) -> dict:
+    """The packed gate/up GEMM at M = 560 (int8 in, SiLU*mul epilogue) over four
+    layers' cold weights, after a 256 MiB copy that calibrates the counters."""
+    import torch
+
+    from nanopointllm_amd import _lib, w8a8, workloads as W
+
+    src = torch.empty(CALIBRATION_COPY_BYTES, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    del src, dst
+    m, layers = 560, [Layer(i, 8, device) for i in range(4)]
+    spec = {p.name: p for p in W.PROJECTIONS}["gateup"]
+    xq, sx = w8a8.quant_rows(W.prefill_activations(m, spec.k, seed=11).to(device))
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        for layer in layers:
+            p = layer.weights["gateup"]
+            w8a8.linear_i8in(xq, sx, p.packed, p.scale, None, p.out_features,
+                             epilogue=_lib.EPI_SILU_MUL)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / 20
+    return {"m": m, "n": spec.n, "k": spec.k, "launches": 20, "host_ms_per_call": round(ms, 4)}
 
 
 class Layer:
@@ -409,6 +440,9 @@ def main() -> int:
         return 2
     _lib.load()
     device = torch.device("cuda:0")
+    if args.profile_gemm:
+        print(json.dumps({"profile_gemm": profile_gemm(device)}))
+        return 0
     m = args.m
     log(f"building {args.layers} layers of packed W8A8 weights (M={m})")
     layers = [Layer(i, m, device) for i in range(args.layers)]
