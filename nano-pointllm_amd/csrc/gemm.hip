@@ -7,16 +7,18 @@
 // Design (MFMA-bound), chosen by measurement on MI355X:
 //   * v_mfma_i32_32x32x32_i8, which sustains ~2x the int8 rate of the
 //     16x16x64 form (4.4 vs 2.7 POPS in a register-only loop).
-//   * Every wavefront owns one 32x32 output block; the workgroup tile is a
-//     WM x WN grid of them: 128x128 with 16 wavefronts for large problems,
-//     64x64 with 4 wavefronts (4 workgroups per CU) when 128x128 tiles would
-//     not cover every CU.  Many resident wavefronts per SIMD hide the LDS and
-//     memory latency better than larger per-wave tiles did.
+//   * Every wavefront owns BC adjacent 32x32 output blocks; the workgroup
+//     tile is a WM x WN grid of them: 128x256 (16 wavefronts of 32x64) when
+//     there are enough such tiles to fill every CU twice, else 128x128 (16
+//     wavefronts of 32x32), else 64x64 with 4 wavefronts (4 workgroups per CU)
+//     when 128x128 tiles would not cover every CU.  Many resident wavefronts
+//     per SIMD hide the LDS and memory latency better than larger per-wave
+//     tiles did; the 32x64 block halves the activation reads from LDS.
 //   * Both operands are in the packed 16x64 tile layout, so a k-step (64) of
 //     the workgroup tile is (BM + BN)/16 fragments of 1 KiB.  Each wavefront
-//     copies its share with global_load_lds_dwordx4 straight into a 4-stage
-//     LDS ring (lane l lands at slot base + 16*l, the fragment layout),
-//     keeping three k-steps in flight; explicit vmcnt waits and one barrier
+//     copies its share with global_load_lds_dwordx4 straight into a 3- or
+//     4-stage LDS ring (lane l lands at slot base + 16*l, the fragment layout),
+//     keeping STG - 1 k-steps in flight; explicit vmcnt waits and one barrier
 //     per k-step order the ring.  A 32x32x32 operand is the lane slots of two
 //     adjacent 16-row tiles, read with ds_read_b128 as four contiguous
 //     256-byte runs.
@@ -51,7 +53,6 @@ struct GemmParams {
 };
 
 constexpr int kXcds = 8;
-constexpr int kStages = 4;  // LDS ring depth (k-steps in flight)
 
 typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -74,16 +75,18 @@ __device__ inline void wait_vmcnt() {
 // overtake them; unlike __syncthreads it does not drain outstanding loads.
 __device__ inline void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// WM x WN wavefronts, each owning one 32x32 block (BM = 32 WM, BN = 32 WN).
-template <int WM, int WN, int OCC, int EPI, typename TY, typename TH>
+// WM x WN wavefronts, each owning BC 32x32 blocks side by side (BM = 32 WM,
+// BN = 32 WN BC), with an STG-deep LDS ring.
+template <int WM, int WN, int BC, int STG, int OCC, int EPI, typename TY, typename TH>
 __global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_kernel(GemmParams p) {
   constexpr int NW = WM * WN;
-  constexpr int BMF = 2 * WM;  // 16-row activation tiles per k-step
-  constexpr int BNF = 2 * WN;  // 16-row weight tiles per k-step
+  constexpr int BMF = 2 * WM;       // 16-row activation tiles per k-step
+  constexpr int BNF = 2 * WN * BC;  // 16-row weight tiles per k-step
   constexpr int F = BMF + BNF;
-  constexpr int LPW = F / NW;  // fragment copies per wave per k-step
-  static_assert(F % NW == 0, "fragments must split evenly over the wavefronts");
-  __shared__ i32x4 lds[kStages][F][64];
+  // Fragment copies per wave per k-step: LPW for the first F - (LPW-1) NW
+  // waves, LPW - 1 for the rest.
+  constexpr int LPW = (F + NW - 1) / NW;
+  __shared__ i32x4 lds[STG][F][64];
 
   // XCD-major tile mapping: workgroup b runs on XCD b % 8.
   const int b = blockIdx.x;
@@ -102,10 +105,11 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_kernel(GemmParams p) {
   // mb0 + f, the rest weight blocks nb0 + f - BMF.  Blocks past the operand
   // are clamped to its last block: their products only reach accumulator
   // rows or columns that the epilogue never stores.
+  const bool full = (LPW - 1) * NW + wave < F;  // wave-uniform
   const i32x4* src[LPW];
 #pragma unroll
   for (int q = 0; q < LPW; ++q) {
-    const int f = q * NW + wave;
+    const int f = min(q * NW + wave, F - 1);
     if (f < BMF) {
       src[q] = p.a + static_cast<int64_t>(min(mb0 + f, p.MB - 1)) * KB * 64 + lane;
     } else {
@@ -115,17 +119,20 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_kernel(GemmParams p) {
   auto issue = [&](int kb, int slot) {
 #pragma unroll
     for (int q = 0; q < LPW; ++q)
-      __builtin_amdgcn_global_load_lds(
-          static_cast<const void*>(src[q] + static_cast<int64_t>(kb) * 64),
-          (lds_void*)(&lds[slot][q * NW + wave][0]), 16, 0, 0);
+      if (q < LPW - 1 || full)
+        __builtin_amdgcn_global_load_lds(
+            static_cast<const void*>(src[q] + static_cast<int64_t>(kb) * 64),
+            (lds_void*)(&lds[slot][q * NW + wave][0]), 16, 0, 0);
   };
 
-  i32x16 acc;
+  i32x16 acc[BC];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) acc[r] = 0;
+  for (int j = 0; j < BC; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0;
 
 #pragma unroll
-  for (int s = 0; s < kStages - 1; ++s)
+  for (int s = 0; s < STG - 1; ++s)
     if (s < KB) issue(s, s);
 
   // 32x32x32 operands of k-half h: lane l takes 16 bytes of row l%32 of a
@@ -134,76 +141,86 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_kernel(GemmParams p) {
   const int fhalf = (lane >> 4) & 1;
   for (int kb = 0; kb < KB; ++kb) {
     // Stage kb has landed once only the later stages' loads may remain.
-    if (kb + kStages - 2 < KB) {
-      wait_vmcnt<LPW * (kStages - 2)>();
+    if (kb + STG - 2 < KB) {
+      if (full) {
+        wait_vmcnt<LPW * (STG - 2)>();
+      } else {
+        wait_vmcnt<(LPW - 1) * (STG - 2)>();
+      }
     } else {
       wait_vmcnt<0>();
     }
     ring_barrier();
     // Every wave has finished reading the slot of stage kb-1: refill it.
-    if (kb + kStages - 1 < KB) issue(kb + kStages - 1, (kb + kStages - 1) % kStages);
-    const int slot = kb % kStages;
+    if (kb + STG - 1 < KB) issue(kb + STG - 1, (kb + STG - 1) % STG);
+    const int slot = kb % STG;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
       const int fslot = (lane & 15) + 16 * (2 * h + (lane >> 5));
       const i32x4 af = lds[slot][2 * wm + fhalf][fslot];
-      const i32x4 bf = lds[slot][BMF + 2 * wn + fhalf][fslot];
-      acc = mfma_32x32x32(af, bf, acc);
+      i32x4 bf[BC];
+#pragma unroll
+      for (int j = 0; j < BC; ++j) bf[j] = lds[slot][BMF + 2 * (wn * BC + j) + fhalf][fslot];
+#pragma unroll
+      for (int j = 0; j < BC; ++j) acc[j] = mfma_32x32x32(af, bf[j], acc[j]);
     }
   }
 
-  // Epilogue.  Register r of lane l holds row (mb0 + 2wm)*16 + 8(r/4) +
-  // 4(l/32) + r%4 and column (nb0 + 2wn)*16 + l%32.
-  const int64_t n = static_cast<int64_t>(nb0 + 2 * wn) * 16 + (lane & 31);
-  const bool n_ok = n < p.N;
-  float swn = 0.0f;
-  if constexpr (EPI != kEpiI32 && EPI != kEpiRequant) swn = n_ok ? p.sw[n] : 0.0f;
-  uint32_t rq_mult = 0;
-  int32_t rq_shift = 0, rq_bias = 0;
-  if constexpr (EPI == kEpiRequant) {
-    if (n_ok) {
-      rq_mult = p.rq_mult[n];
-      rq_shift = p.rq_shift[n];
-      rq_bias = p.rq_bias != nullptr ? p.rq_bias[n] : 0;
-    }
-  }
+  // Epilogue.  Register r of block j in lane l holds row (mb0 + 2wm)*16 +
+  // 8(r/4) + 4(l/32) + r%4 and column (nb0 + 2(wn BC + j))*16 + l%32.
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int m = (mb0 + 2 * wm) * 16 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-    const bool m_ok = m < p.M;
-    const int32_t a = acc[r];
-    if constexpr (EPI == kEpiI32) {
-      if (m_ok && n_ok) static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] = a;
-    } else if constexpr (EPI == kEpiDequant) {
-      if (m_ok && n_ok) {
-        static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
-            from_f32<TY>(dequant1(a, p.sx[m], swn, p.bias, n));
+  for (int j = 0; j < BC; ++j) {
+    const int64_t n = static_cast<int64_t>(nb0 + 2 * (wn * BC + j)) * 16 + (lane & 31);
+    const bool n_ok = n < p.N;
+    float swn = 0.0f;
+    if constexpr (EPI != kEpiI32 && EPI != kEpiRequant) swn = n_ok ? p.sw[n] : 0.0f;
+    uint32_t rq_mult = 0;
+    int32_t rq_shift = 0, rq_bias = 0;
+    if constexpr (EPI == kEpiRequant) {
+      if (n_ok) {
+        rq_mult = p.rq_mult[n];
+        rq_shift = p.rq_shift[n];
+        rq_bias = p.rq_bias != nullptr ? p.rq_bias[n] : 0;
       }
-    } else if constexpr (EPI == kEpiRequant) {
-      if (m_ok && n_ok) {
-        static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
-            static_cast<int8_t>(requant1(a, rq_bias, rq_mult, rq_shift));
-      }
-    } else if constexpr (EPI == kEpiBf16Exact) {
-      if (m_ok && n_ok) {
-        static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
-            __builtin_bit_cast(TY, dequant_bf16_exact(a, f16_bits(p.sx[m]), f16_bits(swn)));
-      }
-    } else {
-      // Interleaved gate/up: even column = gate, odd column = up of output
-      // n / 2.  Every lane dequantizes its own column; the even lane takes
-      // the up value from its odd neighbour.
-      const float sxm = m_ok ? p.sx[m] : 0.0f;
-      const float v =
-          (m_ok && n_ok) ? to_f32(from_f32<TH>(dequant1(a, sxm, swn, p.bias, n))) : 0.0f;
-      const float u = __shfl_xor(v, 1);
-      if ((lane & 1) == 0 && m_ok && n_ok) {
-        const TH h = from_f32<TH>(silu_mul<TH>(v, u));
-        TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n / 2;
-        if constexpr (EPI == kEpiSilu) {
-          *y = h;
-        } else {
-          *y = static_cast<int8_t>(quant1(to_f32(h), p.out_scale));
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = (mb0 + 2 * wm) * 16 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const bool m_ok = m < p.M;
+      const int32_t a = acc[j][r];
+      if constexpr (EPI == kEpiI32) {
+        if (m_ok && n_ok) static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] = a;
+      } else if constexpr (EPI == kEpiDequant) {
+        if (m_ok && n_ok) {
+          static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
+              from_f32<TY>(dequant1(a, p.sx[m], swn, p.bias, n));
+        }
+      } else if constexpr (EPI == kEpiRequant) {
+        if (m_ok && n_ok) {
+          static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
+              static_cast<int8_t>(requant1(a, rq_bias, rq_mult, rq_shift));
+        }
+      } else if constexpr (EPI == kEpiBf16Exact) {
+        if (m_ok && n_ok) {
+          static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
+              __builtin_bit_cast(TY, dequant_bf16_exact(a, f16_bits(p.sx[m]), f16_bits(swn)));
+        }
+      } else {
+        // Interleaved gate/up: even column = gate, odd column = up of output
+        // n / 2.  Every lane dequantizes its own column; the even lane takes
+        // the up value from its odd neighbour.
+        const float sxm = m_ok ? p.sx[m] : 0.0f;
+        const float v =
+            (m_ok && n_ok) ? to_f32(from_f32<TH>(dequant1(a, sxm, swn, p.bias, n))) : 0.0f;
+        const float u = __shfl_xor(v, 1);
+        if ((lane & 1) == 0 && m_ok && n_ok) {
+          const TH h = from_f32<TH>(silu_mul<TH>(v, u));
+          TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n / 2;
+          if constexpr (EPI == kEpiSilu) {
+            *y = h;
+          } else {
+            *y = static_cast<int8_t>(quant1(to_f32(h), p.out_scale));
+          }
         }
       }
     }
@@ -212,24 +229,43 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_kernel(GemmParams p) {
 
 // Launches one tile configuration for the problem in p (tile counts are
 // filled in here).
-template <int WM, int WN, int OCC, int EPI, typename TY, typename TH>
+template <int WM, int WN, int BC, int STG, int OCC, int EPI, typename TY, typename TH>
 hipError_t launch_cfg(GemmParams p, hipStream_t st) {
   p.tiles_m = static_cast<int>(ceil_div(p.MB, 2 * WM));
-  const int tiles_n = static_cast<int>(ceil_div(p.NB, 2 * WN));
+  const int tiles_n = static_cast<int>(ceil_div(p.NB, 2 * WN * BC));
   p.tiles = p.tiles_m * tiles_n;
   p.per_xcd = static_cast<int>(ceil_div(p.tiles, kXcds));
   if (p.tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_kernel<WM, WN, OCC, EPI, TY, TH>), dim3(p.per_xcd * kXcds),
+  hipLaunchKernelGGL((gemm_kernel<WM, WN, BC, STG, OCC, EPI, TY, TH>), dim3(p.per_xcd * kXcds),
                      dim3(WM * WN * 64), 0, st, p);
   return hipGetLastError();
 }
 
-// 128x128 tiles (16 waves) when they cover every CU, else 64x64 (4 waves).
+// Tile configurations, chosen by tile count (measured on MI355X, random data,
+// cold weights, LLaMA-7B projections at M = 256..2048):
+//   * 128x256, 16 waves of 32x64 blocks, 3-stage ring, 2 workgroups per CU,
+//     when there are at least ~0.82 tiles per workgroup slot (2 per CU): each
+//     MFMA moves 1.5 KiB of operands through LDS instead of 2, 3-12% faster.
+//     Just past one full round of slots (1 to 1.16 tiles per slot) the few
+//     tiles of the second round cost more than that saves, and the 128x128
+//     tile is kept;
+//   * else 128x128, 16 waves of 32x32, 4 stages, 2 per CU, when those cover
+//     every CU;
+//   * else 64x64, 4 waves, 4 per CU.
 template <int EPI, typename TY, typename TH>
 hipError_t launch_t(const GemmParams& p, hipStream_t st) {
+  // (The integer-requant epilogue needs more registers than two workgroups
+  // per CU leave it, so it keeps the 128x128 tile.)
+  if constexpr (EPI != kEpiRequant) {
+    const int64_t wide_tiles = ceil_div(p.MB, 8) * ceil_div(p.NB, 16);
+    const int64_t slots = static_cast<int64_t>(cu_count()) * 2;
+    const bool short_second_round = wide_tiles > slots && wide_tiles * 100 < slots * 116;
+    if (wide_tiles * 100 >= slots * 82 && !short_second_round)
+      return launch_cfg<4, 4, 2, 3, 2, EPI, TY, TH>(p, st);
+  }
   const int64_t big_tiles = ceil_div(p.MB, 8) * ceil_div(p.NB, 8);
-  if (big_tiles >= 256) return launch_cfg<4, 4, 2, EPI, TY, TH>(p, st);
-  return launch_cfg<2, 2, 4, EPI, TY, TH>(p, st);
+  if (big_tiles >= cu_count()) return launch_cfg<4, 4, 1, 4, 2, EPI, TY, TH>(p, st);
+  return launch_cfg<2, 2, 1, 4, 4, EPI, TY, TH>(p, st);
 }
 
 }  // namespace

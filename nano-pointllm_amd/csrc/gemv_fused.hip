@@ -26,6 +26,7 @@
 // Quantizing x once per CU costs M*K*~10 VALU ops per CU; for decode shapes
 // that hides behind the weight loads already in flight, and it saves the
 // separate quantization launch and its round trip through memory.
+#include <atomic>
 #include <type_traits>
 
 #include "w8a8_internal.h"
@@ -402,20 +403,6 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   }
 }
 
-int cu_count() {
-  static int cached[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cached[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        n <= 0)
-      n = 256;
-    cached[dev] = n;
-  }
-  return cached[dev];
-}
-
 template <int EPI, typename TX, typename TY, typename TH>
 hipError_t launch_f(const FusedParams& p, hipStream_t st) {
   // x chunks per thread: rows spread over 1024 / mpad(M) threads each.
@@ -459,6 +446,22 @@ hipError_t dispatch_f(const FusedParams& p, int epi, int y_dtype, int h_dtype, h
 }
 
 }  // namespace
+
+// Compute units of the current device (cached per device; every thread that
+// fills an entry stores the same value).
+int cu_count() {
+  static std::atomic<int> cached[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int n = cached[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cached[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
 
 // Decode shapes: up to 8 rows of 16-bit activations, K <= 12288 and at most
 // 64 output blocks per workgroup (N <= 1024 * CUs).  Each CU quantizes all

@@ -90,6 +90,8 @@ constexpr int64_t kGemvMaxRows = 64;
 // Decode linear with the per-token quantization fused in (gemv_fused.hip):
 // 16-bit x, 1 <= M <= 8, K % 8 == 0, K <= 12288, 16-byte aligned rows,
 // N <= 1024 * CUs, and enough weight bytes per CU to hide the quantization.
+// Compute units of the current device.
+int cu_count();
 bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
                           int64_t K);
 // The fused kernel's weight stream on int8 activations (op.a row-major as for
