@@ -76,11 +76,10 @@ __device__ inline i32x4 mfma_16x16x64(i32x4 a, i32x4 b, i32x4 c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
-// |x| of a packed pair of 16-bit floats, as unsigned integers.  For
+// |x| of 16-bit floats as unsigned integers (the sign bit cleared): for
 // non-negative binary16 / bfloat16 values the bit patterns order like the
 // values, so the integer max is the absmax.
-__device__ inline uint32_t abs_lo(uint32_t v) { return v & 0x7fffu; }
-__device__ inline uint32_t abs_hi(uint32_t v) { return (v >> 16) & 0x7fffu; }
+typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 template <typename TX>
 __device__ inline float bits_to_f32(uint32_t b16) {
@@ -302,12 +301,15 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
     }
   }
   load_ops();
-  uint32_t am = 0;
+  // |x| patterns of both halves at once (v_pk_max_u16).
+  u16x2 am2 = {0, 0};
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
 #pragma unroll
-    for (int q = 0; q < 4; ++q) am = max(am, max(abs_lo(raw[i][q]), abs_hi(raw[i][q])));
+    for (int q = 0; q < 4; ++q)
+      am2 = __builtin_elementwise_max(am2, __builtin_bit_cast(u16x2, raw[i][q] & 0x7fff7fffu));
   }
+  uint32_t am = max(static_cast<uint32_t>(am2[0]), static_cast<uint32_t>(am2[1]));
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) am = max(am, static_cast<uint32_t>(__shfl_xor(static_cast<int>(am), off)));
   // The first weight loads go out once x has arrived (the absmax above waits
@@ -344,18 +346,19 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
           xv[2 * q] = bits_to_f32<TX>(raw[i][q] & 0xffffu);
           xv[2 * q + 1] = bits_to_f32<TX>(raw[i][q] >> 16);
         }
-        int32_t qi[8];
+        u32x2 qw;
         if constexpr (NCH <= 4) {
-          quant8_dyn(xv, s, r, qi);
+          qw = quant8_dyn(xv, s, r);
         } else {
           // Many chunks per thread leave no registers for the fast path.
+          int32_t qi[8];
 #pragma unroll
           for (int j = 0; j < 8; ++j) qi[j] = quant1_h(xv[j], s, r);
+          qw = u32x2{pack4_i8(qi[0], qi[1], qi[2], qi[3]), pack4_i8(qi[4], qi[5], qi[6], qi[7])};
         }
         const int k = c * 8;
         const int off = (((k >> 6) * 4 + ((k & 63) >> 4)) * 8 + row) * 16 + (k & 15);
-        *reinterpret_cast<u32x2*>(a_lds + off) =
-            u32x2{pack4_i8(qi[0], qi[1], qi[2], qi[3]), pack4_i8(qi[4], qi[5], qi[6], qi[7])};
+        *reinterpret_cast<u32x2*>(a_lds + off) = qw;
       }
     }
   }

@@ -127,32 +127,53 @@ __device__ inline int32_t quant1_h(float x, float s, float r) {
   return static_cast<int32_t>(q);
 }
 
-// Quantizes 8 values with a dynamic row scale s (scale_from_absmax of the
-// row's |x|max, so |x / s| <= 127.07) and r = 1/s, exactly and faster than
-// quant1_h: rint(x * r) already rounds x / s correctly (ties to even) unless
-// x * r lies within 2^-15 of a half-integer, since |x*r - x/s| <= 127.07 *
-// 2^-23 < 2^-16 and x*r - rint(x*r) is exact.  When any lane of the
-// wavefront holds such a value the 8 values are redone with quant1_h (a
-// wave-uniform branch).  No clamp is needed: |rint(x * r)| <= 127.
-__device__ inline void quant8_dyn(const float (&x)[8], float s, float r, int32_t (&q)[8]) {
-  float dev = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const float y = x[j] * r;
-    const float t = __builtin_rintf(y);
-    dev = fmaxf(dev, fabsf(y - t));
-    q[j] = static_cast<int32_t>(t);
-  }
-  if (__any(dev >= 0.5f - 0x1p-15f)) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) q[j] = quant1_h(x[j], s, r);
-  }
-}
-
 __device__ inline uint32_t pack4_i8(int32_t a, int32_t b, int32_t c, int32_t d) {
   return (static_cast<uint32_t>(a) & 0xffu) | ((static_cast<uint32_t>(b) & 0xffu) << 8) |
          ((static_cast<uint32_t>(c) & 0xffu) << 16) | ((static_cast<uint32_t>(d) & 0xffu) << 24);
 }
+
+// Quantizes 8 values with a dynamic row scale s (scale_from_absmax of the
+// row's |x|max, so |x / s| <= 127.07) and r = 1/s, exactly and faster than
+// quant1_h, into two words of 4 int8 each.  t = fma(x, r, 1.5 * 2^23) is
+// 1.5 * 2^23 plus the integer nearest to the exact product x*r (ties to
+// even): with |x*r| < 128 it stays in [2^23, 2^24), where the ulp is 1, so
+// the low byte of its bit pattern is that integer as an int8.  It rounds
+// x / s correctly unless x*r lies within 2^-15 of a half-integer
+// (|x*r - x/s| <= 127.07 * 2^-24), which the exact remainder
+// e = fma(x, r, -(t - 1.5 * 2^23)) detects: |e| >= 0.5 - 2^-14 takes every
+// such case (and a few more).  When any lane of the wavefront has one, the 8
+// values are redone with quant1_h (a wave-uniform branch).  No clamp is
+// needed: |rint(x / s)| <= 127.
+__device__ inline u32x2 quant8_dyn(const float (&x)[8], float s, float r) {
+  constexpr float kMagic = 0x1.8p23f;
+  float t[8];
+  float dev = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    t[j] = __builtin_fmaf(x[j], r, kMagic);
+    dev = fmaxf(dev, fabsf(__builtin_fmaf(x[j], r, kMagic - t[j])));
+  }
+  if (__any(dev >= 0.5f - 0x1p-14f)) {
+    int32_t q[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q[j] = quant1_h(x[j], s, r);
+    return u32x2{pack4_i8(q[0], q[1], q[2], q[3]), pack4_i8(q[4], q[5], q[6], q[7])};
+  }
+  u32x2 w;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    // v_perm_b32 byte selectors: 0-3 pick bytes of the second operand, 4-7
+    // bytes of the first, 12 a zero byte.
+    const uint32_t lo = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, t[4 * h + 1]),
+                                              __builtin_bit_cast(uint32_t, t[4 * h]), 0x0c0c0400u);
+    const uint32_t hi = __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, t[4 * h + 3]),
+                                              __builtin_bit_cast(uint32_t, t[4 * h + 2]),
+                                              0x04000c0cu);
+    w[h] = lo | hi;
+  }
+  return w;
+}
+
 
 // Dequant epilogue (w8a8.py:134-137): three separate binary32 roundings.
 // dequant1 with the bias value already loaded (added only when present, so a

@@ -1,10 +1,17 @@
 """The fast dynamic-scale quantizer of the fused decode kernel, restated on the
-host with binary32 numpy arithmetic (the same IEEE operations the kernel
-runs) and checked against the exact answer.
+host with the same IEEE operations the kernel runs, and checked against the
+exact answer.
 
-quant8_dyn (csrc/w8a8_common.h) takes rint(x * r), r = fl32(1/s), as the
-quantized value of x / s unless fl32(x * r) lies within 2^-15 of a
-half-integer, where the wavefront redoes the chunk with the exact tie test.
+quant8_dyn (csrc/w8a8_common.h) computes t = fma(x, r, 1.5 * 2^23) with
+r = fl32(1/s): 1.5 * 2^23 plus the integer nearest the exact product x * r,
+whose low byte is the int8 result.  It keeps that value unless the exact
+remainder e = fma(x, r, -(t - 1.5 * 2^23)) has |e| >= 0.5 - 2^-14 (x * r
+near a half-integer), where the wavefront redoes the chunk with the exact tie
+test.  The fused multiply-adds are restated in float64: x * r has at most
+11 + 24 significant bits, so float64 holds the product exactly and the sums
+within 2^-29, after which one rounding to binary32 follows.  That 2^-29 can
+move the binary32 rounding only within 2^-29 of a half-integer, inside the
+band the fallback takes, so the restated fast path is the hardware's.
 The claim pinned here: whenever the fast path is taken, it equals the
 correctly rounded (ties to even) quotient of quantize_symmetric
 (nanopointllm/compression/w8a8.py:33-43), for every finite binary16 and
@@ -18,7 +25,8 @@ from __future__ import annotations
 import numpy as np
 import pytest
 
-THRESH = np.float32(0.5 - 2.0 ** -15)
+THRESH = np.float32(0.5 - 2.0 ** -14)
+MAGIC = 1.5 * 2.0 ** 23
 
 
 def _all_finite(kind: str) -> np.ndarray:
@@ -40,10 +48,15 @@ def _scales() -> np.ndarray:
 
 
 def _fast_path(x: np.ndarray, s: np.float32):
+    """(value, taken) of the fast path, and the int8 read from t's low byte."""
     r = np.float32(1.0) / s
-    y = x * r
-    t = np.rint(y)
-    return t, np.abs(y - t) < THRESH
+    p = x.astype(np.float64) * np.float64(r)                # exact
+    t = (p + MAGIC).astype(np.float32)                     # fma(x, r, MAGIC)
+    n = t.astype(np.float64) - MAGIC                       # exact
+    e = (p - n).astype(np.float32)                         # fma(x, r, MAGIC - t)
+    low = (t.view(np.uint32) & np.uint32(0xFF)).astype(np.uint8).view(np.int8)
+    np.testing.assert_array_equal(low.astype(np.float64), n)
+    return n.astype(np.float32), np.abs(e) < THRESH
 
 
 @pytest.mark.parametrize("kind", ["f16", "bf16"])
@@ -64,24 +77,23 @@ def test_fast_path_is_exact_for_dynamic_scales(kind):
 
 
 def test_fast_path_flags_every_tie():
-    """Exact ties (x / s = k + 1/2) always fall back, and a planted wider
-    threshold (ignoring the 2^-15 margin) would accept a wrong rounding."""
+    """Exact ties (x / s = k + 1/2) always fall back, and wherever the nearest
+    integer to x * r is not the correctly rounded x / s, the fallback is taken."""
     s = np.float32(2.0)
     x = np.arange(-254, 255, dtype=np.float32)          # x / s hits every half-integer
     t, fast = _fast_path(x, s)
     ties = (x % 2) != 0
     assert not fast[ties].any()
-    # With a threshold of exactly 0.5 a tie would pass as a fast value whose
-    # rint rounds to even; a near-tie from an inexact r would not.  Find a scale
-    # where fl32(x * r) lands on the wrong side of a half-integer.
+    # An inexact r can put x * r on the other side of a half-integer than
+    # x / s.  Find scales where that happens and check the fallback takes them.
     found = False
     xs = _all_finite("f16")
     for sc in _scales():
         x = xs[np.abs(xs) <= np.float32(127.0625) * sc]
-        y = x * (np.float32(1.0) / sc)
+        t, fast = _fast_path(x, sc)
         exact = np.rint(x.astype(np.float64) / np.float64(sc))
-        wrong = np.rint(y) != exact
+        wrong = t != exact
         if wrong.any():
             found = True
-            assert (np.abs(y - np.rint(y))[wrong] >= THRESH).all()
+            assert not fast[wrong].any()
     assert found, "no scale where plain rint(x * r) is wrong: the fallback would be untested"
