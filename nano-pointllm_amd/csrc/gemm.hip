@@ -77,8 +77,11 @@ __device__ inline void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_
 
 // WM x WN wavefronts, each owning BC 32x32 blocks side by side (BM = 32 WM,
 // BN = 32 WN BC), with an STG-deep LDS ring.
+// The second launch bound is waves per SIMD: OCC workgroups of WM x WN
+// wavefronts over the CU's 4 SIMDs, so the register budget admits OCC
+// workgroups per CU.
 template <int WM, int WN, int BC, int STG, int OCC, int EPI, typename TY, typename TH>
-__global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_kernel(GemmParams p) {
+__global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(GemmParams p) {
   constexpr int NW = WM * WN;
   constexpr int BMF = 2 * WM;       // 16-row activation tiles per k-step
   constexpr int BNF = 2 * WN * BC;  // 16-row weight tiles per k-step
@@ -168,9 +171,29 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_kernel(GemmParams p) {
 
   // Epilogue.  Register r of block j in lane l holds row (mb0 + 2wm)*16 +
   // 8(r/4) + 4(l/32) + r%4 and column (nb0 + 2(wn BC + j))*16 + l%32.
+  // When the output tile fits in the LDS ring, the values go to LDS first and
+  // leave as 16-byte row chunks (a lane's own values are 2 rows x 32 columns
+  // apart, so stored directly they make short partial-line writes).
+  constexpr int BM = 32 * WM;
+  constexpr int BN = 32 * WN * BC;
+  constexpr bool kHalfCols = EPI == kEpiSilu || EPI == kEpiSiluQ8;  // one output per gate/up pair
+  constexpr int BNO = kHalfCols ? BN / 2 : BN;
+  constexpr int kOutBytes = static_cast<int>(sizeof(TY));
+  constexpr bool kStage = BM * BNO * kOutBytes <= STG * F * 1024 && (BNO * kOutBytes) % 16 == 0;
+  [[maybe_unused]] TY* const stile = reinterpret_cast<TY*>(&lds[0][0][0]);
+  if constexpr (kStage) ring_barrier();  // every wave is done reading the ring
+  // Writes output (m, n_out) of tile-local row ml and column nlo.
+  auto put = [&](int ml, int nlo, bool ok, int64_t m, int64_t n_out, TY v) {
+    if constexpr (kStage) {
+      stile[ml * BNO + nlo] = v;
+    } else {
+      if (ok) static_cast<TY*>(p.y)[m * p.ldy + n_out] = v;
+    }
+  };
 #pragma unroll
   for (int j = 0; j < BC; ++j) {
-    const int64_t n = static_cast<int64_t>(nb0 + 2 * (wn * BC + j)) * 16 + (lane & 31);
+    const int nl = 32 * (wn * BC + j) + (lane & 31);
+    const int64_t n = static_cast<int64_t>(nb0) * 16 + nl;
     const bool n_ok = n < p.N;
     float swn = 0.0f;
     if constexpr (EPI != kEpiI32 && EPI != kEpiRequant) swn = n_ok ? p.sw[n] : 0.0f;
@@ -185,42 +208,65 @@ __global__ __launch_bounds__(WM * WN * 64, OCC) void gemm_kernel(GemmParams p) {
     }
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int m = (mb0 + 2 * wm) * 16 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const int ml = 32 * wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const int m = mb0 * 16 + ml;
       const bool m_ok = m < p.M;
+      const bool ok = m_ok && n_ok;
       const int32_t a = acc[j][r];
       if constexpr (EPI == kEpiI32) {
-        if (m_ok && n_ok) static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] = a;
+        put(ml, nl, ok, m, n, a);
       } else if constexpr (EPI == kEpiDequant) {
-        if (m_ok && n_ok) {
-          static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
-              from_f32<TY>(dequant1(a, p.sx[m], swn, p.bias, n));
-        }
+        const float sxm = m_ok ? p.sx[m] : 0.0f;
+        put(ml, nl, ok, m, n, from_f32<TY>(dequant1(a, sxm, swn, ok ? p.bias : nullptr, n)));
       } else if constexpr (EPI == kEpiRequant) {
-        if (m_ok && n_ok) {
-          static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
-              static_cast<int8_t>(requant1(a, rq_bias, rq_mult, rq_shift));
-        }
+        put(ml, nl, ok, m, n, static_cast<int8_t>(requant1(a, rq_bias, rq_mult, rq_shift)));
       } else if constexpr (EPI == kEpiBf16Exact) {
-        if (m_ok && n_ok) {
-          static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] =
-              __builtin_bit_cast(TY, dequant_bf16_exact(a, f16_bits(p.sx[m]), f16_bits(swn)));
-        }
+        const float sxm = m_ok ? p.sx[m] : 0.0f;
+        put(ml, nl, ok, m, n,
+            __builtin_bit_cast(TY, dequant_bf16_exact(a, f16_bits(sxm), f16_bits(swn))));
       } else {
         // Interleaved gate/up: even column = gate, odd column = up of output
         // n / 2.  Every lane dequantizes its own column; the even lane takes
         // the up value from its odd neighbour.
         const float sxm = m_ok ? p.sx[m] : 0.0f;
-        const float v =
-            (m_ok && n_ok) ? to_f32(from_f32<TH>(dequant1(a, sxm, swn, p.bias, n))) : 0.0f;
+        const float v = ok ? to_f32(from_f32<TH>(dequant1(a, sxm, swn, p.bias, n))) : 0.0f;
         const float u = __shfl_xor(v, 1);
-        if ((lane & 1) == 0 && m_ok && n_ok) {
+        if ((lane & 1) == 0) {
           const TH h = from_f32<TH>(silu_mul<TH>(v, u));
-          TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n / 2;
           if constexpr (EPI == kEpiSilu) {
-            *y = h;
+            put(ml, nl / 2, ok, m, n / 2, h);
           } else {
-            *y = static_cast<int8_t>(quant1(to_f32(h), p.out_scale));
+            put(ml, nl / 2, ok, m, n / 2, static_cast<int8_t>(quant1(to_f32(h), p.out_scale)));
           }
+        }
+      }
+    }
+  }
+  if constexpr (kStage) {
+    __syncthreads();
+    constexpr int EV = 16 / kOutBytes;  // outputs per 16-byte chunk
+    constexpr int CPR = BNO / EV;       // chunks per tile row
+    constexpr int NT = NW * 64;
+    constexpr int RPP = NT / CPR;       // tile rows per pass
+    static_assert(NT % CPR == 0, "threads cover whole rows");
+    const int64_t n_out_total = kHalfCols ? p.N / 2 : p.N;
+    const int64_t n0 = kHalfCols ? static_cast<int64_t>(nb0) * 8 : static_cast<int64_t>(nb0) * 16;
+    const bool vec_ok =
+        ((reinterpret_cast<uintptr_t>(p.y) | static_cast<uintptr_t>(p.ldy * kOutBytes)) & 15) == 0;
+#pragma unroll
+    for (int base = 0; base < BM; base += RPP) {
+      const int ml = base + static_cast<int>(threadIdx.x) / CPR;
+      const int nlo = (static_cast<int>(threadIdx.x) % CPR) * EV;
+      const int64_t m = static_cast<int64_t>(mb0) * 16 + ml;
+      const int64_t n = n0 + nlo;
+      if (ml < BM && m < p.M && n < n_out_total) {
+        TY* dst = static_cast<TY*>(p.y) + m * p.ldy + n;
+        const TY* src = stile + ml * BNO + nlo;
+        if (vec_ok && n + EV <= n_out_total) {
+          *reinterpret_cast<i32x4*>(dst) = *reinterpret_cast<const i32x4*>(src);
+        } else {
+          for (int e = 0; e < EV; ++e)
+            if (n + e < n_out_total) dst[e] = src[e];
         }
       }
     }
