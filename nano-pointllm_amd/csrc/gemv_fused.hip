@@ -467,10 +467,12 @@ int cu_count() {
 }
 
 // Decode shapes: up to 8 rows of 16-bit activations, K <= 12288 and at most
-// 64 output blocks per workgroup (N <= 1024 * CUs).  Each CU quantizes all
-// M x K activations (~11 VALU ops per element, ~2.3 us at M = 8, K = 4096),
-// which only pays off while the CU's share of the weights keeps its loads
-// busy for longer: measured on MI355X, the fused kernel beats quantization +
+// 64 output blocks per workgroup (N <= 1024 * CUs).  Each CU fetches and
+// quantizes all M x K activations (the quantization itself takes 0.8 us at
+// M = 8, K = 4096; with the x fetch and the barriers the stream reaches full
+// rate about 4.5 us into the launch), which only pays off while the CU's
+// share of the weights keeps its loads busy for longer: measured on MI355X,
+// the fused kernel beats quantization +
 // gemv_kernel when a CU streams at least 128 KiB of weights and at least 4
 // bytes per activation element it quantizes (LLaMA-7B at M = 8: packed QKV and
 // gate/up fused, O and down not; at M <= 4 only O is not).
