@@ -360,6 +360,47 @@ def mixed_chain(layers, device, h_scale_m: int = 567) -> dict:
             "TOPS": round(ops / (per * 1e-3) / 1e12, 1), "h_scale": h_scale}
 
 
+def decode_step_int8_mlp(layers, m: int, device) -> dict:
+    """The decode step with the int8 MLP chain (static-A8 requant,
+    lightweight_runner.py:362-379 with a calibrated h scale): gate/up's epilogue
+    writes int8 h, and the down projection takes it without a quantization
+    launch.  QKV and O are as in the default step."""
+    import torch
+
+    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd.w8a8 import static_activation_scale
+
+    x0, gu0 = layers[0].x["gateup"], layers[0].weights["gateup"]
+    h = w8a8.linear_dynamic(x0, gu0.packed, gu0.scale, None, gu0.out_features,
+                            epilogue=_lib.EPI_SILU_MUL)
+    h_scale = float(static_activation_scale(h.abs().max(), device=device))
+    s_rows = torch.full((m,), h_scale, dtype=torch.float32, device=device)
+
+    def step():
+        for layer in layers:
+            w, x = layer.weights, layer.x
+            w8a8.linear_dynamic(x["qkv"], w["qkv"].packed, w["qkv"].scale, None,
+                                w["qkv"].out_features)
+            w8a8.linear_dynamic(x["o"], w["o"].packed, w["o"].scale, None, w["o"].out_features)
+            hq = w8a8.linear_dynamic(x["gateup"], w["gateup"].packed, w["gateup"].scale, None,
+                                     w["gateup"].out_features, epilogue=_lib.EPI_SILU_MUL_Q8,
+                                     y_scale=h_scale)
+            w8a8.linear_i8in(hq, s_rows, w["down"].packed, w["down"].scale, None,
+                             w["down"].out_features, out_dtype=torch.float16)
+
+    ms, g = time_graph(step, steps=10, warmup=3)
+    del g
+    spec = {p.name: p for p in W.PROJECTIONS}
+    per_layer = (W.algorithmic_bytes(m, spec["qkv"].n, spec["qkv"].k)
+                 + W.algorithmic_bytes(m, spec["o"].n, spec["o"].k)
+                 + W.algorithmic_bytes(m, spec["gateup"].n, spec["gateup"].k, silu=True,
+                                       int8_out=True)
+                 + W.algorithmic_bytes(m, spec["down"].n, spec["down"].k, int8_in=True))
+    nbytes = per_layer * len(layers)
+    return {"ms": round(ms, 4), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes,
+            "h_scale": h_scale}
+
+
 def stack_with_lm_head(layers, m: int, device) -> dict:
     """The 32-layer W8A8 stack plus the fp16 LM head [32003 x 4096] (torch
     F.linear: the LM head is not a W8A8 linear)."""
@@ -484,6 +525,8 @@ def main() -> int:
         extra["mixed_567_gateup_down_int8_chain"] = mixed_chain(layers, device)
         log("stack + fp16 LM head")
         extra["stack_with_fp16_lm_head"] = stack_with_lm_head(layers, m, device)
+        log("decode step with the int8 MLP chain")
+        extra["decode_step_int8_mlp_chain"] = decode_step_int8_mlp(layers, m, device)
 
     cpu = None
     if not args.no_cpu:
