@@ -473,9 +473,10 @@ int cu_count() {
 // rate about 4.5 us into the launch), which only pays off while the CU's
 // share of the weights keeps its loads busy for longer: measured on MI355X,
 // the fused kernel beats quantization +
-// gemv_kernel when a CU streams at least 128 KiB of weights and at least 4
-// bytes per activation element it quantizes (LLaMA-7B at M = 8: packed QKV and
-// gate/up fused, O and down not; at M <= 4 only O is not).
+// gemv_kernel when a CU streams at least 64 KiB of weights and at least 4
+// bytes per activation element it quantizes (LLaMA-7B at M = 8: packed QKV
+// and gate/up fused, O and down not, down 25% slower fused; at M <= 4 all four
+// fused, O 4-7% faster than quantize + GEMV, down within 1%).
 bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
                           int64_t K) {
   if (!((x_dtype == kF16 || x_dtype == kBF16) && M >= 1 && M <= kFusedMaxRows && K >= 8 &&
@@ -486,7 +487,7 @@ bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, in
   const int64_t g = nb < cu_count() ? nb : cu_count();
   const int64_t blocks_per_cu = ceil_div(nb, g);
   const int64_t weight_bytes_per_cu = blocks_per_cu * kTileRows * ceil_div(K, kTileK) * kTileK;
-  return blocks_per_cu <= kFusedMaxBlocks && weight_bytes_per_cu >= (128 << 10) &&
+  return blocks_per_cu <= kFusedMaxBlocks && weight_bytes_per_cu >= (64 << 10) &&
          weight_bytes_per_cu >= 4 * M * K;
 }
 

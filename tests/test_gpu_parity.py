@@ -307,7 +307,7 @@ def _linear_without_workspace(x, wp, sw, bias, n, epi, y_dtype):
     return rc, y, sx
 
 
-# Shapes the fused kernel takes on a 256-CU MI355X (per CU >= 128 KiB of
+# Shapes the fused kernel takes on a 256-CU MI355X (per CU >= 64 KiB of
 # weights and >= 4 weight bytes per quantized activation element): 3, 8, 32
 # and 2 blocks per CU; K = 256 leaves 12 of the 16 wavefronts without a
 # k-range, K = 12288 is the largest K the kernel takes.
@@ -332,6 +332,28 @@ def test_fused_decode_path(cuda, m, n, k):
     rc, acc, _ = _linear_without_workspace(xc, wp, swt, None, n, _lib.EPI_I32, torch.int32)
     assert rc == 0
     exp, eacc, _, esx = O.w8a8_linear_dynamic(x.float().numpy(), qw, sw, bias)
+    np.testing.assert_array_equal(sx.cpu().numpy(), esx[:, 0])
+    np.testing.assert_array_equal(acc.cpu().numpy(), eacc)
+    np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+
+
+@pytest.mark.parametrize("m", [1, 2, 4])
+def test_fused_decode_o_shape_small_m(cuda, m):
+    """The O projection (4096 x 4096, one 64 KiB block per CU) takes the
+    workspace-free kernel at M <= 4: outputs, scales and accumulators."""
+    from nanopointllm_amd import _lib, w8a8
+
+    n, k = 4096, 4096
+    x = (torch.randn(m, k, generator=torch.Generator().manual_seed(m)) * 3).to(torch.float16)
+    _, qw, sw = weight_q(n, k, seed=5)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    swt, xc = torch.from_numpy(sw).to(cuda), x.to(cuda)
+    note(f"fused decode o-shape m={m}")
+    rc, y, sx = _linear_without_workspace(xc, wp, swt, None, n, _lib.EPI_DEQUANT, torch.float16)
+    assert rc == 0, _lib.load().w8a8_status_string(rc)
+    rc, acc, _ = _linear_without_workspace(xc, wp, swt, None, n, _lib.EPI_I32, torch.int32)
+    assert rc == 0
+    exp, eacc, _, esx = O.w8a8_linear_dynamic(x.float().numpy(), qw, sw)
     np.testing.assert_array_equal(sx.cpu().numpy(), esx[:, 0])
     np.testing.assert_array_equal(acc.cpu().numpy(), eacc)
     np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
@@ -363,14 +385,14 @@ def test_fused_decode_exact_ties(cuda, m):
 
 
 def test_fused_path_not_taken_for_small_shapes(cuda):
-    """O-sized and tiny projections go through quantization + GEMV (they need a
-    workspace) and give the same results."""
+    """O-sized projections at M = 8 and tiny ones go through quantization +
+    GEMV (they need a workspace) and give the same results."""
     from nanopointllm_amd import _lib, w8a8
 
     for n, k in [(4096, 4096), (40, 64), (16, 8)]:
         _, qw, sw = weight_q(n, k, seed=n + k)
         wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
-        x = torch.randn(4, k, generator=torch.Generator().manual_seed(k)).to(torch.float16)
+        x = torch.randn(8, k, generator=torch.Generator().manual_seed(k)).to(torch.float16)
         note(f"unfused decode n={n} k={k}")
         rc, _, _ = _linear_without_workspace(x.to(cuda), wp, torch.from_numpy(sw).to(cuda), None,
                                              n, _lib.EPI_DEQUANT, torch.float16)
