@@ -47,6 +47,9 @@ constexpr int kCacheNT = 2;
 constexpr int kBlockBytes = 1024;
 constexpr int kFusedMaxRows = 8;
 constexpr int kFusedMaxKB = 192;  // K <= 12288
+// 9 to 16 rows: full 16-row A fragments in LDS, so K is capped lower.
+constexpr int kFusedMaxRows16 = 16;
+constexpr int kFusedMaxKB16 = 96;  // K <= 6144
 constexpr int kFusedI8MinKB = 129;  // int8 x: K > 8192
 constexpr int kFusedMaxBlocks = 64;  // 16-row output blocks per workgroup
 static_assert(kFusedMaxBlocks * 16 == kFusedThreads, "one epilogue operand per thread");
@@ -145,19 +148,25 @@ __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
 // NCH: 16-byte x chunks each thread holds while quantizing (sized to the
 // shape, so small shapes keep their registers for the ring).  RING: register
 // buffers of the weight stream; RING - 1 steps are in flight in the main
-// loop, kFusedPreSteps of them during the quantization.
-template <int EPI, typename TX, typename TY, typename TH, int NCH, int RING>
+// loop, kFusedPreSteps of them during the quantization.  ROWS: activation
+// rows per A fragment in LDS, 8 (M <= 8, half a fragment; the other half is
+// zero) or 16 (M <= 16, K <= 6144).
+template <int EPI, typename TX, typename TY, typename TH, int NCH, int RING, int ROWS>
 __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p) {
   static_assert(NCH <= kFusedMaxChunks && RING >= 2 && kFusedPreSteps < RING,
                 "fused kernel shape");
+  static_assert(ROWS == kFusedMaxRows || ROWS == kFusedMaxRows16, "8 or 16 rows");
   // TX = int8_t: x comes quantized, with per-row scales (no quantization).
   constexpr bool kI8 = std::is_same<TX, int8_t>::value;
+  static_assert(!kI8 || ROWS == kFusedMaxRows, "int8 staging holds 8 rows");
+  constexpr int kAStride = ROWS * 64;  // LDS bytes of one k-block's A fragment
   static_assert(kFusedMaxKB * 4 <= kFusedThreads, "one int8 x chunk per thread and row");
   // A fragments: [kb][g][row < 8][16 bytes]
-  __shared__ __attribute__((aligned(16))) int8_t a_lds[kFusedMaxKB * 512];
+  __shared__ __attribute__((aligned(16)))
+      int8_t a_lds[ROWS == kFusedMaxRows ? kFusedMaxKB * 512 : kFusedMaxKB16 * 1024];
   __shared__ int32_t red[2][kFusedWaves][256];
   __shared__ uint32_t amax_w[kFusedWaves];
-  __shared__ float row_s[kFusedMaxRows];
+  __shared__ float row_s[ROWS];
   __shared__ float ops_lds[kFusedMaxBlocks * 32];  // per block: 16 scales, 16 biases
 
   const int tid = threadIdx.x;
@@ -282,7 +291,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   } else {
   // ---------------------------------------------------------- quantize x
   // Rows are spread over power-of-two groups of TPR >= 128 threads.
-  const int mpad = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
+  const int mpad = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : (M <= 8 ? 8 : 16)));
   const int tpr = kFusedThreads / mpad;
   const int row = tid / tpr;
   const int j0 = tid - row * tpr;
@@ -347,7 +356,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
           xv[2 * q + 1] = bits_to_f32<TX>(raw[i][q] >> 16);
         }
         u32x2 qw;
-        if constexpr (NCH <= 4) {
+        if constexpr (NCH <= 8) {
           qw = quant8_dyn(xv, s, r);
         } else {
           // Many chunks per thread leave no registers for the fast path.
@@ -357,7 +366,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
           qw = u32x2{pack4_i8(qi[0], qi[1], qi[2], qi[3]), pack4_i8(qi[4], qi[5], qi[6], qi[7])};
         }
         const int k = c * 8;
-        const int off = (((k >> 6) * 4 + ((k & 63) >> 4)) * 8 + row) * 16 + (k & 15);
+        const int off = (((k >> 6) * 4 + ((k & 63) >> 4)) * ROWS + row) * 16 + (k & 15);
         *reinterpret_cast<u32x2*>(a_lds + off) = qw;
       }
     }
@@ -369,7 +378,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
 
   // ------------------------------------------------------- stream weights
   const bool a_live = li < M;
-  const int a_off = (lg * 8 + li) * 16;
+  const int a_off = (lg * ROWS + li) * 16;
   i32x4 acc = i32x4{0, 0, 0, 0};
   int j = 0, c = 0;  // step being computed
   auto step = [&](const i32x4(&cur)[kFusedCH], i32x4(&freed)[kFusedCH], int t) {
@@ -379,7 +388,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
     for (int i = 0; i < kFusedCH; ++i) {
       const int kb = kb0 + c * kFusedCH + i;
       if (live && kb < kb1) {
-        const i32x4 a = a_live ? *reinterpret_cast<const i32x4*>(a_lds + kb * 512 + a_off)
+        const i32x4 a = a_live ? *reinterpret_cast<const i32x4*>(a_lds + kb * kAStride + a_off)
                                : i32x4{0, 0, 0, 0};
         acc = mfma_16x16x64(a, cur[i], acc);
       }
@@ -409,19 +418,27 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
 template <int EPI, typename TX, typename TY, typename TH>
 hipError_t launch_f(const FusedParams& p, hipStream_t st) {
   // x chunks per thread: rows spread over 1024 / mpad(M) threads each.
-  const int mpad = p.M <= 1 ? 1 : (p.M <= 2 ? 2 : (p.M <= 4 ? 4 : 8));
+  const int mpad = p.M <= 1 ? 1 : (p.M <= 2 ? 2 : (p.M <= 4 ? 4 : (p.M <= 8 ? 8 : 16)));
   const int per_thread = static_cast<int>(ceil_div(static_cast<int64_t>(p.KB) * 8,
                                                    kFusedThreads / mpad));
   const dim3 grid(p.G), block(kFusedThreads);
+  constexpr int R8 = kFusedMaxRows, R16 = kFusedMaxRows16;
   if constexpr (std::is_same<TX, int8_t>::value) {
-    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 1, 3>), grid, block, 0, st, p);
-  } else if (per_thread <= 2)
-    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 2, 3>), grid, block, 0, st, p);
-  else if (per_thread <= 4)
-    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 4, 3>), grid, block, 0, st, p);
-  else
-    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, kFusedMaxChunks, 3>), grid, block, 0,
-                       st, p);
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 1, 3, R8>), grid, block, 0, st, p);
+  } else if (p.M > kFusedMaxRows) {
+    if (per_thread <= 8)
+      hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 8, 3, R16>), grid, block, 0, st, p);
+    else
+      hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, kFusedMaxChunks, 3, R16>), grid,
+                         block, 0, st, p);
+  } else if (per_thread <= 2) {
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 2, 3, R8>), grid, block, 0, st, p);
+  } else if (per_thread <= 4) {
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 4, 3, R8>), grid, block, 0, st, p);
+  } else {
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, kFusedMaxChunks, 3, R8>), grid, block,
+                       0, st, p);
+  }
   return hipGetLastError();
 }
 
@@ -479,9 +496,10 @@ int cu_count() {
 // fused, O 4-7% faster than quantize + GEMV, down within 1%).
 bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
                           int64_t K) {
-  if (!((x_dtype == kF16 || x_dtype == kBF16) && M >= 1 && M <= kFusedMaxRows && K >= 8 &&
-        K % 8 == 0 && ceil_div(K, kTileK) <= kFusedMaxKB && ldx % 8 == 0 &&
-        (reinterpret_cast<uintptr_t>(x) & 15u) == 0))
+  if (!((x_dtype == kF16 || x_dtype == kBF16) && M >= 1 && M <= kFusedMaxRows16 && K >= 8 &&
+        K % 8 == 0 &&
+        ceil_div(K, kTileK) <= (M <= kFusedMaxRows ? kFusedMaxKB : kFusedMaxKB16) &&
+        ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0))
     return false;
   const int64_t nb = ceil_div(N, kTileRows);
   const int64_t g = nb < cu_count() ? nb : cu_count();

@@ -337,6 +337,81 @@ def test_fused_decode_path(cuda, m, n, k):
     np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
 
 
+@pytest.mark.parametrize("m", [9, 12, 13, 16])
+@pytest.mark.parametrize("n,k", [(32768, 1000), (131072, 256), (24576, 4096), (20480, 6144)])
+def test_fused_decode_16_rows(cuda, m, n, k):
+    """9 to 16 rows on the workspace-free kernel (full 16-row A fragments,
+    K <= 6144): outputs, row scales and int32 accumulators against the
+    oracle."""
+    from nanopointllm_amd import _lib, w8a8
+
+    g = torch.Generator().manual_seed(m * 77 + k)
+    x = (torch.randn(m, k, generator=g) * 2.0)
+    x[:, :: max(1, k // 5)] *= 25
+    x = x.to(torch.float16)
+    _, qw, sw = weight_q(n, k, seed=n + 11)
+    bias = np.linspace(-1, 1, n).astype(np.float32)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    swt, bt, xc = torch.from_numpy(sw).to(cuda), torch.from_numpy(bias).to(cuda), x.to(cuda)
+    note(f"fused decode 16 rows m={m} n={n} k={k}")
+    rc, y, sx = _linear_without_workspace(xc, wp, swt, bt, n, _lib.EPI_DEQUANT, torch.float16)
+    assert rc == 0, _lib.load().w8a8_status_string(rc)
+    rc, acc, _ = _linear_without_workspace(xc, wp, swt, None, n, _lib.EPI_I32, torch.int32)
+    assert rc == 0
+    exp, eacc, _, esx = O.w8a8_linear_dynamic(x.float().numpy(), qw, sw, bias)
+    np.testing.assert_array_equal(sx.cpu().numpy(), esx[:, 0])
+    np.testing.assert_array_equal(acc.cpu().numpy(), eacc)
+    np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+
+
+@pytest.mark.parametrize("m", [10, 16])
+def test_fused_decode_16_rows_silu_bf16_ties(cuda, m):
+    """The SiLU*mul epilogue, bfloat16 x and integer activations whose every
+    chunk holds exact ties, on the 16-row fused kernel."""
+    from nanopointllm_amd import _lib, w8a8
+
+    inter, k = 12288, 4096
+    g = torch.Generator().manual_seed(m)
+    x = (torch.randn(m, k, generator=g) * 3).to(torch.float16)
+    _, qw, sw = weight_q(2 * inter, k, seed=m + 100)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda), _lib.ROWS_INTERLEAVE_HALVES)
+    sp = O.pack_gateup_rows(sw[:inter, None], sw[inter:, None], "interleave")[:, 0]
+    qp = O.pack_gateup_rows(qw[:inter], qw[inter:], "interleave")
+    spt = torch.from_numpy(np.ascontiguousarray(sp)).to(cuda)
+    note(f"fused decode 16 rows silu m={m}")
+    rc, h, sx = _linear_without_workspace(x.to(cuda), wp, spt, None, 2 * inter, _lib.EPI_SILU_MUL,
+                                          torch.float16)
+    assert rc == 0, _lib.load().w8a8_status_string(rc)
+    eq, es = O.dynamic_per_token_quant(x.float().numpy())
+    np.testing.assert_array_equal(sx.cpu().numpy(), es[:, 0])
+    eh = O.gateup_silu_mul_from_acc(O.int32_matmul_f64(eq, qp), es, sp, layout="interleave")
+    key = lambda v: (lambda i: np.where(i < 0, -(i & 0x7FFF), i))(
+        v.astype(np.float16).view(np.int16).astype(np.int32))
+    u = np.abs(key(f16_to_np(h)) - key(eh))
+    assert u.max() <= 2 and np.mean(u == 0) > 0.999
+    # bfloat16 x, dequant to bfloat16
+    n = 2 * inter  # 6 blocks per CU: the routing takes the fused kernel up to M = 16
+    wq = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    swq = torch.from_numpy(sw).to(cuda)
+    xb = (torch.randn(m, k, generator=g) * 2).to(torch.bfloat16)
+    rc, yb, sxb = _linear_without_workspace(xb.to(cuda), wq, swq, None, n, _lib.EPI_DEQUANT,
+                                            torch.bfloat16)
+    assert rc == 0
+    exp, _, _, esx = O.w8a8_linear_dynamic(xb.float().numpy(), qw, sw)
+    np.testing.assert_array_equal(sxb.cpu().numpy(), esx[:, 0])
+    np.testing.assert_array_equal(yb.float().cpu().numpy(),
+                                  torch.from_numpy(exp).to(torch.bfloat16).float().numpy())
+    # ties: integer activations with |x|max = 254 give s = 2
+    xt = torch.randint(-254, 255, (m, k), generator=g).to(torch.float16)
+    xt[:, 0] = 254
+    rc, acc, sxt = _linear_without_workspace(xt.to(cuda), wq, swq, None, n, _lib.EPI_I32,
+                                             torch.int32)
+    assert rc == 0
+    tq, ts = O.dynamic_per_token_quant(xt.float().numpy())
+    np.testing.assert_array_equal(sxt.cpu().numpy(), ts[:, 0])
+    np.testing.assert_array_equal(acc.cpu().numpy(), O.int32_matmul_f64(tq, qw))
+
+
 @pytest.mark.parametrize("m", [1, 2, 4])
 def test_fused_decode_o_shape_small_m(cuda, m):
     """The O projection (4096 x 4096, one 64 KiB block per CU) takes the
