@@ -117,19 +117,28 @@ LinearOperands make_ops(const int8_t* a, int64_t lda, const float* sx, const int
   return op;
 }
 
+// GEMV or GEMM for an m x n product.  The GEMV's time grows with M (each
+// weight fragment meets M activation rows) while the GEMM's barely does at
+// M <= 64; measured on MI355X with LLaMA-7B shapes at M = 24..64, the GEMM
+// wins once M * N >= 32 * 12288 (QKV from M = 32, gate/up from M = 24) and
+// the GEMV keeps the N = 4096 projections (O, down) up to M = 64.
+inline bool use_gemv(int64_t m, int64_t n) {
+  return m <= kGemvMaxRows && (m <= 16 || m * n < 32 * 12288);
+}
+
 // Runs the int8 product for activations already staged in `act` (row-major
 // [m, round_up(k,64)] for the GEMV, packed tiles for the GEMM).
 inline hipError_t run_product(const LinearOperands& op, hipStream_t st) {
-  return op.M <= kGemvMaxRows ? launch_gemv(op, st) : launch_gemm(op, st);
+  return use_gemv(op.M, op.N) ? launch_gemv(op, st) : launch_gemm(op, st);
 }
 
 // Stages caller int8 activations for run_product: the GEMV reads them in
 // place when rows are 16-byte aligned and zero-padded reads are not needed;
 // otherwise they are copied (GEMV) or packed (GEMM) into the workspace.
-inline hipError_t stage_i8(const int8_t* xq, int64_t ldq, int64_t m, int64_t k, int8_t* act,
-                           const int8_t** a, int64_t* lda, hipStream_t st) {
+inline hipError_t stage_i8(const int8_t* xq, int64_t ldq, int64_t m, int64_t n, int64_t k,
+                           int8_t* act, const int8_t** a, int64_t* lda, hipStream_t st) {
   const int64_t kp = round_up(k, kTileK);
-  if (m <= kGemvMaxRows) {
+  if (use_gemv(m, n)) {
     if (k % kTileK == 0 && ldq % 16 == 0 && aligned(xq, 16)) {
       *a = xq;
       *lda = ldq;
@@ -235,7 +244,7 @@ int w8a8_gemm_i32(const int8_t* xq, int64_t ldq, const int8_t* w_packed, int32_t
   int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
   const int8_t* a = nullptr;
   int64_t lda = 0;
-  hipError_t e = stage_i8(xq, ldq, m, k, act, &a, &lda, stream);
+  hipError_t e = stage_i8(xq, ldq, m, n, k, act, &a, &lda, stream);
   if (e != hipSuccess) return status_of(e);
   LinearOperands op = make_ops(a, lda, nullptr, w_packed, nullptr, nullptr, W8A8_EPI_I32, acc,
                                kI32, ldacc, 0.0f, kF16, m, n, k);
@@ -271,7 +280,7 @@ int w8a8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
   float* sx = x_scale_out != nullptr ? x_scale_out : static_cast<float*>(workspace);
   int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
   const int64_t kp = round_up(k, kTileK);
-  const bool gemv = m <= kGemvMaxRows;
+  const bool gemv = use_gemv(m, n);
   hipError_t e = launch_quant_rows(x, x_dtype, ldx, m, k, nullptr, 0, act, kp, kp, !gemv, sx,
                                    stream);
   if (e != hipSuccess) return status_of(e);
@@ -298,7 +307,7 @@ int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
   int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
   const int8_t* a = nullptr;
   int64_t lda = 0;
-  hipError_t e = stage_i8(xq, ldq, m, k, act, &a, &lda, stream);
+  hipError_t e = stage_i8(xq, ldq, m, n, k, act, &a, &lda, stream);
   if (e != hipSuccess) return status_of(e);
   LinearOperands op = make_ops(a, lda, x_scale, w_packed, w_scale, bias, epilogue, y, y_dtype,
                                ldy, y_scale, inter_dtype, m, n, k);
@@ -351,7 +360,7 @@ int w8a8_linear_i8in_requant(const int8_t* xq, int64_t ldq, const int8_t* w_pack
   int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
   const int8_t* a = nullptr;
   int64_t lda = 0;
-  hipError_t e = stage_i8(xq, ldq, m, k, act, &a, &lda, stream);
+  hipError_t e = stage_i8(xq, ldq, m, n, k, act, &a, &lda, stream);
   if (e != hipSuccess) return status_of(e);
   LinearOperands op = make_ops(a, lda, nullptr, w_packed, nullptr, nullptr, W8A8_EPI_REQUANT, y,
                                kI8, ldy, 0.0f, kF16, m, n, k);

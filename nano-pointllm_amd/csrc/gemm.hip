@@ -1,4 +1,5 @@
-// Prefill-regime W8A8 GEMM (M > 64): y = epi(xq @ wq^T) with int8 MFMA.
+// Prefill-regime W8A8 GEMM (M > 64, or M > 16 with M * N >= 32 * 12288):
+// y = epi(xq @ wq^T) with int8 MFMA.
 //
 // Replaces the prefill/mixed projections (llama/paged_attention.py:1349-1352,
 // 1488; llama/lightweight_runner.py:320-404) for the int8 contract of

@@ -1,4 +1,5 @@
-// Decode-regime W8A8 GEMV (M <= 64): y[m, n] = epi(sum_k xq[m, k] * wq[n, k]).
+// Decode-regime W8A8 GEMV (M <= 16, or M <= 64 with M * N < 32 * 12288):
+// y[m, n] = epi(sum_k xq[m, k] * wq[n, k]).
 //
 // Replaces the F.linear call sites of the decode path
 // (llama/paged_attention.py:97-124, llama/lightweight_runner.py:38-54,
