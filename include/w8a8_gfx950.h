@@ -158,11 +158,11 @@ int w8a8_gemm_i32(const int8_t* xq, int64_t ldq, const int8_t* w_packed, int32_t
  *   epilogues); y_scale: static scale of W8A8_EPI_SILU_MUL_Q8; inter_dtype
  *   (F16/BF16): rounding type of the SiLU intermediates; x_scale_out: nullable
  *   [m], receives s_x.
- * Decode inputs (F16/BF16 x, 1 <= m <= 8, k % 8 == 0, k <= 12288, 16-byte
- * aligned, and per CU at least 128 KiB of weights and 4 weight bytes per
- * activation element) run as one kernel with the quantization fused in and
- * need no workspace (it may be null); every other case needs
- * w8a8_workspace_bytes(m, k) bytes.
+ * Decode inputs (F16/BF16 x, 1 <= m <= 8 with k <= 12288 or m <= 16 with
+ * k <= 6144, k % 8 == 0, 16-byte aligned, and per CU at least 64 KiB of
+ * weights and 4 weight bytes per activation element) run as one kernel with
+ * the quantization fused in and need no workspace (it may be null); every
+ * other case needs w8a8_workspace_bytes(m, k) bytes.
  */
 int w8a8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
                 const float* w_scale, const float* bias, int epilogue, void* y, int y_dtype,
