@@ -44,7 +44,7 @@ typedef enum w8a8_dtype {
 typedef enum w8a8_status {
   W8A8_OK = 0,
   W8A8_ERR_NULL = -1,      /* required pointer is null */
-  W8A8_ERR_SHAPE = -2,     /* negative size, leading dimension too small, K overflow */
+  W8A8_ERR_SHAPE = -2,     /* negative size, rows/N above INT32_MAX, leading dimension too small, K overflow */
   W8A8_ERR_DTYPE = -3,     /* unsupported dtype / epilogue combination */
   W8A8_ERR_ALIGN = -4,     /* pointer or leading dimension misaligned */
   W8A8_ERR_WORKSPACE = -5, /* workspace missing or too small */

@@ -15,6 +15,10 @@ thread_local int g_last_hip_error = 0;
 // (the overflow guard of compare_linear_bf16_qdq_integer, w8a8.py:152-153).
 constexpr int64_t kMaxK = ((int64_t{1} << 31) - 1) / (127 * 127);
 
+// Row and column counts are carried as int in the kernels' parameters and
+// launch one workgroup per row in the quantizers.
+constexpr int64_t kMaxRows = INT32_MAX;
+
 inline int status_of(hipError_t e) {
   if (e == hipSuccess) return W8A8_OK;
   g_last_hip_error = static_cast<int>(e);
@@ -78,7 +82,7 @@ inline int check_linear(const int8_t* w_packed, const float* w_scale, int epi, v
                         int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,
                         int64_t n, int64_t k) {
   if (m < 0 || n < 0 || k < 0) return W8A8_ERR_SHAPE;
-  if (k > kMaxK) return W8A8_ERR_SHAPE;
+  if (k > kMaxK || m > kMaxRows || n > kMaxRows) return W8A8_ERR_SHAPE;
   const int64_t cols = output_cols(epi, y_dtype, inter_dtype, n);
   if (cols < 0) return W8A8_ERR_DTYPE;
   if (m == 0 || n == 0) return W8A8_OK;
@@ -194,7 +198,7 @@ int64_t w8a8_workspace_bytes(int64_t m, int64_t k) {
 
 int w8a8_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
                     int8_t* q, int64_t ldq, float* scales, hipStream_t stream) {
-  if (rows < 0 || k < 0) return W8A8_ERR_SHAPE;
+  if (rows < 0 || k < 0 || rows > kMaxRows) return W8A8_ERR_SHAPE;
   if (!float_dtype(x_dtype)) return W8A8_ERR_DTYPE;
   if (rows == 0) return W8A8_OK;
   if (x == nullptr || q == nullptr || scales == nullptr) return W8A8_ERR_NULL;
@@ -208,7 +212,7 @@ int w8a8_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t
 int w8a8_quant_rows_scaled(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
                            const float* scale, int64_t scale_stride, int8_t* q, int64_t ldq,
                            hipStream_t stream) {
-  if (rows < 0 || k < 0 || scale_stride < 0) return W8A8_ERR_SHAPE;
+  if (rows < 0 || k < 0 || scale_stride < 0 || rows > kMaxRows) return W8A8_ERR_SHAPE;
   if (!float_dtype(x_dtype)) return W8A8_ERR_DTYPE;
   if (rows == 0) return W8A8_OK;
   if (x == nullptr || q == nullptr || scale == nullptr) return W8A8_ERR_NULL;
@@ -221,7 +225,7 @@ int w8a8_quant_rows_scaled(const void* x, int x_dtype, int64_t rows, int64_t k, 
 
 int w8a8_pack_rows(const int8_t* src, int64_t rows, int64_t k, int64_t ld, int layout,
                    int8_t* packed, hipStream_t stream) {
-  if (rows < 0 || k < 0) return W8A8_ERR_SHAPE;
+  if (rows < 0 || k < 0 || rows > kMaxRows) return W8A8_ERR_SHAPE;
   if (layout != W8A8_ROWS_AS_IS && layout != W8A8_ROWS_INTERLEAVE_HALVES) return W8A8_ERR_DTYPE;
   if (layout == W8A8_ROWS_INTERLEAVE_HALVES && rows % 2 != 0) return W8A8_ERR_SHAPE;
   if (rows == 0 || k == 0) return W8A8_OK;

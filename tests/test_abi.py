@@ -56,6 +56,12 @@ def test_invalid_arguments_return_status_without_launch():
     assert lib.w8a8_linear(fake, _lib.F16, 200000, fake, fake, None, _lib.EPI_DEQUANT, fake,
                            _lib.F16, 8, 0.0, _lib.F16, 1, 8, 133145, None, fake, 1 << 30,
                            None) == _lib.ERR_SHAPE
+    # M or N beyond the kernels' int range
+    assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_DEQUANT, fake,
+                           _lib.F16, 1 << 31, 0.0, _lib.F16, 1, 1 << 31, 64, None, fake,
+                           1 << 30, None) == _lib.ERR_SHAPE
+    assert lib.w8a8_quant_rows(fake, _lib.F16, 1 << 31, 4, 4, fake, 4, fake,
+                               None) == _lib.ERR_SHAPE
     # SiLU epilogue needs an even N and a 16-bit output
     assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_SILU_MUL, fake,
                            _lib.F32, 8, 0.0, _lib.F16, 1, 16, 64, None, fake, 1 << 20,
