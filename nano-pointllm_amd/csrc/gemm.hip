@@ -6,23 +6,23 @@
 // integer_linear_per_output_reference (nanopointllm/compression/w8a8.py:118-139).
 //
 // Design (MFMA-bound), chosen by measurement on MI355X:
-//   * v_mfma_i32_32x32x32_i8, which sustains ~2x the int8 rate of the
-//     16x16x64 form (4.4 vs 2.7 POPS in a register-only loop).
-//   * Every wavefront owns BC adjacent 32x32 output blocks; the workgroup
-//     tile is a WM x WN grid of them: 128x256 (16 wavefronts of 32x64) when
-//     there are enough such tiles to fill every CU twice, else 128x128 (16
-//     wavefronts of 32x32), else 64x64 with 4 wavefronts (4 workgroups per CU)
-//     when 128x128 tiles would not cover every CU.  Many resident wavefronts
-//     per SIMD hide the LDS and memory latency better than larger per-wave
-//     tiles did; the 32x64 block halves the activation reads from LDS.
+//   * v_mfma_i32_16x16x64_i8.  Its operand is exactly one packed 16x64
+//     fragment (lane l holds 16 bytes of row l%16), read with one contiguous
+//     ds_read_b128.  On random int8 data it sustains more than the 32x32x32
+//     form: 3.3 against 3.0 POPS from LDS alone, and 15-25% more in this
+//     kernel on LLaMA-7B shapes (the matrix pipes slow down with the
+//     data-dependent switching of their inputs).
+//   * Every wavefront owns a BR x BC grid of 16x16 output blocks; the
+//     workgroup tile is a WM x WN grid of wavefronts: 128x256 (8 wavefronts
+//     of 64x64) when there are enough such tiles to fill every CU twice, else
+//     128x128 (16 wavefronts of 32x32), else 64x64 (4 wavefronts of 32x32,
+//     4 workgroups per CU) when 128x128 tiles would not cover every CU.
 //   * Both operands are in the packed 16x64 tile layout, so a k-step (64) of
 //     the workgroup tile is (BM + BN)/16 fragments of 1 KiB.  Each wavefront
 //     copies its share with global_load_lds_dwordx4 straight into a 3- or
 //     4-stage LDS ring (lane l lands at slot base + 16*l, the fragment layout),
 //     keeping STG - 1 k-steps in flight; explicit vmcnt waits and one barrier
-//     per k-step order the ring.  A 32x32x32 operand is the lane slots of two
-//     adjacent 16-row tiles, read with ds_read_b128 as four contiguous
-//     256-byte runs.
+//     per k-step order the ring.
 //   * Workgroups are mapped XCD-major: consecutive tiles of the same weight
 //     column block land on the same XCD and share its L2.
 #include "w8a8_internal.h"
@@ -55,11 +55,12 @@ struct GemmParams {
 
 constexpr int kXcds = 8;
 
-typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
 typedef __attribute__((address_space(3))) void lds_void;
 
-__device__ inline i32x16 mfma_32x32x32(i32x4 a, i32x4 b, i32x16 c) {
-  return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+// C layout: lane l, register r holds row 4(l/16) + r (activation) and column
+// l%16 (weight row) of the 16x16 block.
+__device__ inline i32x4 mfma_16x16x64(i32x4 a, i32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
 // Waits until at most n of this wave's vector-memory loads (the LDS-DMA
@@ -76,16 +77,16 @@ __device__ inline void wait_vmcnt() {
 // overtake them; unlike __syncthreads it does not drain outstanding loads.
 __device__ inline void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// WM x WN wavefronts, each owning BC 32x32 blocks side by side (BM = 32 WM,
-// BN = 32 WN BC), with an STG-deep LDS ring.
+// WM x WN wavefronts, each owning BR x BC blocks of 16x16 (BM = 16 WM BR,
+// BN = 16 WN BC), with an STG-deep LDS ring.
 // The second launch bound is waves per SIMD: OCC workgroups of WM x WN
 // wavefronts over the CU's 4 SIMDs, so the register budget admits OCC
 // workgroups per CU.
-template <int WM, int WN, int BC, int STG, int OCC, int EPI, typename TY, typename TH>
+template <int WM, int WN, int BR, int BC, int STG, int OCC, int EPI, typename TY, typename TH>
 __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(GemmParams p) {
   constexpr int NW = WM * WN;
-  constexpr int BMF = 2 * WM;       // 16-row activation tiles per k-step
-  constexpr int BNF = 2 * WN * BC;  // 16-row weight tiles per k-step
+  constexpr int BMF = WM * BR;  // 16-row activation tiles per k-step
+  constexpr int BNF = WN * BC;  // 16-row weight tiles per k-step
   constexpr int F = BMF + BNF;
   // Fragment copies per wave per k-step: LPW for the first F - (LPW-1) NW
   // waves, LPW - 1 for the rest.
@@ -129,20 +130,18 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
             (lds_void*)(&lds[slot][q * NW + wave][0]), 16, 0, 0);
   };
 
-  i32x16 acc[BC];
+  i32x4 acc[BR][BC];
 #pragma unroll
-  for (int j = 0; j < BC; ++j)
+  for (int i = 0; i < BR; ++i)
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[j][r] = 0;
+    for (int j = 0; j < BC; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0;
 
 #pragma unroll
   for (int s = 0; s < STG - 1; ++s)
     if (s < KB) issue(s, s);
 
-  // 32x32x32 operands of k-half h: lane l takes 16 bytes of row l%32 of a
-  // 16-row tile pair at k 32h + 16(l/32): slot (l%16) + 16(2h + l/32) of
-  // tile (l%32)/16.
-  const int fhalf = (lane >> 4) & 1;
   for (int kb = 0; kb < KB; ++kb) {
     // Stage kb has landed once only the later stages' loads may remain.
     if (kb + STG - 2 < KB) {
@@ -158,25 +157,24 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
     // Every wave has finished reading the slot of stage kb-1: refill it.
     if (kb + STG - 1 < KB) issue(kb + STG - 1, (kb + STG - 1) % STG);
     const int slot = kb % STG;
+    i32x4 af[BR], bf[BC];
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int fslot = (lane & 15) + 16 * (2 * h + (lane >> 5));
-      const i32x4 af = lds[slot][2 * wm + fhalf][fslot];
-      i32x4 bf[BC];
+    for (int i = 0; i < BR; ++i) af[i] = lds[slot][wm * BR + i][lane];
 #pragma unroll
-      for (int j = 0; j < BC; ++j) bf[j] = lds[slot][BMF + 2 * (wn * BC + j) + fhalf][fslot];
+    for (int j = 0; j < BC; ++j) bf[j] = lds[slot][BMF + wn * BC + j][lane];
 #pragma unroll
-      for (int j = 0; j < BC; ++j) acc[j] = mfma_32x32x32(af, bf[j], acc[j]);
-    }
+    for (int i = 0; i < BR; ++i)
+#pragma unroll
+      for (int j = 0; j < BC; ++j) acc[i][j] = mfma_16x16x64(af[i], bf[j], acc[i][j]);
   }
 
-  // Epilogue.  Register r of block j in lane l holds row (mb0 + 2wm)*16 +
-  // 8(r/4) + 4(l/32) + r%4 and column (nb0 + 2(wn BC + j))*16 + l%32.
+  // Epilogue.  Register r of block (i, j) in lane l holds tile row
+  // 16(wm BR + i) + 4(l/16) + r and tile column 16(wn BC + j) + l%16.
   // When the output tile fits in the LDS ring, the values go to LDS first and
-  // leave as 16-byte row chunks (a lane's own values are 2 rows x 32 columns
-  // apart, so stored directly they make short partial-line writes).
-  constexpr int BM = 32 * WM;
-  constexpr int BN = 32 * WN * BC;
+  // leave as 16-byte row chunks (stored directly, 16 lanes cover only 16
+  // columns of a row: short partial-line writes).
+  constexpr int BM = 16 * WM * BR;
+  constexpr int BN = 16 * WN * BC;
   constexpr bool kHalfCols = EPI == kEpiSilu || EPI == kEpiSiluQ8;  // one output per gate/up pair
   constexpr int BNO = kHalfCols ? BN / 2 : BN;
   constexpr int kOutBytes = static_cast<int>(sizeof(TY));
@@ -192,8 +190,10 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
     }
   };
 #pragma unroll
+  for (int i = 0; i < BR; ++i)
+#pragma unroll
   for (int j = 0; j < BC; ++j) {
-    const int nl = 32 * (wn * BC + j) + (lane & 31);
+    const int nl = 16 * (wn * BC + j) + (lane & 15);
     const int64_t n = static_cast<int64_t>(nb0) * 16 + nl;
     const bool n_ok = n < p.N;
     float swn = 0.0f;
@@ -207,38 +207,60 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
         rq_bias = p.rq_bias != nullptr ? p.rq_bias[n] : 0;
       }
     }
+    if constexpr (kHalfCols) {
+      // Interleaved gate/up: even column = gate, odd column = up of output
+      // n / 2.  Every lane dequantizes its own column at rows r and r + 1;
+      // then the even lane forms output row r from its gate and the odd
+      // lane's up, and the odd lane output row r + 1 from the even lane's
+      // gate and its own up, so each SiLU is evaluated by one lane.
+      const bool odd = (lane & 1) != 0;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int ml = 32 * wm + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      const int m = mb0 * 16 + ml;
-      const bool m_ok = m < p.M;
-      const bool ok = m_ok && n_ok;
-      const int32_t a = acc[j][r];
-      if constexpr (EPI == kEpiI32) {
-        put(ml, nl, ok, m, n, a);
-      } else if constexpr (EPI == kEpiDequant) {
-        const float sxm = m_ok ? p.sx[m] : 0.0f;
-        put(ml, nl, ok, m, n, from_f32<TY>(dequant1(a, sxm, swn, ok ? p.bias : nullptr, n)));
-      } else if constexpr (EPI == kEpiRequant) {
-        put(ml, nl, ok, m, n, static_cast<int8_t>(requant1(a, rq_bias, rq_mult, rq_shift)));
-      } else if constexpr (EPI == kEpiBf16Exact) {
-        const float sxm = m_ok ? p.sx[m] : 0.0f;
-        put(ml, nl, ok, m, n,
-            __builtin_bit_cast(TY, dequant_bf16_exact(a, f16_bits(sxm), f16_bits(swn))));
-      } else {
-        // Interleaved gate/up: even column = gate, odd column = up of output
-        // n / 2.  Every lane dequantizes its own column; the even lane takes
-        // the up value from its odd neighbour.
-        const float sxm = m_ok ? p.sx[m] : 0.0f;
-        const float v = ok ? to_f32(from_f32<TH>(dequant1(a, sxm, swn, p.bias, n))) : 0.0f;
-        const float u = __shfl_xor(v, 1);
-        if ((lane & 1) == 0) {
-          const TH h = from_f32<TH>(silu_mul<TH>(v, u));
-          if constexpr (EPI == kEpiSilu) {
-            put(ml, nl / 2, ok, m, n / 2, h);
-          } else {
-            put(ml, nl / 2, ok, m, n / 2, static_cast<int8_t>(quant1(to_f32(h), p.out_scale)));
-          }
+      for (int r = 0; r < 4; r += 2) {
+        const int ml0 = 16 * (wm * BR + i) + 4 * (lane >> 4) + r;
+        float v[2];
+        bool vok[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const int m = mb0 * 16 + ml0 + e;
+          const bool m_ok = m < p.M;
+          vok[e] = m_ok && n_ok;
+          const float sxm = m_ok ? p.sx[m] : 0.0f;
+          v[e] = vok[e] ? to_f32(from_f32<TH>(dequant1(acc[i][j][r + e], sxm, swn, p.bias, n)))
+                        : 0.0f;
+        }
+        const float x = __shfl_xor(odd ? v[0] : v[1], 1);
+        const float g = odd ? x : v[0];
+        const float u = odd ? v[1] : x;
+        const int ml = ml0 + (odd ? 1 : 0);
+        const int64_t m = static_cast<int64_t>(mb0) * 16 + ml;
+        const bool ok = odd ? vok[1] : vok[0];
+        const TH h = from_f32<TH>(silu_mul<TH>(g, u));
+        if constexpr (EPI == kEpiSilu) {
+          put(ml, nl / 2, ok, m, n / 2, h);
+        } else {
+          put(ml, nl / 2, ok, m, n / 2, static_cast<int8_t>(quant1(to_f32(h), p.out_scale)));
+        }
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int ml = 16 * (wm * BR + i) + 4 * (lane >> 4) + r;
+        const int m = mb0 * 16 + ml;
+        const bool m_ok = m < p.M;
+        const bool ok = m_ok && n_ok;
+        const int32_t a = acc[i][j][r];
+        if constexpr (EPI == kEpiI32) {
+          put(ml, nl, ok, m, n, a);
+        } else if constexpr (EPI == kEpiDequant) {
+          const float sxm = m_ok ? p.sx[m] : 0.0f;
+          put(ml, nl, ok, m, n, from_f32<TY>(dequant1(a, sxm, swn, ok ? p.bias : nullptr, n)));
+        } else if constexpr (EPI == kEpiRequant) {
+          put(ml, nl, ok, m, n, static_cast<int8_t>(requant1(a, rq_bias, rq_mult, rq_shift)));
+        } else {
+          static_assert(EPI == kEpiBf16Exact, "epilogue");
+          const float sxm = m_ok ? p.sx[m] : 0.0f;
+          put(ml, nl, ok, m, n,
+              __builtin_bit_cast(TY, dequant_bf16_exact(a, f16_bits(sxm), f16_bits(swn))));
         }
       }
     }
@@ -276,43 +298,39 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
 
 // Launches one tile configuration for the problem in p (tile counts are
 // filled in here).
-template <int WM, int WN, int BC, int STG, int OCC, int EPI, typename TY, typename TH>
+template <int WM, int WN, int BR, int BC, int STG, int OCC, int EPI, typename TY, typename TH>
 hipError_t launch_cfg(GemmParams p, hipStream_t st) {
-  p.tiles_m = static_cast<int>(ceil_div(p.MB, 2 * WM));
-  const int tiles_n = static_cast<int>(ceil_div(p.NB, 2 * WN * BC));
+  p.tiles_m = static_cast<int>(ceil_div(p.MB, WM * BR));
+  const int tiles_n = static_cast<int>(ceil_div(p.NB, WN * BC));
   p.tiles = p.tiles_m * tiles_n;
   p.per_xcd = static_cast<int>(ceil_div(p.tiles, kXcds));
   if (p.tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_kernel<WM, WN, BC, STG, OCC, EPI, TY, TH>), dim3(p.per_xcd * kXcds),
-                     dim3(WM * WN * 64), 0, st, p);
+  hipLaunchKernelGGL((gemm_kernel<WM, WN, BR, BC, STG, OCC, EPI, TY, TH>),
+                     dim3(p.per_xcd * kXcds), dim3(WM * WN * 64), 0, st, p);
   return hipGetLastError();
 }
 
 // Tile configurations, chosen by tile count (measured on MI355X, random data,
 // cold weights, LLaMA-7B projections at M = 256..2048):
-//   * 128x256, 16 waves of 32x64 blocks, 3-stage ring, 2 workgroups per CU,
-//     when there are at least ~0.82 tiles per workgroup slot (2 per CU): each
-//     MFMA moves 1.5 KiB of operands through LDS instead of 2, 3-12% faster.
-//     Just past one full round of slots (1 to 1.16 tiles per slot) the few
-//     tiles of the second round cost more than that saves, and the 128x128
-//     tile is kept;
+//   * 128x256, 8 waves of 64x64, 3-stage ring, 2 workgroups per CU, when
+//     there are at least ~0.82 tiles per workgroup slot (2 per CU): each
+//     MFMA moves half as many operand bytes through LDS as with 32x32 per
+//     wave.  Just past one full round of slots (1 to 1.25 tiles per slot) the
+//     few tiles of the second round cost more than that saves, and the
+//     128x128 tile is kept;
 //   * else 128x128, 16 waves of 32x32, 4 stages, 2 per CU, when those cover
 //     every CU;
-//   * else 64x64, 4 waves, 4 per CU.
+//   * else 64x64, 4 waves of 32x32, 4 per CU.
 template <int EPI, typename TY, typename TH>
 hipError_t launch_t(const GemmParams& p, hipStream_t st) {
-  // (The integer-requant epilogue needs more registers than two workgroups
-  // per CU leave it, so it keeps the 128x128 tile.)
-  if constexpr (EPI != kEpiRequant) {
-    const int64_t wide_tiles = ceil_div(p.MB, 8) * ceil_div(p.NB, 16);
-    const int64_t slots = static_cast<int64_t>(cu_count()) * 2;
-    const bool short_second_round = wide_tiles > slots && wide_tiles * 100 < slots * 116;
-    if (wide_tiles * 100 >= slots * 82 && !short_second_round)
-      return launch_cfg<4, 4, 2, 3, 2, EPI, TY, TH>(p, st);
-  }
+  const int64_t wide_tiles = ceil_div(p.MB, 8) * ceil_div(p.NB, 16);
+  const int64_t slots = static_cast<int64_t>(cu_count()) * 2;
+  const bool short_second_round = wide_tiles > slots && wide_tiles * 100 < slots * 125;
+  if (wide_tiles * 100 >= slots * 82 && !short_second_round)
+    return launch_cfg<2, 4, 4, 4, 3, 2, EPI, TY, TH>(p, st);
   const int64_t big_tiles = ceil_div(p.MB, 8) * ceil_div(p.NB, 8);
-  if (big_tiles >= cu_count()) return launch_cfg<4, 4, 1, 4, 2, EPI, TY, TH>(p, st);
-  return launch_cfg<2, 2, 1, 4, 4, EPI, TY, TH>(p, st);
+  if (big_tiles >= cu_count()) return launch_cfg<4, 4, 2, 2, 4, 2, EPI, TY, TH>(p, st);
+  return launch_cfg<2, 2, 2, 2, 4, 4, EPI, TY, TH>(p, st);
 }
 
 }  // namespace

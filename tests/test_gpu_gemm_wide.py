@@ -1,14 +1,14 @@
 """Prefill GEMM shapes with enough 128x256 output tiles to fill the chip twice
-over, which select the wide tile (16 waves of 32x64 blocks, three LDS stages).
+over, which select the wide tile (8 waves of 64x64 blocks, three LDS stages).
 
 Bars as for every GEMM path: int32 accumulators bit-exact against the
 oracle's integer product; binary16 / bfloat16 / binary32 dequant outputs
 bit-equal to the oracle's dequant (w8a8.py:118-139) rounded once; SiLU*mul
 within two binary16 ulps and >99.9% bit-equal; the int8 requant of SiLU*mul
 bit-exact against the oracle applied to the kernel's own binary16 h.  Shapes
-are ragged in M, N and K (partial tiles, a partial last 32x64 block, K not a
-multiple of 64).  The integer requant epilogue (requant1) keeps the 128x128
-tile at every shape.
+are ragged in M, N and K (partial tiles, a partial last 16-row block, K not a
+multiple of 64).  The integer requant epilogue (requant1) takes the same
+tiles as the others.
 """
 from __future__ import annotations
 
@@ -37,10 +37,10 @@ def _ulps16(a, b):
 
 def _selects_wide(m, n, cus=256):
     """The launch rule on the MI355X's 256 CUs (two workgroup slots each):
-    at least 0.82 tiles per slot, and not 1 to 1.16."""
+    at least 0.82 tiles per slot, and not 1 to 1.25."""
     mb, nb = -(-m // 16), -(-n // 16)
     r = -(-mb // 8) * -(-nb // 16) / (2 * cus)
-    return r >= 0.82 and not 1 < r < 1.16
+    return r >= 0.82 and not 1 < r < 1.25
 
 
 def _case(m, n, k, seed):
@@ -103,8 +103,8 @@ def test_wide_tile_silu_mul_and_int8_chain(cuda):
 
 
 def test_requant1_epilogue_at_a_wide_shape(cuda):
-    """The integer requant epilogue at a shape that would select the wide tile:
-    equal to requantize_int32 of the exact product (that kernel is pinned to the
+    """The integer requant epilogue on the wide tile: equal to
+    requantize_int32 of the exact product (that kernel is pinned to the
     oracle elsewhere), and a random sample of entries against the oracle."""
     from nanopointllm_amd import integer_epilogues as E, w8a8
 
