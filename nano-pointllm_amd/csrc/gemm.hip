@@ -78,20 +78,23 @@ __device__ inline void wait_vmcnt() {
 __device__ inline void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // WM x WN wavefronts, each owning BR x BC blocks of 16x16 (BM = 16 WM BR,
-// BN = 16 WN BC), with an STG-deep LDS ring.
+// BN = 16 WN BC), with an STG-deep LDS ring whose stages hold KT k-blocks
+// (64 K each) of both operands.
 // The second launch bound is waves per SIMD: OCC workgroups of WM x WN
 // wavefronts over the CU's 4 SIMDs, so the register budget admits OCC
 // workgroups per CU.
-template <int WM, int WN, int BR, int BC, int STG, int OCC, int EPI, typename TY, typename TH>
+template <int WM, int WN, int BR, int BC, int STG, int OCC, int KT, int EPI, typename TY,
+          typename TH>
 __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(GemmParams p) {
   constexpr int NW = WM * WN;
-  constexpr int BMF = WM * BR;  // 16-row activation tiles per k-step
-  constexpr int BNF = WN * BC;  // 16-row weight tiles per k-step
+  constexpr int BMF = WM * BR;  // 16-row activation tiles per k-block
+  constexpr int BNF = WN * BC;  // 16-row weight tiles per k-block
   constexpr int F = BMF + BNF;
-  // Fragment copies per wave per k-step: LPW for the first F - (LPW-1) NW
+  constexpr int FS = F * KT;    // fragments per stage
+  // Fragment copies per wave per stage: LPW for the first FS - (LPW-1) NW
   // waves, LPW - 1 for the rest.
-  constexpr int LPW = (F + NW - 1) / NW;
-  __shared__ i32x4 lds[STG][F][64];
+  constexpr int LPW = (FS + NW - 1) / NW;
+  __shared__ i32x4 lds[STG][FS][64];
 
   // XCD-major tile mapping: workgroup b runs on XCD b % 8.
   const int b = blockIdx.x;
@@ -105,29 +108,37 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
   const int wm = wave / WN;
   const int wn = wave % WN;
   const int KB = p.KB;
+  const int NS = static_cast<int>(ceil_div(KB, KT));  // ring stages over K
 
-  // Fragment f = q*NW + wave of each k-step: f < BMF are activation blocks
-  // mb0 + f, the rest weight blocks nb0 + f - BMF.  Blocks past the operand
-  // are clamped to its last block: their products only reach accumulator
-  // rows or columns that the epilogue never stores.
-  const bool full = (LPW - 1) * NW + wave < F;  // wave-uniform
+  // Fragment f = q*NW + wave of a stage is k-block f / F of the stage; of
+  // that k-block, g = f % F < BMF are activation blocks mb0 + g, the rest
+  // weight blocks nb0 + g - BMF.  Blocks past the operand are clamped to its
+  // last block: their products only reach accumulator rows or columns that
+  // the epilogue never stores.  K-blocks past KB (the last stage of a K that
+  // is not a multiple of 64 KT) reload block KB - 1 and are not multiplied.
+  const bool full = (LPW - 1) * NW + wave < FS;  // wave-uniform
   const i32x4* src[LPW];
+  int kk_of[LPW];
 #pragma unroll
   for (int q = 0; q < LPW; ++q) {
-    const int f = min(q * NW + wave, F - 1);
-    if (f < BMF) {
-      src[q] = p.a + static_cast<int64_t>(min(mb0 + f, p.MB - 1)) * KB * 64 + lane;
+    const int f = min(q * NW + wave, FS - 1);
+    const int g = f % F;
+    kk_of[q] = f / F;
+    if (g < BMF) {
+      src[q] = p.a + static_cast<int64_t>(min(mb0 + g, p.MB - 1)) * KB * 64 + lane;
     } else {
-      src[q] = p.w + static_cast<int64_t>(min(nb0 + f - BMF, p.NB - 1)) * KB * 64 + lane;
+      src[q] = p.w + static_cast<int64_t>(min(nb0 + g - BMF, p.NB - 1)) * KB * 64 + lane;
     }
   }
-  auto issue = [&](int kb, int slot) {
+  auto issue = [&](int stage, int slot) {
 #pragma unroll
     for (int q = 0; q < LPW; ++q)
-      if (q < LPW - 1 || full)
+      if (q < LPW - 1 || full) {
+        const int kb = min(stage * KT + kk_of[q], KB - 1);
         __builtin_amdgcn_global_load_lds(
             static_cast<const void*>(src[q] + static_cast<int64_t>(kb) * 64),
             (lds_void*)(&lds[slot][q * NW + wave][0]), 16, 0, 0);
+      }
   };
 
   i32x4 acc[BR][BC];
@@ -140,11 +151,11 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
 
 #pragma unroll
   for (int s = 0; s < STG - 1; ++s)
-    if (s < KB) issue(s, s);
+    if (s < NS) issue(s, s);
 
-  for (int kb = 0; kb < KB; ++kb) {
-    // Stage kb has landed once only the later stages' loads may remain.
-    if (kb + STG - 2 < KB) {
+  for (int st = 0; st < NS; ++st) {
+    // Stage st has landed once only the later stages' loads may remain.
+    if (st + STG - 2 < NS) {
       if (full) {
         wait_vmcnt<LPW * (STG - 2)>();
       } else {
@@ -154,18 +165,23 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
       wait_vmcnt<0>();
     }
     ring_barrier();
-    // Every wave has finished reading the slot of stage kb-1: refill it.
-    if (kb + STG - 1 < KB) issue(kb + STG - 1, (kb + STG - 1) % STG);
-    const int slot = kb % STG;
-    i32x4 af[BR], bf[BC];
+    // Every wave has finished reading the slot of stage st-1: refill it.
+    if (st + STG - 1 < NS) issue(st + STG - 1, (st + STG - 1) % STG);
+    const int slot = st % STG;
 #pragma unroll
-    for (int i = 0; i < BR; ++i) af[i] = lds[slot][wm * BR + i][lane];
+    for (int kk = 0; kk < KT; ++kk) {
+      if (KT == 1 || st * KT + kk < KB) {
+        i32x4 af[BR], bf[BC];
 #pragma unroll
-    for (int j = 0; j < BC; ++j) bf[j] = lds[slot][BMF + wn * BC + j][lane];
+        for (int i = 0; i < BR; ++i) af[i] = lds[slot][kk * F + wm * BR + i][lane];
 #pragma unroll
-    for (int i = 0; i < BR; ++i)
+        for (int j = 0; j < BC; ++j) bf[j] = lds[slot][kk * F + BMF + wn * BC + j][lane];
 #pragma unroll
-      for (int j = 0; j < BC; ++j) acc[i][j] = mfma_16x16x64(af[i], bf[j], acc[i][j]);
+        for (int i = 0; i < BR; ++i)
+#pragma unroll
+          for (int j = 0; j < BC; ++j) acc[i][j] = mfma_16x16x64(af[i], bf[j], acc[i][j]);
+      }
+    }
   }
 
   // Epilogue.  Register r of block (i, j) in lane l holds tile row
@@ -178,7 +194,7 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
   constexpr bool kHalfCols = EPI == kEpiSilu || EPI == kEpiSiluQ8;  // one output per gate/up pair
   constexpr int BNO = kHalfCols ? BN / 2 : BN;
   constexpr int kOutBytes = static_cast<int>(sizeof(TY));
-  constexpr bool kStage = BM * BNO * kOutBytes <= STG * F * 1024 && (BNO * kOutBytes) % 16 == 0;
+  constexpr bool kStage = BM * BNO * kOutBytes <= STG * FS * 1024 && (BNO * kOutBytes) % 16 == 0;
   [[maybe_unused]] TY* const stile = reinterpret_cast<TY*>(&lds[0][0][0]);
   if constexpr (kStage) ring_barrier();  // every wave is done reading the ring
   // Writes output (m, n_out) of tile-local row ml and column nlo.
@@ -298,39 +314,50 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
 
 // Launches one tile configuration for the problem in p (tile counts are
 // filled in here).
-template <int WM, int WN, int BR, int BC, int STG, int OCC, int EPI, typename TY, typename TH>
+template <int WM, int WN, int BR, int BC, int STG, int OCC, int KT, int EPI, typename TY,
+          typename TH>
 hipError_t launch_cfg(GemmParams p, hipStream_t st) {
   p.tiles_m = static_cast<int>(ceil_div(p.MB, WM * BR));
   const int tiles_n = static_cast<int>(ceil_div(p.NB, WN * BC));
   p.tiles = p.tiles_m * tiles_n;
   p.per_xcd = static_cast<int>(ceil_div(p.tiles, kXcds));
   if (p.tiles == 0) return hipSuccess;
-  hipLaunchKernelGGL((gemm_kernel<WM, WN, BR, BC, STG, OCC, EPI, TY, TH>),
+  hipLaunchKernelGGL((gemm_kernel<WM, WN, BR, BC, STG, OCC, KT, EPI, TY, TH>),
                      dim3(p.per_xcd * kXcds), dim3(WM * WN * 64), 0, st, p);
   return hipGetLastError();
 }
 
 // Tile configurations, chosen by tile count (measured on MI355X, random data,
 // cold weights, LLaMA-7B projections at M = 256..2048):
-//   * 128x256, 8 waves of 64x64, 3-stage ring, 2 workgroups per CU, when
-//     there are at least ~0.82 tiles per workgroup slot (2 per CU): each
-//     MFMA moves half as many operand bytes through LDS as with 32x32 per
-//     wave.  Just past one full round of slots (1 to 1.25 tiles per slot) the
-//     few tiles of the second round cost more than that saves, and the
-//     128x128 tile is kept;
-//   * else 128x128, 16 waves of 32x32, 4 stages, 2 per CU, when those cover
-//     every CU;
-//   * else 64x64, 4 waves of 32x32, 4 per CU.
+//   * 128x256, 8 waves of 64x64, 3-stage ring of one k-block, 2 workgroups
+//     per CU, when there are at least ~0.82 tiles per workgroup slot (2 per
+//     CU): each MFMA moves half as many operand bytes through LDS as with
+//     32x32 per wave.  Just past one full round of slots (1 to 1.25 tiles
+//     per slot) the few tiles of the second round cost more than that saves,
+//     and the 128x128 tile is kept;
+//   * else 128x128, 16 waves of 32x32, 4-stage ring of one k-block, 2 per
+//     CU, when there are more of those tiles than CUs;
+//   * else, when 64x64 tiles fit in two per CU: 64x64, 4 waves of 32x32,
+//     2-stage ring of four k-blocks (256 K), 2 per CU;
+//   * else 128x128 with a 4-stage ring of two k-blocks (128 K), one per CU.
+//     With one round of tiles or less, every k-step's barrier and memory
+//     latency is exposed: stages of several k-blocks cut the barriers, and
+//     the deeper ring keeps more bytes in flight per CU (96 KiB).  With
+//     weights streamed from HBM these are 8-14% faster on O and down at
+//     M = 560..1024, and the 64x64 form 15-20% at M = 384.
 template <int EPI, typename TY, typename TH>
 hipError_t launch_t(const GemmParams& p, hipStream_t st) {
+  const int64_t cus = cu_count();
   const int64_t wide_tiles = ceil_div(p.MB, 8) * ceil_div(p.NB, 16);
-  const int64_t slots = static_cast<int64_t>(cu_count()) * 2;
+  const int64_t slots = cus * 2;
   const bool short_second_round = wide_tiles > slots && wide_tiles * 100 < slots * 125;
   if (wide_tiles * 100 >= slots * 82 && !short_second_round)
-    return launch_cfg<2, 4, 4, 4, 3, 2, EPI, TY, TH>(p, st);
+    return launch_cfg<2, 4, 4, 4, 3, 2, 1, EPI, TY, TH>(p, st);
   const int64_t big_tiles = ceil_div(p.MB, 8) * ceil_div(p.NB, 8);
-  if (big_tiles >= cu_count()) return launch_cfg<4, 4, 2, 2, 4, 2, EPI, TY, TH>(p, st);
-  return launch_cfg<2, 2, 2, 2, 4, 4, EPI, TY, TH>(p, st);
+  if (big_tiles > cus) return launch_cfg<4, 4, 2, 2, 4, 2, 1, EPI, TY, TH>(p, st);
+  const int64_t small_tiles = ceil_div(p.MB, 4) * ceil_div(p.NB, 4);
+  if (small_tiles <= slots) return launch_cfg<2, 2, 2, 2, 2, 2, 4, EPI, TY, TH>(p, st);
+  return launch_cfg<4, 4, 2, 2, 4, 1, 2, EPI, TY, TH>(p, st);
 }
 
 }  // namespace
