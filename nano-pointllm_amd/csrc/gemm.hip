@@ -286,8 +286,8 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
     constexpr int EV = 16 / kOutBytes;  // outputs per 16-byte chunk
     constexpr int CPR = BNO / EV;       // chunks per tile row
     constexpr int NT = NW * 64;
-    constexpr int RPP = NT / CPR;       // tile rows per pass
-    static_assert(NT % CPR == 0, "threads cover whole rows");
+    constexpr int RPP = NT / CPR;       // tile rows per pass; threads past RPP * CPR idle
+    static_assert(RPP >= 1, "a pass covers at least one tile row");
     const int64_t n_out_total = kHalfCols ? p.N / 2 : p.N;
     const int64_t n0 = kHalfCols ? static_cast<int64_t>(nb0) * 8 : static_cast<int64_t>(nb0) * 16;
     const bool vec_ok =
@@ -298,7 +298,7 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
       const int nlo = (static_cast<int>(threadIdx.x) % CPR) * EV;
       const int64_t m = static_cast<int64_t>(mb0) * 16 + ml;
       const int64_t n = n0 + nlo;
-      if (ml < BM && m < p.M && n < n_out_total) {
+      if (static_cast<int>(threadIdx.x) < RPP * CPR && ml < BM && m < p.M && n < n_out_total) {
         TY* dst = static_cast<TY*>(p.y) + m * p.ldy + n;
         const TY* src = stile + ml * BNO + nlo;
         if (vec_ok && n + EV <= n_out_total) {
@@ -328,36 +328,43 @@ hipError_t launch_cfg(GemmParams p, hipStream_t st) {
 }
 
 // Tile configurations, chosen by tile count (measured on MI355X, random data,
-// cold weights, LLaMA-7B projections at M = 256..2048):
-//   * 128x256, 8 waves of 64x64, 3-stage ring of one k-block, 2 workgroups
-//     per CU, when there are at least ~0.82 tiles per workgroup slot (2 per
-//     CU): each MFMA moves half as many operand bytes through LDS as with
-//     32x32 per wave.  Just past one full round of slots (1 to 1.25 tiles
-//     per slot) the few tiles of the second round cost more than that saves,
-//     and the 128x128 tile is kept;
-//   * else 128x128, 16 waves of 32x32, 4-stage ring of one k-block, 2 per
-//     CU, when there are more of those tiles than CUs;
-//   * else, when 64x64 tiles fit in two per CU: 64x64, 4 waves of 32x32,
-//     2-stage ring of four k-blocks (256 K), 2 per CU;
-//   * else 128x128 with a 4-stage ring of two k-blocks (128 K), one per CU.
-//     With one round of tiles or less, every k-step's barrier and memory
-//     latency is exposed: stages of several k-blocks cut the barriers, and
-//     the deeper ring keeps more bytes in flight per CU (96 KiB).  With
-//     weights streamed from HBM these are 8-14% faster on O and down at
-//     M = 560..1024, and the 64x64 form 15-20% at M = 384.
+// cold weights, LLaMA-7B projections at M = 256..2048).  A launch is fastest
+// when its tiles fill one round of workgroup slots (2 per CU) as closely as
+// possible, and when several rounds are needed, with the widest tile:
+//   * 128x128 tiles, when they fit in one round: 16 waves of 32x32, a
+//     4-stage ring of one k-block (64 K), 2 workgroups per CU, when there
+//     are more of them than CUs; else (one tile per CU or less, where every
+//     k-step's barrier and memory latency is exposed) ring stages of several
+//     k-blocks cut the barriers and keep more bytes in flight: 64x64 (4 waves
+//     of 32x32, a 2-stage ring of four k-blocks, 2 per CU) when those tiles
+//     fit in one round, else 128x128 with a 4-stage ring of two k-blocks,
+//     one per CU (8-14% faster on O and down at M = 560..1024, 15-20% at
+//     M = 384, with weights streamed from HBM);
+//   * else the widest of 128x192, 128x224 and 128x256 whose tiles still fit
+//     in one round, trying the narrowest first (8 waves of 32x96, 32x112 or
+//     64x64, 3-stage ring): 128x224 takes gate/up at M = 560 in 495 tiles,
+//     8% faster than 430 tiles of 128x256;
+//   * else (several rounds) 128x256, except just past one round of those
+//     (1 to 1.25 tiles per slot), where the few tiles of the second round cost
+//     more than the wider tile saves and 128x128 is kept.
 template <int EPI, typename TY, typename TH>
 hipError_t launch_t(const GemmParams& p, hipStream_t st) {
   const int64_t cus = cu_count();
-  const int64_t wide_tiles = ceil_div(p.MB, 8) * ceil_div(p.NB, 16);
   const int64_t slots = cus * 2;
+  const int64_t tiles_m = ceil_div(p.MB, 8);  // 128-row tiles
+  const int64_t big_tiles = tiles_m * ceil_div(p.NB, 8);
+  if (big_tiles <= slots) {
+    if (big_tiles > cus) return launch_cfg<4, 4, 2, 2, 4, 2, 1, EPI, TY, TH>(p, st);
+    const int64_t small_tiles = ceil_div(p.MB, 4) * ceil_div(p.NB, 4);
+    if (small_tiles <= slots) return launch_cfg<2, 2, 2, 2, 2, 2, 4, EPI, TY, TH>(p, st);
+    return launch_cfg<4, 4, 2, 2, 4, 1, 2, EPI, TY, TH>(p, st);
+  }
+  if (tiles_m * ceil_div(p.NB, 12) <= slots) return launch_cfg<4, 2, 2, 6, 3, 2, 1, EPI, TY, TH>(p, st);
+  if (tiles_m * ceil_div(p.NB, 14) <= slots) return launch_cfg<4, 2, 2, 7, 3, 2, 1, EPI, TY, TH>(p, st);
+  const int64_t wide_tiles = tiles_m * ceil_div(p.NB, 16);
   const bool short_second_round = wide_tiles > slots && wide_tiles * 100 < slots * 125;
-  if (wide_tiles * 100 >= slots * 82 && !short_second_round)
-    return launch_cfg<2, 4, 4, 4, 3, 2, 1, EPI, TY, TH>(p, st);
-  const int64_t big_tiles = ceil_div(p.MB, 8) * ceil_div(p.NB, 8);
-  if (big_tiles > cus) return launch_cfg<4, 4, 2, 2, 4, 2, 1, EPI, TY, TH>(p, st);
-  const int64_t small_tiles = ceil_div(p.MB, 4) * ceil_div(p.NB, 4);
-  if (small_tiles <= slots) return launch_cfg<2, 2, 2, 2, 2, 2, 4, EPI, TY, TH>(p, st);
-  return launch_cfg<4, 4, 2, 2, 4, 1, 2, EPI, TY, TH>(p, st);
+  if (short_second_round) return launch_cfg<4, 4, 2, 2, 4, 2, 1, EPI, TY, TH>(p, st);
+  return launch_cfg<2, 4, 4, 4, 3, 2, 1, EPI, TY, TH>(p, st);
 }
 
 }  // namespace

@@ -20,6 +20,7 @@ import numpy as np
 import pytest
 import torch
 
+from gemm_tiles import gemm_config as _config
 from oracle import w8a8_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -28,18 +29,6 @@ pytestmark = pytest.mark.gpu
 def note(msg: str) -> None:
     sys.__stderr__.write(f"[gpu-case] {msg}\n")
     sys.__stderr__.flush()
-
-
-def _config(m, n, cus=256):
-    """The launch rule on the MI355X's 256 CUs (two workgroup slots each)."""
-    mb, nb = -(-m // 16), -(-n // 16)
-    slots = 2 * cus
-    wide = -(-mb // 8) * -(-nb // 16)
-    if wide * 100 >= slots * 82 and not (wide > slots and wide * 100 < slots * 125):
-        return "wide"
-    if -(-mb // 8) * -(-nb // 8) > cus:
-        return "big"
-    return "small-deep" if -(-mb // 4) * -(-nb // 4) <= slots else "big-deep"
 
 
 def _ulps16(a, b):

@@ -1,5 +1,7 @@
-"""Prefill GEMM shapes with enough 128x256 output tiles to fill the chip twice
-over, which select the wide tile (8 waves of 64x64 blocks, three LDS stages).
+"""Prefill GEMM shapes past one round of 128x128 tiles, which select the
+128-row tiles of 192, 224 or 256 columns (8 waves each, three LDS stages):
+the widest whose tiles still fit in one round of workgroup slots, else (for
+several rounds) 128x256.
 
 Bars as for every GEMM path: int32 accumulators bit-exact against the
 oracle's integer product; binary16 / bfloat16 / binary32 dequant outputs
@@ -18,6 +20,7 @@ import numpy as np
 import pytest
 import torch
 
+from gemm_tiles import gemm_config
 from oracle import w8a8_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -35,14 +38,6 @@ def _ulps16(a, b):
     return np.abs(key(a) - key(b))
 
 
-def _selects_wide(m, n, cus=256):
-    """The launch rule on the MI355X's 256 CUs (two workgroup slots each):
-    at least 0.82 tiles per slot, and not 1 to 1.25."""
-    mb, nb = -(-m // 16), -(-n // 16)
-    r = -(-mb // 8) * -(-nb // 16) / (2 * cus)
-    return r >= 0.82 and not 1 < r < 1.25
-
-
 def _case(m, n, k, seed):
     g = torch.Generator().manual_seed(seed)
     xq = torch.randint(-127, 128, (m, k), generator=g, dtype=torch.int8)
@@ -54,13 +49,14 @@ def _case(m, n, k, seed):
     return xq, wq, sx, sw, bias
 
 
-@pytest.mark.parametrize("m,n,k", [(1000, 14005, 200), (2100, 6200, 320), (1100, 20000, 576)])
-def test_wide_tile_int32_and_dequant(cuda, m, n, k):
+@pytest.mark.parametrize("m,n,k,cfg", [(1000, 14005, 200, "w224"), (2100, 6200, 320, "w224"),
+                                        (1100, 20000, 576, "w256"), (1000, 12000, 330, "w192")])
+def test_wide_tile_int32_and_dequant(cuda, m, n, k, cfg):
     from nanopointllm_amd import w8a8
 
-    assert _selects_wide(m, n)
+    assert gemm_config(m, n) == cfg
     xq, wq, sx, sw, bias = _case(m, n, k, seed=m + n + k)
-    note(f"gemm wide m={m} n={n} k={k}")
+    note(f"gemm {cfg} m={m} n={n} k={k}")
     xd, wp = xq.to(cuda), w8a8.pack_rows(wq.to(cuda))
     eacc = O.int32_matmul_f64(xq.numpy(), wq.numpy())
     np.testing.assert_array_equal(w8a8.gemm_i32(xd, wp, n).cpu().numpy(), eacc)
@@ -77,13 +73,14 @@ def test_wide_tile_int32_and_dequant(cuda, m, n, k):
             np.testing.assert_array_equal(got, want, err_msg=f"{dt} bias={b is not None}")
 
 
-def test_wide_tile_silu_mul_and_int8_chain(cuda):
+@pytest.mark.parametrize("m,inter,k,cfg", [(1000, 7002, 320, "w224"), (1100, 10000, 200, "w256"),
+                                            (1000, 6000, 330, "w192")])
+def test_wide_tile_silu_mul_and_int8_chain(cuda, m, inter, k, cfg):
     from nanopointllm_amd import _lib, w8a8
 
-    m, inter, k = 1000, 7002, 320
-    assert _selects_wide(m, 2 * inter)
-    xq, wq, sx, sw, _ = _case(m, 2 * inter, k, seed=11)
-    note(f"gemm wide silu m={m} inter={inter} k={k}")
+    assert gemm_config(m, 2 * inter) == cfg
+    xq, wq, sx, sw, _ = _case(m, 2 * inter, k, seed=11 + k)
+    note(f"gemm {cfg} silu m={m} inter={inter} k={k}")
     wp = w8a8.pack_rows(wq.to(cuda), _lib.ROWS_INTERLEAVE_HALVES)
     sp = O.pack_gateup_rows(sw[:inter, None], sw[inter:, None], "interleave")[:, 0]
     qp = O.pack_gateup_rows(wq.numpy()[:inter], wq.numpy()[inter:], "interleave")
@@ -102,19 +99,20 @@ def test_wide_tile_silu_mul_and_int8_chain(cuda):
     np.testing.assert_array_equal(hq.cpu().numpy(), eq)
 
 
-def test_requant1_epilogue_at_a_wide_shape(cuda):
-    """The integer requant epilogue on the wide tile: equal to
+@pytest.mark.parametrize("m,n,k,cfg", [(1000, 14005, 200, "w224"), (1100, 20000, 200, "w256")])
+def test_requant1_epilogue_at_a_wide_shape(cuda, m, n, k, cfg):
+    """The integer requant epilogue on the wide tiles: equal to
     requantize_int32 of the exact product (that kernel is pinned to the
     oracle elsewhere), and a random sample of entries against the oracle."""
     from nanopointllm_amd import integer_epilogues as E, w8a8
 
-    m, n, k = 1000, 14005, 200
+    assert gemm_config(m, n) == cfg
     xq, wq, _, sw, _ = _case(m, n, k, seed=5)
     comp = [O.compile_fp16_requant_scale(0.02, float(w), 0.5) for w in sw]
     mult = np.array([c[0] for c in comp], np.uint32)
     shift = np.array([c[1] for c in comp], np.int32)
     bias = np.random.default_rng(5).integers(-3000, 3000, n).astype(np.int32)
-    note(f"gemm wide requant1 m={m} n={n} k={k}")
+    note(f"gemm {cfg} requant1 m={m} n={n} k={k}")
     multt = torch.from_numpy(mult.view(np.int32)).to(cuda)
     shiftt, biast = torch.from_numpy(shift).to(cuda), torch.from_numpy(bias).to(cuda)
     xd, wp = xq.to(cuda), w8a8.pack_rows(wq.to(cuda))
