@@ -339,7 +339,10 @@ hipError_t launch_cfg(GemmParams p, hipStream_t st) {
 //     of 32x32, a 2-stage ring of four k-blocks, 2 per CU) when those tiles
 //     fit in one round, else 128x128 with a 4-stage ring of two k-blocks,
 //     one per CU (8-14% faster on O and down at M = 560..1024, 15-20% at
-//     M = 384, with weights streamed from HBM);
+//     M = 384, with weights streamed from HBM).  With at most one 64x64 tile
+//     per CU, 32x32 tiles of one wave (a 3-stage ring of four k-blocks, 3 per
+//     CU by LDS) spread the work over more CUs when they fit in one round:
+//     9-13% faster on QKV at M = 64 and on O and down at M = 128;
 //   * else the widest of 128x192, 128x224 and 128x256 whose tiles still fit
 //     in one round, trying the narrowest first (8 waves of 32x96, 32x112 or
 //     64x64, 3-stage ring): 128x224 takes gate/up at M = 560 in 495 tiles,
@@ -356,6 +359,8 @@ hipError_t launch_t(const GemmParams& p, hipStream_t st) {
   if (big_tiles <= slots) {
     if (big_tiles > cus) return launch_cfg<4, 4, 2, 2, 4, 2, 1, EPI, TY, TH>(p, st);
     const int64_t small_tiles = ceil_div(p.MB, 4) * ceil_div(p.NB, 4);
+    if (small_tiles <= cus && ceil_div(p.MB, 2) * ceil_div(p.NB, 2) <= 3 * cus)
+      return launch_cfg<1, 1, 2, 2, 3, 4, 4, EPI, TY, TH>(p, st);
     if (small_tiles <= slots) return launch_cfg<2, 2, 2, 2, 2, 2, 4, EPI, TY, TH>(p, st);
     return launch_cfg<4, 4, 2, 2, 4, 1, 2, EPI, TY, TH>(p, st);
   }

@@ -15,7 +15,10 @@ def gemm_config(m: int, n: int, cus: int = 256) -> str:
     if big <= slots:
         if big > cus:
             return "big"
-        return "small-deep" if _cdiv(mb, 4) * _cdiv(nb, 4) <= slots else "big-deep"
+        small = _cdiv(mb, 4) * _cdiv(nb, 4)
+        if small <= cus and _cdiv(mb, 2) * _cdiv(nb, 2) <= 3 * cus:
+            return "tiny-deep"
+        return "small-deep" if small <= slots else "big-deep"
     if tiles_m * _cdiv(nb, 12) <= slots:
         return "w192"
     if tiles_m * _cdiv(nb, 14) <= slots:

@@ -1,7 +1,8 @@
 """Prefill GEMM shapes with at most one round of tiles, which select ring
-stages of several k-blocks: the 64x64 tile with stages of four k-blocks
-(256 K) when its tiles fit in two per CU, else the 128x128 tile with stages of
-two k-blocks (128 K) and one workgroup per CU.
+stages of several k-blocks: one-wave 32x32 tiles with stages of four k-blocks
+(256 K) when there is at most one 64x64 tile per CU, else the 64x64 tile with
+stages of four k-blocks when its tiles fit in two per CU, else the 128x128
+tile with stages of two k-blocks (128 K) and one workgroup per CU.
 
 Bars as for every GEMM path: int32 accumulators bit-exact against the
 oracle's integer product; binary16 / bfloat16 dequant outputs bit-equal to the
@@ -51,15 +52,17 @@ def _case(m, n, k, seed):
 
 # (m, n, k, config).  K-blocks of 64: 4197 -> 66, 1000 -> 16, 70 -> 2,
 # 3100 -> 49 (a last 128-K stage of one k-block), 4250 -> 67 (a last 256-K
-# stage of three), 11008 -> 172, and 70 on the 64x64 tile (one stage of two).
+# stage of three), 11008 -> 172, and 70 (one 256-K stage of two).
 SHAPES = [
     (560, 4000, 4197, "big-deep"),
     (1000, 4096, 1000, "big-deep"),
     (700, 4100, 70, "big-deep"),
     (130, 12288, 3100, "big-deep"),
-    (100, 1000, 4250, "small-deep"),
     (300, 6000, 11008, "small-deep"),
-    (65, 8000, 70, "small-deep"),
+    (300, 6000, 4250, "small-deep"),
+    (100, 1000, 4250, "tiny-deep"),
+    (65, 8000, 70, "tiny-deep"),
+    (128, 4096, 11008, "tiny-deep"),
 ]
 
 
@@ -83,12 +86,12 @@ def test_deep_stage_int32_and_dequant(cuda, m, n, k, cfg):
                                           err_msg=f"{dt} bias={b is not None}")
 
 
-@pytest.mark.parametrize("m,inter,k", [(560, 2000, 4197), (100, 500, 4250)])
+@pytest.mark.parametrize("m,inter,k", [(560, 2000, 4197), (300, 3000, 4250), (100, 500, 4250)])
 def test_deep_stage_silu_mul_and_int8_chain(cuda, m, inter, k):
     from nanopointllm_amd import _lib, w8a8
 
     cfg = _config(m, 2 * inter)
-    assert cfg in ("big-deep", "small-deep")
+    assert cfg in ("big-deep", "small-deep", "tiny-deep")
     xq, wq, sx, sw, _ = _case(m, 2 * inter, k, seed=7 + k)
     note(f"gemm {cfg} silu m={m} inter={inter} k={k}")
     wp = w8a8.pack_rows(wq.to(cuda), _lib.ROWS_INTERLEAVE_HALVES)
@@ -109,11 +112,11 @@ def test_deep_stage_silu_mul_and_int8_chain(cuda, m, inter, k):
     np.testing.assert_array_equal(hq.cpu().numpy(), eq)
 
 
-@pytest.mark.parametrize("m,n,k", [(560, 4000, 4197), (100, 1000, 4250)])
+@pytest.mark.parametrize("m,n,k", [(560, 4000, 4197), (300, 6000, 4250), (100, 1000, 4250)])
 def test_deep_stage_requant1_epilogue(cuda, m, n, k):
     from nanopointllm_amd import integer_epilogues as E, w8a8
 
-    assert _config(m, n) in ("big-deep", "small-deep")
+    assert _config(m, n) in ("big-deep", "small-deep", "tiny-deep")
     xq, wq, _, sw, _ = _case(m, n, k, seed=5 + k)
     comp = [O.compile_fp16_requant_scale(0.02, float(w), 0.5) for w in sw]
     mult = np.array([c[0] for c in comp], np.uint32)
