@@ -160,7 +160,8 @@ int w8a8_gemm_i32(const int8_t* xq, int64_t ldq, const int8_t* w_packed, int32_t
  *   [m], receives s_x.
  * Decode inputs (F16/BF16 x, 1 <= m <= 8 with k <= 12288 or m <= 16 with
  * k <= 6144, k % 8 == 0, 16-byte aligned, and per CU at least 64 KiB of
- * weights and 4 weight bytes per activation element) run as one kernel with
+ * weights and 4 weight bytes per activation element, 2 when m > 8) run as
+ * one kernel with
  * the quantization fused in and need no workspace (it may be null); every
  * other case needs w8a8_workspace_bytes(m, k) bytes.
  */

@@ -493,7 +493,9 @@ int cu_count() {
 // gemv_kernel when a CU streams at least 64 KiB of weights and at least 4
 // bytes per activation element it quantizes (LLaMA-7B at M = 8: packed QKV
 // and gate/up fused, O and down not, down 25% slower fused; at M <= 4 all four
-// fused, O 4-7% faster than quantize + GEMV, down within 1%).
+// fused, O 4-7% faster than quantize + GEMV, down within 1%).  With 9-16 rows
+// the quantize + GEMV route pays more per row, and 2 bytes per element
+// suffice (packed QKV at M = 13-16: 12-17% faster fused).
 bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
                           int64_t K) {
   if (!((x_dtype == kF16 || x_dtype == kBF16) && M >= 1 && M <= kFusedMaxRows16 && K >= 8 &&
@@ -505,8 +507,9 @@ bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, in
   const int64_t g = nb < cu_count() ? nb : cu_count();
   const int64_t blocks_per_cu = ceil_div(nb, g);
   const int64_t weight_bytes_per_cu = blocks_per_cu * kTileRows * ceil_div(K, kTileK) * kTileK;
+  const int64_t bytes_per_elem = M <= kFusedMaxRows ? 4 : 2;
   return blocks_per_cu <= kFusedMaxBlocks && weight_bytes_per_cu >= (64 << 10) &&
-         weight_bytes_per_cu >= 4 * M * K;
+         weight_bytes_per_cu >= bytes_per_elem * M * K;
 }
 
 hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const LinearOperands& op,

@@ -338,7 +338,8 @@ def test_fused_decode_path(cuda, m, n, k):
 
 
 @pytest.mark.parametrize("m", [9, 12, 13, 16])
-@pytest.mark.parametrize("n,k", [(32768, 1000), (131072, 256), (24576, 4096), (20480, 6144)])
+@pytest.mark.parametrize("n,k", [(32768, 1000), (131072, 256), (24576, 4096), (20480, 6144),
+                                 (12288, 4096)])
 def test_fused_decode_16_rows(cuda, m, n, k):
     """9 to 16 rows on the workspace-free kernel (full 16-row A fragments,
     K <= 6144): outputs, row scales and int32 accumulators against the
@@ -460,15 +461,15 @@ def test_fused_decode_exact_ties(cuda, m):
 
 
 def test_fused_path_not_taken_for_small_shapes(cuda):
-    """O-sized projections at M = 8 and tiny ones go through quantization +
-    GEMV (they need a workspace) and give the same results."""
+    """O-sized projections at M = 8 and 12 and tiny ones go through
+    quantization + GEMV (they need a workspace) and give the same results."""
     from nanopointllm_amd import _lib, w8a8
 
-    for n, k in [(4096, 4096), (40, 64), (16, 8)]:
+    for m, n, k in [(8, 4096, 4096), (12, 4096, 4096), (8, 40, 64), (8, 16, 8)]:
         _, qw, sw = weight_q(n, k, seed=n + k)
         wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
-        x = torch.randn(8, k, generator=torch.Generator().manual_seed(k)).to(torch.float16)
-        note(f"unfused decode n={n} k={k}")
+        x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.float16)
+        note(f"unfused decode m={m} n={n} k={k}")
         rc, _, _ = _linear_without_workspace(x.to(cuda), wp, torch.from_numpy(sw).to(cuda), None,
                                              n, _lib.EPI_DEQUANT, torch.float16)
         assert rc == _lib.ERR_WORKSPACE
