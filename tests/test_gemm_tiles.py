@@ -1,0 +1,38 @@
+"""The GEMM tile rule (restated in gemm_tiles.py) on the LLaMA-7B prefill
+shapes that the measurements in the design notes quote: which configuration
+each shape takes on the MI355X's 256 CUs.  The GPU tests run every
+configuration for exactness; this pins the shape-to-configuration map."""
+from __future__ import annotations
+
+import pytest
+
+from gemm_tiles import gemm_config
+
+QKV, O, GATEUP, DOWN = 12288, 4096, 22016, 4096
+
+
+@pytest.mark.parametrize("m,n,cfg", [
+    (560, QKV, "big"), (768, QKV, "w192"), (1024, QKV, "w192"), (2048, QKV, "w256"),
+    (560, O, "big-deep"), (768, O, "big-deep"), (1024, O, "big-deep"),
+    (560, GATEUP, "w224"), (768, GATEUP, "big"), (1024, GATEUP, "w256"),
+    (64, QKV, "tiny-deep"), (128, O, "tiny-deep"), (256, O, "small-deep"),
+    (256, QKV, "big-deep"), (384, GATEUP, "w192"), (8192, 8192, "w256"),
+])
+def test_llama7b_prefill_tiles(m, n, cfg):
+    assert gemm_config(m, n) == cfg
+
+
+def test_every_config_fits_one_round_or_is_the_widest():
+    """Within one round of 512 workgroup slots the rule never leaves a config
+    that would also fit with more tiles; past it, only 128x256 or 128x128."""
+    for m in range(65, 4097, 37):
+        for n in (4096, 11008, 12288, 22016, 32000):
+            cfg = gemm_config(m, n)
+            mb, nb = -(-m // 16), -(-n // 16)
+            tm = -(-mb // 8)
+            tiles = {"w192": tm * -(-nb // 12), "w224": tm * -(-nb // 14),
+                     "w256": tm * -(-nb // 16), "big": tm * -(-nb // 8)}
+            if cfg in ("w192", "w224"):
+                assert tiles[cfg] <= 512 and tiles["big"] > 512
+            if cfg == "w224":
+                assert tiles["w192"] > 512
