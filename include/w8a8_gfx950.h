@@ -31,7 +31,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 2
+#define W8A8_ABI_VERSION 3
 
 typedef enum w8a8_dtype {
   W8A8_F32 = 0,
@@ -99,6 +99,16 @@ int64_t w8a8_packed_bytes(int64_t rows, int64_t k);
 /* Workspace bytes needed by w8a8_linear / w8a8_linear_i8in / w8a8_gemm_i32
  * for an [m, k] activation. */
 int64_t w8a8_workspace_bytes(int64_t m, int64_t k);
+
+/* GEMM workgroup tile that w8a8_gemm_i32 / w8a8_linear / w8a8_linear_i8in
+ * launch for an m x n product in the GEMM regime, on a device with `cus`
+ * compute units: 0 = 32x32 (one wave, ring stages of four k-blocks), 1 =
+ * 64x64 (stages of four k-blocks), 2 = 128x128 (one workgroup per CU, stages
+ * of two k-blocks), 3 = 128x128, 4 = 128x192, 5 = 128x224, 6 = 128x256; -1
+ * for a negative or zero size.  A pure function of its arguments (no device
+ * call): it lets tests name the configuration a shape exercises.  No
+ * counterpart in the reference, whose products are dense F.linear calls. */
+int w8a8_gemm_tile_config(int64_t m, int64_t n, int64_t cus);
 
 /*
  * Per-row symmetric int8 quantization with a dynamic scale per row:

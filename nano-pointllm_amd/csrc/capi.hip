@@ -16,8 +16,9 @@ thread_local int g_last_hip_error = 0;
 constexpr int64_t kMaxK = ((int64_t{1} << 31) - 1) / (127 * 127);
 
 // Row and column counts are carried as int in the kernels' parameters and
-// launch one workgroup per row in the quantizers.
-constexpr int64_t kMaxRows = INT32_MAX;
+// launch one workgroup per row in the quantizers; the margin keeps a count
+// rounded up to whole 256-row tiles inside int as well.
+constexpr int64_t kMaxRows = INT32_MAX - 256;
 
 inline int status_of(hipError_t e) {
   if (e == hipSuccess) return W8A8_OK;
@@ -196,6 +197,11 @@ int64_t w8a8_workspace_bytes(int64_t m, int64_t k) {
   return scale_region(m) + act_region(m, k);
 }
 
+int w8a8_gemm_tile_config(int64_t m, int64_t n, int64_t cus) {
+  if (m <= 0 || n <= 0 || cus <= 0 || m > kMaxRows || n > kMaxRows) return -1;
+  return gemm_tile_choice(ceil_div(m, kTileRows), ceil_div(n, kTileRows), cus);
+}
+
 int w8a8_quant_rows(const void* x, int x_dtype, int64_t rows, int64_t k, int64_t ldx,
                     int8_t* q, int64_t ldq, float* scales, hipStream_t stream) {
   if (rows < 0 || k < 0 || rows > kMaxRows) return W8A8_ERR_SHAPE;
@@ -327,7 +333,7 @@ int w8a8_prologue_quant(const void* x, int x_dtype, int64_t ldx, const void* res
   if (!half_dtype(x_dtype)) return W8A8_ERR_DTYPE;
   const bool w32 = norm_weight != nullptr && norm_weight_dtype == kF32;
   if (norm_weight != nullptr && norm_weight_dtype != x_dtype && !w32) return W8A8_ERR_DTYPE;
-  if (m < 0 || k < 0 || k > prologue_max_k() || m > INT32_MAX) return W8A8_ERR_SHAPE;
+  if (m < 0 || k < 0 || k > prologue_max_k() || m > kMaxRows) return W8A8_ERR_SHAPE;
   if (m == 0 || k == 0) return W8A8_OK;
   if (x == nullptr || q == nullptr) return W8A8_ERR_NULL;
   if (residual != nullptr && residual_out == nullptr) return W8A8_ERR_NULL;

@@ -237,7 +237,7 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
         bool vok[2];
 #pragma unroll
         for (int e = 0; e < 2; ++e) {
-          const int m = mb0 * 16 + ml0 + e;
+          const int64_t m = static_cast<int64_t>(mb0) * 16 + ml0 + e;
           const bool m_ok = m < p.M;
           vok[e] = m_ok && n_ok;
           const float sxm = m_ok ? p.sx[m] : 0.0f;
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int ml = 16 * (wm * BR + i) + 4 * (lane >> 4) + r;
-        const int m = mb0 * 16 + ml;
+        const int64_t m = static_cast<int64_t>(mb0) * 16 + ml;
         const bool m_ok = m < p.M;
         const bool ok = m_ok && n_ok;
         const int32_t a = acc[i][j][r];
@@ -317,11 +317,13 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
 template <int WM, int WN, int BR, int BC, int STG, int OCC, int KT, int EPI, typename TY,
           typename TH>
 hipError_t launch_cfg(GemmParams p, hipStream_t st) {
-  p.tiles_m = static_cast<int>(ceil_div(p.MB, WM * BR));
-  const int tiles_n = static_cast<int>(ceil_div(p.NB, WN * BC));
-  p.tiles = p.tiles_m * tiles_n;
-  p.per_xcd = static_cast<int>(ceil_div(p.tiles, kXcds));
-  if (p.tiles == 0) return hipSuccess;
+  const int64_t tiles_m = ceil_div(p.MB, WM * BR);
+  const int64_t tiles = tiles_m * ceil_div(p.NB, WN * BC);
+  if (tiles == 0) return hipSuccess;
+  if (ceil_div(tiles, kXcds) * kXcds > INT32_MAX) return hipErrorInvalidConfiguration;
+  p.tiles_m = static_cast<int>(tiles_m);
+  p.tiles = static_cast<int>(tiles);
+  p.per_xcd = static_cast<int>(ceil_div(tiles, kXcds));
   hipLaunchKernelGGL((gemm_kernel<WM, WN, BR, BC, STG, OCC, KT, EPI, TY, TH>),
                      dim3(p.per_xcd * kXcds), dim3(WM * WN * 64), 0, st, p);
   return hipGetLastError();
@@ -352,27 +354,43 @@ hipError_t launch_cfg(GemmParams p, hipStream_t st) {
 //     more than the wider tile saves and 128x128 is kept.
 template <int EPI, typename TY, typename TH>
 hipError_t launch_t(const GemmParams& p, hipStream_t st) {
-  const int64_t cus = cu_count();
-  const int64_t slots = cus * 2;
-  const int64_t tiles_m = ceil_div(p.MB, 8);  // 128-row tiles
-  const int64_t big_tiles = tiles_m * ceil_div(p.NB, 8);
-  if (big_tiles <= slots) {
-    if (big_tiles > cus) return launch_cfg<4, 4, 2, 2, 4, 2, 1, EPI, TY, TH>(p, st);
-    const int64_t small_tiles = ceil_div(p.MB, 4) * ceil_div(p.NB, 4);
-    if (small_tiles <= cus && ceil_div(p.MB, 2) * ceil_div(p.NB, 2) <= 3 * cus)
+  switch (gemm_tile_choice(p.MB, p.NB, cu_count())) {
+    case kGemmTinyDeep:
       return launch_cfg<1, 1, 2, 2, 3, 4, 4, EPI, TY, TH>(p, st);
-    if (small_tiles <= slots) return launch_cfg<2, 2, 2, 2, 2, 2, 4, EPI, TY, TH>(p, st);
-    return launch_cfg<4, 4, 2, 2, 4, 1, 2, EPI, TY, TH>(p, st);
+    case kGemmSmallDeep:
+      return launch_cfg<2, 2, 2, 2, 2, 2, 4, EPI, TY, TH>(p, st);
+    case kGemmBigDeep:
+      return launch_cfg<4, 4, 2, 2, 4, 1, 2, EPI, TY, TH>(p, st);
+    case kGemmBig:
+      return launch_cfg<4, 4, 2, 2, 4, 2, 1, EPI, TY, TH>(p, st);
+    case kGemmW192:
+      return launch_cfg<4, 2, 2, 6, 3, 2, 1, EPI, TY, TH>(p, st);
+    case kGemmW224:
+      return launch_cfg<4, 2, 2, 7, 3, 2, 1, EPI, TY, TH>(p, st);
+    default:
+      return launch_cfg<2, 4, 4, 4, 3, 2, 1, EPI, TY, TH>(p, st);
   }
-  if (tiles_m * ceil_div(p.NB, 12) <= slots) return launch_cfg<4, 2, 2, 6, 3, 2, 1, EPI, TY, TH>(p, st);
-  if (tiles_m * ceil_div(p.NB, 14) <= slots) return launch_cfg<4, 2, 2, 7, 3, 2, 1, EPI, TY, TH>(p, st);
-  const int64_t wide_tiles = tiles_m * ceil_div(p.NB, 16);
-  const bool short_second_round = wide_tiles > slots && wide_tiles * 100 < slots * 125;
-  if (short_second_round) return launch_cfg<4, 4, 2, 2, 4, 2, 1, EPI, TY, TH>(p, st);
-  return launch_cfg<2, 4, 4, 4, 3, 2, 1, EPI, TY, TH>(p, st);
 }
 
 }  // namespace
+
+int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus) {
+  const int64_t slots = cus * 2;
+  const int64_t tiles_m = ceil_div(MB, 8);  // 128-row tiles
+  const int64_t big_tiles = tiles_m * ceil_div(NB, 8);
+  if (big_tiles <= slots) {
+    if (big_tiles > cus) return kGemmBig;
+    const int64_t small_tiles = ceil_div(MB, 4) * ceil_div(NB, 4);
+    if (small_tiles <= cus && ceil_div(MB, 2) * ceil_div(NB, 2) <= 3 * cus) return kGemmTinyDeep;
+    if (small_tiles <= slots) return kGemmSmallDeep;
+    return kGemmBigDeep;
+  }
+  if (tiles_m * ceil_div(NB, 12) <= slots) return kGemmW192;
+  if (tiles_m * ceil_div(NB, 14) <= slots) return kGemmW224;
+  const int64_t wide_tiles = tiles_m * ceil_div(NB, 16);
+  const bool short_second_round = wide_tiles > slots && wide_tiles * 100 < slots * 125;
+  return short_second_round ? kGemmBig : kGemmW256;
+}
 
 hipError_t launch_gemm(const LinearOperands& op, hipStream_t st) {
   GemmParams p;

@@ -80,6 +80,19 @@ hipError_t launch_pack_rows(const int8_t* src, int64_t rows, int64_t K, int64_t 
 hipError_t launch_pad_rows(const int8_t* src, int64_t rows, int64_t K, int64_t ld, int8_t* dst,
                            int64_t ldd, hipStream_t st);
 
+// GEMM workgroup tiles (gemm.hip), as chosen by gemm_tile_choice for MB x NB
+// 16-row blocks on `cus` compute units with two workgroup slots each.
+enum GemmTile : int {
+  kGemmTinyDeep = 0,   // 32x32, 1 wave, 3-stage ring of four k-blocks
+  kGemmSmallDeep = 1,  // 64x64, 4 waves, 2-stage ring of four k-blocks
+  kGemmBigDeep = 2,    // 128x128, 16 waves, 4-stage ring of two k-blocks, 1 per CU
+  kGemmBig = 3,        // 128x128, 16 waves, 4-stage ring of one k-block
+  kGemmW192 = 4,       // 128x192, 8 waves
+  kGemmW224 = 5,       // 128x224, 8 waves
+  kGemmW256 = 6,       // 128x256, 8 waves
+};
+int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus);
+
 // M <= 64 (the GEMV regime).
 hipError_t launch_gemv(const LinearOperands& op, hipStream_t st);
 // Any M; activations packed.

@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libw8a8_gfx950.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 F32, F16, BF16, I32, I8 = 0, 1, 2, 3, 4
 EPI_I32, EPI_DEQUANT, EPI_SILU_MUL, EPI_SILU_MUL_Q8 = 0, 1, 2, 3
@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "w8a8_last_hip_error",
     "w8a8_packed_bytes",
     "w8a8_workspace_bytes",
+    "w8a8_gemm_tile_config",
     "w8a8_quant_rows",
     "w8a8_quant_rows_scaled",
     "w8a8_pack_rows",
@@ -63,6 +64,7 @@ _SIGNATURES = {
     "w8a8_last_hip_error": (_int, []),
     "w8a8_packed_bytes": (_i64, [_i64, _i64]),
     "w8a8_workspace_bytes": (_i64, [_i64, _i64]),
+    "w8a8_gemm_tile_config": (_int, [_i64, _i64, _i64]),
     "w8a8_quant_rows": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp, _vp]),
     "w8a8_quant_rows_scaled": (_int, [_vp, _int, _i64, _i64, _i64, _vp, _i64, _vp, _i64, _vp]),
     "w8a8_pack_rows": (_int, [_vp, _i64, _i64, _i64, _int, _vp, _vp]),

@@ -31,59 +31,97 @@ import torch.nn as nn
 
 from . import w8a8 as _w
 
-_CONV = (nn.Conv1d, nn.Conv2d)
+# Modules whose inputs carry their channels on dimension 1 (N, C, ...); every
+# other module reads its channels from the last dimension.
+_CHANNEL_FIRST = (nn.Conv1d, nn.Conv2d)
+
+
+def _channel_dim(module: nn.Module) -> int:
+    return 1 if isinstance(module, _CHANNEL_FIRST) else -1
+
+
+def _channel_rows(values: torch.Tensor, dim: int) -> torch.Tensor:
+    """``values`` as a 2-D [samples, channels] view, channels from ``dim``."""
+    return values.movedim(dim, -1).reshape(-1, values.shape[dim])
 
 
 class ActivationAbsmaxCollector(AbstractContextManager):
     """Collect tensor and input-channel ranges without changing model outputs
-    (w8a8.py:265-314)."""
+    (w8a8.py:265-314; same attributes and ``static_scales()``).
+
+    The running maxima stay on the inputs' device and each hook updates them
+    in place, so a calibration forward never waits for the host.  The tensor
+    maximum is the maximum of the channel maxima, so one running vector per
+    module is kept (a running scalar for 0-d inputs); ``tensor_absmax`` and
+    ``channel_absmax`` copy them to the host when they are read.
+    """
 
     def __init__(self, modules: dict[str, nn.Module]) -> None:
         self.modules = modules
-        self.tensor_absmax: dict[str, float] = defaultdict(float)
-        self.channel_absmax: dict[str, torch.Tensor] = {}
         self.samples: dict[str, int] = defaultdict(int)
+        self._channel_peaks: dict[str, torch.Tensor] = {}  # f32 [channels]
+        self._scalar_peaks: dict[str, torch.Tensor] = {}   # f32 [], 0-d inputs
         self._handles = []
-        self._device = torch.device("cuda")
 
     def __enter__(self) -> "ActivationAbsmaxCollector":
-        for name, module in self.modules.items():
-            self._handles.append(module.register_forward_pre_hook(self._hook(name)))
+        self._handles = [module.register_forward_pre_hook(self._observer(name, module))
+                         for name, module in self.modules.items()]
         return self
 
     def __exit__(self, exc_type, exc_value, traceback) -> None:
-        for handle in self._handles:
-            handle.remove()
-        self._handles.clear()
+        while self._handles:
+            self._handles.pop().remove()
 
-    def _hook(self, name: str):
-        def collect(module, inputs) -> None:
+    def _observer(self, name: str, module: nn.Module):
+        dim = _channel_dim(module)
+
+        def observe(_module, inputs) -> None:
             if not inputs or not isinstance(inputs[0], torch.Tensor):
                 raise TypeError(f"{name} does not have a tensor first input")
-            values = inputs[0].detach().float()
-            self._device = values.device
-            self.tensor_absmax[name] = max(self.tensor_absmax[name],
-                                           float(values.abs().max().item()))
-            if values.dim() >= 1:
-                if isinstance(module, _CONV):
-                    dims = tuple(i for i in range(values.dim()) if i != 1)
-                    flat = values.abs().amax(dim=dims).cpu()
-                    channels = values.shape[1]
-                else:
-                    flat = values.reshape(-1, values.shape[-1]).abs().amax(dim=0).cpu()
-                    channels = values.shape[-1]
-                previous = self.channel_absmax.get(name)
-                self.channel_absmax[name] = flat if previous is None else torch.maximum(previous,
-                                                                                        flat)
-                self.samples[name] += values.numel() // channels
-        return collect
+            values = inputs[0].detach()
+            if values.dim() == 0:
+                store, peak = self._scalar_peaks, values.abs().float()
+            else:
+                store = self._channel_peaks
+                peak = _channel_rows(values, dim).abs().amax(dim=0).float()
+                self.samples[name] += values.numel() // values.shape[dim]
+            held = store.get(name)
+            if held is None:
+                store[name] = peak
+            else:
+                torch.maximum(held, peak, out=held)
+        return observe
+
+    def _module_peaks(self) -> dict[str, torch.Tensor]:
+        """One 0-d device tensor per observed module: its tensor-wide absmax."""
+        peaks: dict[str, torch.Tensor] = {}
+        for store in (self._channel_peaks, self._scalar_peaks):
+            for name, held in store.items():
+                top = held.amax()
+                peaks[name] = top if name not in peaks else torch.maximum(peaks[name], top)
+        return peaks
+
+    @property
+    def tensor_absmax(self) -> dict[str, float]:
+        peaks = self._module_peaks()
+        if not peaks:
+            return defaultdict(float)
+        host = torch.stack(list(peaks.values())).cpu().tolist()
+        return defaultdict(float, zip(peaks, host))
+
+    @property
+    def channel_absmax(self) -> dict[str, torch.Tensor]:
+        return {name: held.cpu() for name, held in self._channel_peaks.items()}
 
     def static_scales(self) -> dict[str, torch.Tensor]:
-        missing = sorted(set(self.modules) - set(self.tensor_absmax))
+        peaks = self._module_peaks()
+        missing = sorted(set(self.modules) - set(peaks))
         if missing:
             raise RuntimeError(f"no activation calibration for modules: {missing[:3]}")
-        return {name: _w.static_activation_scale(absmax, device=self._device).cpu()
-                for name, absmax in self.tensor_absmax.items()}
+        # Every module's static scale (scale_from_absmax, w8a8.py:46-50,
+        # 94-98) in one device computation and one copy to the host.
+        scales = _w.scale_from_absmax(torch.stack(list(peaks.values()))).cpu()
+        return {name: scales[i] for i, name in enumerate(peaks)}
 
 
 class SequentialActivationQDQ(AbstractContextManager):
@@ -108,78 +146,97 @@ class SequentialActivationQDQ(AbstractContextManager):
         self._handles = []
 
     def __enter__(self) -> "SequentialActivationQDQ":
-        for name, module in self.modules.items():
-            self._handles.append(module.register_forward_pre_hook(self._hook(name)))
+        self._handles = [module.register_forward_pre_hook(self._hook(name))
+                         for name, module in self.modules.items()]
         return self
 
     def __exit__(self, exc_type, exc_value, traceback) -> None:
-        for handle in self._handles:
-            handle.remove()
-        self._handles.clear()
+        while self._handles:
+            self._handles.pop().remove()
 
     def _hook(self, name: str):
         def quantize(module, inputs):
-            values = inputs[0]
             smoothing = self.input_smoothing_scales.get(name)
-            static = self.static_scales.get(name) if self.mode == "static" else None
-            conv = isinstance(module, _CONV)
-            if not conv and values.dtype in (torch.float16, torch.bfloat16):
-                replacement = _fused_qdq(values, smoothing, static)
-            else:
-                if smoothing is not None:
-                    sm = smoothing.to(device=values.device, dtype=values.dtype)
-                    if conv:
-                        shape = [1] * values.dim()
-                        shape[1] = sm.numel()
-                        sm = sm.reshape(shape)
-                    values = values / sm
-                if static is not None:
-                    replacement = _w.static_activation_qdq(values, static.to(values.device))
-                else:
-                    replacement, _ = _w.dynamic_per_token_activation_qdq(
-                        values, axis=1 if conv else -1)
-            return (replacement, *inputs[1:])
+            # Static mode needs a calibrated scale for every module (a missing
+            # one raises KeyError, as the reference's lookup does).
+            static = self.static_scales[name] if self.mode == "static" else None
+            return (_qdq_input(inputs[0], _channel_dim(module), smoothing, static), *inputs[1:])
         return quantize
 
 
-def _fused_qdq(values: torch.Tensor, smoothing: torch.Tensor | None,
+def _qdq_input(values: torch.Tensor, dim: int, smoothing: torch.Tensor | None,
                static: torch.Tensor | None) -> torch.Tensor:
+    """``values / smoothing`` then static or per-token QDQ along channel ``dim``.
+
+    16-bit rows with channels last take the fused prologue kernel (divide and
+    quantization in one pass); other inputs divide in torch and quantize with
+    the GPU quantizers of the same contract."""
     if smoothing is not None:
         smoothing = smoothing.to(device=values.device)   # calibration keeps it on the CPU
-    out = _w.prologue_quant(values, smooth=smoothing,
-                            static_scale=None if static is None else float(static))
-    s = out.scale if static is not None else out.scale.unsqueeze(-1)
-    return (out.q.float() * s).to(values.dtype)
+    if dim == -1 and values.dtype in (torch.float16, torch.bfloat16):
+        out = _w.prologue_quant(values, smooth=smoothing,
+                                static_scale=None if static is None else float(static))
+        scale = out.scale if static is not None else out.scale.unsqueeze(-1)
+        return (out.q.float() * scale).to(values.dtype)
+    if smoothing is not None:
+        shape = [1] * values.dim()
+        shape[dim] = smoothing.numel()
+        values = values / smoothing.to(values.dtype).reshape(shape)
+    if static is not None:
+        return _w.static_activation_qdq(values, static.to(values.device))
+    return _w.dynamic_per_token_activation_qdq(values, axis=dim)[0]
+
+
+def _weight_qdq(granularity: str, group_size: int):
+    if granularity == "per_output":
+        return _w.per_output_weight_qdq
+    if granularity == "group":
+        return lambda weight: _w.groupwise_weight_qdq(weight, group_size=group_size)
+    raise ValueError("weight granularity must be per_output or group")
 
 
 @torch.no_grad()
 def apply_weight_qdq(modules: dict[str, nn.Module], *, granularity: str,
                      group_size: int = 128) -> dict[str, dict[str, Any]]:
-    """Fake-quantize module weights in place (w8a8.py:417-447)."""
-    if granularity not in ("per_output", "group"):
-        raise ValueError("weight granularity must be per_output or group")
+    """Fake-quantize module weights in place (w8a8.py:417-447), with the
+    reference's report per module.  Each module's integer range and error are
+    reduced on the device and reach the host in one copy."""
+    qdq = _weight_qdq(granularity, group_size)
     reports = {}
     for name, module in modules.items():
-        if not hasattr(module, "weight"):
+        weight = getattr(module, "weight", None)
+        if weight is None:
             raise TypeError(f"{name} has no weight")
-        weight = module.weight
-        if granularity == "per_output":
-            dequantized, quantized, scales = _w.per_output_weight_qdq(weight)
-        else:
-            dequantized, quantized, scales = _w.groupwise_weight_qdq(weight, group_size=group_size)
-        error = dequantized.float() - weight.detach().float()
-        module.weight.copy_(dequantized)
+        dequantized, quantized, scales = qdq(weight)
+        rmse = (dequantized.float() - weight.detach().float()).square().mean().sqrt()
+        q_lo, q_hi, err = torch.stack([quantized.min().double(), quantized.max().double(),
+                                       rmse.double()]).tolist()
+        shape = list(weight.shape)
+        weight.copy_(dequantized)
         reports[name] = {
-            "shape": list(weight.shape),
+            "shape": shape,
             "parameters": weight.numel(),
             "granularity": granularity,
             "group_size": group_size if granularity == "group" else None,
             "scale_shape": list(scales.shape),
-            "quantized_min": int(quantized.min().item()),
-            "quantized_max": int(quantized.max().item()),
-            "rmse": float(error.square().mean().sqrt().item()),
+            "quantized_min": int(q_lo),
+            "quantized_max": int(q_hi),
+            "rmse": err,
         }
     return reports
+
+
+_SMOOTH_EPS = 1e-5
+
+
+def _smoothing_vector(act_absmax: torch.Tensor, weight_absmax: torch.Tensor,
+                      alpha: float) -> torch.Tensor:
+    """SmoothQuant's per-channel factor (w8a8.py:399-404): ``max(a^alpha /
+    w^(1-alpha), 1e-5)`` with both maxima floored at 1e-5, then stored as
+    binary16 and floored again."""
+    ratio = act_absmax.clamp_min(_SMOOTH_EPS).pow(alpha) / \
+        weight_absmax.clamp_min(_SMOOTH_EPS).pow(1.0 - alpha)
+    return ratio.clamp_min(_SMOOTH_EPS).to(torch.float16).float().clamp_min(_SMOOTH_EPS)
 
 
 @torch.no_grad()
@@ -188,38 +245,39 @@ def apply_smoothquant_transform(modules: dict[str, nn.Module],
                                 alpha: float = 0.5
                                 ) -> tuple[dict[str, torch.Tensor], dict[str, torch.Tensor]]:
     """Exact ``x/s, W*s`` smoothing and the post-transform static A8 scales
-    (w8a8.py:370-414): ``s = max(a^alpha / w^(1-alpha), 1e-5)`` per input
-    channel, stored as binary16 (clamped again at 1e-5), the weight scaled in
-    place.  Returns ``(input_smoothing_scales, activation_scales)`` on the CPU
-    like the reference."""
+    (w8a8.py:370-414).  Each weight is scaled in place along its input
+    channels (dimension 1); the smoothed activation maxima of all modules are
+    converted to static scales together on the device.  Returns
+    ``(input_smoothing_scales, activation_scales)`` on the CPU like the
+    reference."""
     if not 0.0 <= alpha <= 1.0:
         raise ValueError("SmoothQuant alpha must be in [0, 1]")
     missing = sorted(set(modules) - set(channel_absmax))
     if missing:
         raise RuntimeError(f"no channel calibration for modules: {missing[:3]}")
-    input_scales, activation_scales = {}, {}
-    eps = 1e-5
+    vectors: dict[str, torch.Tensor] = {}
+    post_peaks: list[torch.Tensor] = []
     for name, module in modules.items():
-        weight = module.weight.detach().float()
-        if isinstance(module, _CONV):
-            weight_absmax = weight.abs().amax(dim=tuple(i for i in range(weight.dim()) if i != 1))
-            shape = [1] * weight.dim()
-            shape[1] = weight.shape[1]
-        else:
-            weight_absmax = weight.reshape(weight.shape[0], -1).abs().amax(dim=0)
-            shape = [1, weight.shape[1]]
+        weight = module.weight
+        channels = weight.shape[1]
+        # Per input channel |W| max: input channels last, everything else rows.
+        weight_absmax = _channel_rows(weight.detach().float(), 1).abs().amax(dim=0)
         act_absmax = channel_absmax[name].float().to(weight.device)
         if act_absmax.numel() != weight_absmax.numel():
             raise ValueError(f"activation/weight channel mismatch for {name}: "
                              f"{act_absmax.numel()} versus {weight_absmax.numel()}")
-        smoothing = (act_absmax.clamp_min(eps).pow(alpha)
-                     / weight_absmax.clamp_min(eps).pow(1.0 - alpha)).clamp_min(eps)
-        smoothing = smoothing.to(torch.float16).float().clamp_min(eps)
-        module.weight.mul_(smoothing.to(module.weight.dtype).reshape(shape))
-        post_absmax = (act_absmax / smoothing).amax()
-        input_scales[name] = smoothing.cpu()
-        activation_scales[name] = _w.static_activation_scale(post_absmax,
-                                                             device=weight.device).cpu()
+        smoothing = _smoothing_vector(act_absmax, weight_absmax, alpha)
+        shape = [1] * weight.dim()
+        shape[1] = channels
+        weight.mul_(smoothing.to(weight.dtype).reshape(shape))
+        vectors[name] = smoothing
+        post_peaks.append((act_absmax / smoothing).amax())
+    if not vectors:
+        return {}, {}
+    device = post_peaks[0].device
+    scales = _w.scale_from_absmax(torch.stack([p.to(device) for p in post_peaks])).cpu()
+    input_scales = {name: v.cpu() for name, v in vectors.items()}
+    activation_scales = {name: scales[i] for i, name in enumerate(vectors)}
     return input_scales, activation_scales
 
 

@@ -78,12 +78,13 @@ class PackedW8A8Weight:
         return cls.from_int8(q, s, bias, layout=layout)
 
 
-def _packed(build, source: torch.Tensor, weight_cache, cache_key: str, verify_source: bool):
+def _packed(build, source: torch.Tensor, weight_cache, cache_key: str, verify_source: bool,
+            layout: int = _lib.ROWS_AS_IS):
     if weight_cache is None:
         return build()
     from . import weight_cache as _wc
     return _wc.cached(weight_cache, cache_key, build, source=source,
-                      verify_source=verify_source, device=source.device)
+                      verify_source=verify_source, device=source.device, layout=layout)
 
 
 def _interleave_halves(v: torch.Tensor) -> torch.Tensor:
@@ -134,23 +135,26 @@ class W8A8Linear(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         p = self.weight_q
         if self.smooth is None and self.static_scale is None:
-            return _w.linear_dynamic(x, p.packed, p.scale, p.bias, p.out_features)
+            return _w.linear_dynamic(x, p.packed, p.scale, p.bias, p.out_features,
+                                     in_features=p.in_features)
+        if x.shape[-1] != p.in_features:
+            raise ValueError("linear input/weight shapes do not match")
         out = _w.prologue_quant(x, smooth=self.smooth, static_scale=self.static_scale)
         return _w.linear_i8in(out.q, out.scale.reshape(-1), p.packed, p.scale, p.bias,
-                              p.out_features, out_dtype=x.dtype)
+                              p.out_features, out_dtype=x.dtype, in_features=p.in_features)
 
     def forward_i8(self, xq: torch.Tensor, x_scale: torch.Tensor,
                    out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
         """Same product for int8 activations with per-row scales."""
         p = self.weight_q
         return _w.linear_i8in(xq, x_scale, p.packed, p.scale, p.bias, p.out_features,
-                              out_dtype=out_dtype)
+                              out_dtype=out_dtype, in_features=p.in_features)
 
     def accumulators(self, x: torch.Tensor) -> torch.Tensor:
         """Raw int32 accumulators of ``forward`` (for exactness checks)."""
         p = self.weight_q
         return _w.linear_dynamic(x, p.packed, p.scale, None, p.out_features,
-                                 epilogue=_lib.EPI_I32)
+                                 epilogue=_lib.EPI_I32, in_features=p.in_features)
 
 
 class W8A8PackedQKV(nn.Module):
@@ -219,19 +223,20 @@ class W8A8GateUpSiluMul(nn.Module):
                               bu if bu is not None else wu.new_zeros(wu.shape[0])])
         self.weight_q = _packed(
             lambda: PackedW8A8Weight.from_float(weight, bias, layout=_lib.ROWS_INTERLEAVE_HALVES),
-            weight, weight_cache, cache_key, verify_source)
+            weight, weight_cache, cache_key, verify_source, _lib.ROWS_INTERLEAVE_HALVES)
         self.intermediate = wg.shape[0]
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         p = self.weight_q
         return _w.linear_dynamic(x, p.packed, p.scale, p.bias, p.out_features,
-                                 epilogue=_lib.EPI_SILU_MUL)
+                                 epilogue=_lib.EPI_SILU_MUL, in_features=p.in_features)
 
     def forward_q8(self, x: torch.Tensor, h_scale: float) -> torch.Tensor:
         """``quantize_symmetric(SiLU(g) * u, h_scale)`` as int8 (static requant)."""
         p = self.weight_q
         return _w.linear_dynamic(x, p.packed, p.scale, p.bias, p.out_features,
-                                 epilogue=_lib.EPI_SILU_MUL_Q8, y_scale=h_scale)
+                                 epilogue=_lib.EPI_SILU_MUL_Q8, y_scale=h_scale,
+                                 in_features=p.in_features)
 
     def forward_i8(self, xq: torch.Tensor, x_scale: torch.Tensor, *,
                    out_dtype: torch.dtype = torch.float16,
@@ -242,16 +247,17 @@ class W8A8GateUpSiluMul(nn.Module):
         if h_scale is None:
             return _w.linear_i8in(xq, x_scale, p.packed, p.scale, p.bias, p.out_features,
                                   epilogue=_lib.EPI_SILU_MUL, out_dtype=out_dtype,
-                                  inter_dtype=out_dtype)
+                                  inter_dtype=out_dtype, in_features=p.in_features)
         return _w.linear_i8in(xq, x_scale, p.packed, p.scale, p.bias, p.out_features,
                               epilogue=_lib.EPI_SILU_MUL_Q8, out_dtype=torch.int8,
-                              y_scale=h_scale, inter_dtype=out_dtype)
+                              y_scale=h_scale, inter_dtype=out_dtype,
+                              in_features=p.in_features)
 
     def accumulators(self, x: torch.Tensor) -> torch.Tensor:
         """int32 accumulators in packed (interleaved) column order."""
         p = self.weight_q
         return _w.linear_dynamic(x, p.packed, p.scale, None, p.out_features,
-                                 epilogue=_lib.EPI_I32)
+                                 epilogue=_lib.EPI_I32, in_features=p.in_features)
 
 
 class W8A8MLP(nn.Module):

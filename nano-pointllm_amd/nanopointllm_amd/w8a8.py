@@ -120,11 +120,36 @@ def _workspace(m: int, k: int, device: torch.device) -> torch.Tensor:
     return torch.empty((max(workspace_bytes(m, k), 16),), dtype=torch.uint8, device=device)
 
 
-def gemm_i32(xq: torch.Tensor, w_packed: torch.Tensor, n: int) -> torch.Tensor:
+def _check_operands(k: int, w_packed: torch.Tensor, w_scale: torch.Tensor | None,
+                    bias: torch.Tensor | None, n: int, in_features: int | None) -> None:
+    """Host checks before any launch: the C ABI only sees pointers, so an
+    activation whose K differs from the packed weight's, or a weight, scale or
+    bias buffer shorter than ``n`` x ``k`` implies, must be refused here (the
+    reference's F.linear raises on the same mismatch, w8a8.py:126-127)."""
+    if in_features is not None and k != in_features:
+        raise ValueError("linear input/weight shapes do not match")
+    if w_packed.dtype != torch.int8 or not w_packed.is_contiguous():
+        raise ValueError("packed weight must be a contiguous int8 tensor")
+    if n < 0 or w_packed.numel() < packed_bytes(n, k):
+        raise ValueError("linear input/weight shapes do not match")
+    for name, t in (("weight scale", w_scale), ("bias", bias)):
+        if t is None:
+            continue
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 tensor")
+        if t.numel() < n:
+            raise ValueError(f"{name} must have one value per output")
+
+
+def gemm_i32(xq: torch.Tensor, w_packed: torch.Tensor, n: int, *,
+             in_features: int | None = None) -> torch.Tensor:
     """Exact ``int32(xq) @ int32(wq).T`` for packed ``wq`` ([..., K] -> [..., n])."""
     device = _lib.require_cuda(xq, w_packed)
+    if xq.dtype != torch.int8:
+        raise ValueError("gemm_i32 expects int8 activations")
     x2, ldq = _rows_view(xq)
     m, k = x2.shape
+    _check_operands(k, w_packed, None, None, n, in_features)
     acc = torch.empty((m, n), dtype=torch.int32, device=device)
     if m and n:
         ws = _workspace(m, k, device)
@@ -153,11 +178,17 @@ def linear_dynamic(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tenso
                    bias: torch.Tensor | None, n: int, *, epilogue: int = _lib.EPI_DEQUANT,
                    out_dtype: torch.dtype | None = None, y_scale: float = 0.0,
                    inter_dtype: torch.dtype | None = None,
-                   x_scale_out: torch.Tensor | None = None) -> torch.Tensor:
+                   x_scale_out: torch.Tensor | None = None,
+                   in_features: int | None = None) -> torch.Tensor:
     """Per-token dynamic A8 x per-output W8 linear with a fused epilogue."""
     device = _lib.require_cuda(x, w_packed, w_scale, bias)
     x2, ldx = _rows_view(x)
     m, k = x2.shape
+    _check_operands(k, w_packed, w_scale, bias, n, in_features)
+    if x_scale_out is not None and (x_scale_out.dtype != torch.float32
+                                    or not x_scale_out.is_contiguous()
+                                    or x_scale_out.numel() < m):
+        raise ValueError("x_scale_out must be a contiguous float32 tensor with one value per row")
     if out_dtype is None:
         out_dtype = _default_out_dtype(epilogue, x.dtype)
     if inter_dtype is None:
@@ -184,13 +215,17 @@ def linear_dynamic(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tenso
 def linear_i8in(xq: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor,
                 w_scale: torch.Tensor, bias: torch.Tensor | None, n: int, *,
                 epilogue: int = _lib.EPI_DEQUANT, out_dtype: torch.dtype | None = None,
-                y_scale: float = 0.0, inter_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+                y_scale: float = 0.0, inter_dtype: torch.dtype = torch.float16,
+                in_features: int | None = None) -> torch.Tensor:
     """W8A8 linear on already-quantized activations with per-row scales."""
     device = _lib.require_cuda(xq, x_scale, w_packed, w_scale, bias)
+    if xq.dtype != torch.int8:
+        raise ValueError("linear_i8in expects int8 activations")
     if out_dtype is None:
         out_dtype = _default_out_dtype(epilogue, torch.float16)
     x2, ldq = _rows_view(xq)
     m, k = x2.shape
+    _check_operands(k, w_packed, w_scale, bias, n, in_features)
     s = x_scale.detach().to(dtype=torch.float32).reshape(-1)
     if s.numel() == 1 and m != 1:
         s = s.expand(m)

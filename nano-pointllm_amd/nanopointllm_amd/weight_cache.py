@@ -89,9 +89,13 @@ def _read(root: Path, name: str, entry: dict[str, Any]) -> np.ndarray:
     return np.frombuffer(payload, dtype=dtype).reshape(shape).copy()
 
 
-def load_packed_weight(directory, device="cuda", *, source: torch.Tensor | None = None):
+def load_packed_weight(directory, device="cuda", *, source: torch.Tensor | None = None,
+                       shape: tuple[int, int] | None = None, layout: int | None = None):
     """Load one cache entry, checking every checksum (and, with ``source``,
-    that it was made from that weight) before uploading it."""
+    that it was made from that weight) before uploading it.  ``shape`` (N, K)
+    and ``layout`` are checked against the manifest first: a cache directory
+    reused for a model of other dimensions must not hand out a weight of the
+    wrong shape."""
     from .linear import PackedW8A8Weight
 
     root = Path(directory)
@@ -99,10 +103,16 @@ def load_packed_weight(directory, device="cuda", *, source: torch.Tensor | None 
     if manifest.get("schema_version") != CACHE_SCHEMA_VERSION or \
             manifest.get("cache_type") != CACHE_TYPE or manifest.get("tile_format") != TILE_FORMAT:
         raise ValueError("unsupported packed weight cache entry")
-    layout = {v: k for k, v in _LAYOUTS.items()}.get(manifest.get("row_layout"))
-    if layout is None:
+    entry_layout = {v: k for k, v in _LAYOUTS.items()}.get(manifest.get("row_layout"))
+    if entry_layout is None:
         raise ValueError("unknown row layout in packed weight cache entry")
     n, k = int(manifest["shape"]["n"]), int(manifest["shape"]["k"])
+    if shape is not None and (n, k) != (int(shape[0]), int(shape[1])):
+        raise ValueError(f"packed weight cache entry has shape {(n, k)}, expected "
+                         f"{(int(shape[0]), int(shape[1]))}")
+    if layout is not None and entry_layout != layout:
+        raise ValueError("packed weight cache entry has a different row layout")
+    layout = entry_layout
     if source is not None:
         if manifest.get("source_sha256") != source_sha256(source):
             raise ValueError("packed weight cache entry was made from a different weight")
@@ -120,13 +130,20 @@ def load_packed_weight(directory, device="cuda", *, source: torch.Tensor | None 
 
 
 def cached(directory, key: str, build, *, source: torch.Tensor | None = None,
-           verify_source: bool = False, device="cuda"):
+           verify_source: bool = False, device="cuda", layout: int | None = None):
     """Load ``directory/key`` if it exists, else ``build()`` the packed weight
-    and store it there (with the sha256 of ``source``).  ``verify_source``
-    checks a loaded entry against ``source`` (it hashes the source weight)."""
+    and store it there (with the sha256 of ``source``).  A loaded entry's N, K
+    must match ``source``'s shape and its row layout ``layout`` (cheap manifest
+    checks, always made); ``verify_source`` also checks it against ``source``'s
+    sha256 (it hashes the source weight)."""
     entry = Path(directory) / key
     if (entry / "metadata.json").exists():
-        return load_packed_weight(entry, device, source=source if verify_source else None)
+        shape = None
+        if source is not None:
+            flat = source.reshape(source.shape[0], -1)
+            shape = (int(flat.shape[0]), int(flat.shape[1]))
+        return load_packed_weight(entry, device, source=source if verify_source else None,
+                                  shape=shape, layout=layout)
     weight = build()
     save_packed_weight(entry, weight, source=source)
     return weight

@@ -1,7 +1,8 @@
-"""The GEMM tile rule (restated in gemm_tiles.py) on the LLaMA-7B prefill
-shapes that the measurements in the design notes quote: which configuration
-each shape takes on the MI355X's 256 CUs.  The GPU tests run every
-configuration for exactness; this pins the shape-to-configuration map."""
+"""The GEMM tile rule (the library's ``w8a8_gemm_tile_config`` query) on the
+LLaMA-7B prefill shapes that the measurements in the design notes quote:
+which configuration each shape takes on the MI355X's 256 CUs.  The GPU tests
+run every configuration for exactness; this pins the shape-to-configuration
+map, and the rule's invariants over a sweep of shapes."""
 from __future__ import annotations
 
 import pytest
@@ -36,3 +37,14 @@ def test_every_config_fits_one_round_or_is_the_widest():
                 assert tiles[cfg] <= 512 and tiles["big"] > 512
             if cfg == "w224":
                 assert tiles["w192"] > 512
+
+
+def test_query_rejects_empty_or_oversized_problems():
+    from nanopointllm_amd import _lib
+
+    lib = _lib.load()
+    for m, n, cus in ((0, 64, 256), (64, 0, 256), (64, 64, 0), (-1, 64, 256),
+                      (2 ** 31, 64, 256)):
+        assert lib.w8a8_gemm_tile_config(m, n, cus) == -1
+    # Largest accepted row count: the tile round-up still fits a signed int.
+    assert lib.w8a8_gemm_tile_config(2 ** 31 - 1 - 256, 4096, 256) >= 0
