@@ -48,8 +48,12 @@ typedef enum w8a8_status {
   W8A8_ERR_DTYPE = -3,     /* unsupported dtype / epilogue combination */
   W8A8_ERR_ALIGN = -4,     /* pointer or leading dimension misaligned */
   W8A8_ERR_WORKSPACE = -5, /* workspace missing or too small */
-  W8A8_ERR_HIP = -6        /* kernel launch failed; see w8a8_last_hip_error */
+  W8A8_ERR_HIP = -6,       /* kernel launch failed; see w8a8_last_hip_error */
+  W8A8_ERR_TOO_LARGE = -7  /* w8a8_linear_noalloc: more than its static scratch */
 } w8a8_status;
+
+/* Bytes of the static device scratch of w8a8_linear_noalloc (per GPU). */
+#define W8A8_NOALLOC_SCRATCH_BYTES (64 << 20)
 
 typedef enum w8a8_epilogue {
   /* y[m, n] = int32 accumulator */
@@ -180,6 +184,23 @@ int w8a8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
                 int64_t ldy, float y_scale, int inter_dtype, int64_t m, int64_t n, int64_t k,
                 float* x_scale_out, void* workspace, int64_t workspace_bytes,
                 hipStream_t stream);
+
+/*
+ * w8a8_linear without a workspace argument and without any allocation.  No
+ * counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  Shapes that w8a8_linear runs fused need
+ * no scratch; every other shape stages its quantized activations in a static
+ * device array of W8A8_NOALLOC_SCRATCH_BYTES per GPU, and a problem with
+ * w8a8_workspace_bytes(m, k) above that returns W8A8_ERR_TOO_LARGE before any
+ * launch.  All calls on one GPU share that array, so calls that overlap on
+ * one GPU (concurrent streams, or host threads) race: serialize them, e.g. on
+ * one stream.  Arguments, results and errors are otherwise w8a8_linear's.
+ */
+int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
+                        const float* w_scale, const float* bias, int epilogue, void* y,
+                        int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,
+                        int64_t n, int64_t k, float* x_scale_out, hipStream_t stream);
 
 /*
  * As w8a8_linear for already-quantized activations xq (int8 [m, ldq]) with

@@ -2,14 +2,30 @@
 // include/w8a8_gfx950.h).  Validation and dispatch only: shapes, dtypes,
 // alignment and workspace are checked here and reported as status codes; the
 // kernels live in quant.hip, gemv.hip and gemm.hip.
+#include <mutex>
+
 #include "w8a8_gfx950.h"
 #include "w8a8_internal.h"
 
 using namespace w8a8;
 
+// Scratch of w8a8_linear_noalloc: the per-call workspace of w8a8_linear
+// (activation scales + staged int8 activations) in a static device array, so
+// that entry point never allocates.  Every GPU the library runs on holds its
+// own copy for the life of the process.  In host code `scratch` names a
+// host-side stand-in, not the device address: only the address that
+// hipGetSymbolAddress returns for the current device may reach a kernel.
+static __device__ __align__(256) int8_t scratch[W8A8_NOALLOC_SCRATCH_BYTES];
+
 namespace {
 
 thread_local int g_last_hip_error = 0;
+
+// Device address of `scratch`, looked up once per device with that device
+// current (each device has the array at its own address).
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
 
 // Largest K whose worst-case dot product K * 127^2 fits a signed int32
 // (the overflow guard of compare_linear_bf16_qdq_integer, w8a8.py:152-153).
@@ -158,6 +174,24 @@ inline hipError_t stage_i8(const int8_t* xq, int64_t ldq, int64_t m, int64_t n, 
   return launch_pack_rows(xq, m, k, ldq, W8A8_ROWS_AS_IS, act, st);
 }
 
+// Looks up (once per device) the current device's address of `scratch`.
+int scratch_address(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return status_of(e);
+  if (dev < 0 || dev >= kMaxDevices) return W8A8_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return status_of(e);
+    if (p == nullptr) return W8A8_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return W8A8_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -180,6 +214,8 @@ const char* w8a8_status_string(int status) {
       return "workspace missing or too small";
     case W8A8_ERR_HIP:
       return "HIP kernel launch failed";
+    case W8A8_ERR_TOO_LARGE:
+      return "problem needs more than the static scratch of w8a8_linear_noalloc";
     default:
       return "unknown status";
   }
@@ -297,6 +333,28 @@ int w8a8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
   LinearOperands op = make_ops(act, kp, sx, w_packed, w_scale, bias, epilogue, y, y_dtype, ldy,
                                y_scale, inter_dtype, m, n, k);
   return status_of(run_product(op, stream));
+}
+
+int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
+                        const float* w_scale, const float* bias, int epilogue, void* y,
+                        int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,
+                        int64_t n, int64_t k, float* x_scale_out, hipStream_t stream) {
+  // Without a workspace, w8a8_linear validates every argument and either runs
+  // (decode shapes fused with the quantization need none) or reports
+  // W8A8_ERR_WORKSPACE before any launch.
+  int rc = w8a8_linear(x, x_dtype, ldx, w_packed, w_scale, bias, epilogue, y, y_dtype, ldy,
+                       y_scale, inter_dtype, m, n, k, x_scale_out, nullptr, 0, stream);
+  if (rc != W8A8_ERR_WORKSPACE) return rc;
+  if (w8a8_workspace_bytes(m, k) > W8A8_NOALLOC_SCRATCH_BYTES) return W8A8_ERR_TOO_LARGE;
+  void* ws = nullptr;
+  rc = scratch_address(&ws);
+  if (rc != W8A8_OK) return rc;
+  // The quantization writes every scratch byte the product then reads (the
+  // scales, and the int8 rows with their zero padding), so no clearing is
+  // needed between calls.
+  return w8a8_linear(x, x_dtype, ldx, w_packed, w_scale, bias, epilogue, y, y_dtype, ldy,
+                     y_scale, inter_dtype, m, n, k, x_scale_out, ws,
+                     W8A8_NOALLOC_SCRATCH_BYTES, stream);
 }
 
 int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,

@@ -22,6 +22,8 @@ ROWS_AS_IS, ROWS_INTERLEAVE_HALVES = 0, 1
 
 OK = 0
 ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ALIGN, ERR_WORKSPACE, ERR_HIP = -1, -2, -3, -4, -5, -6
+ERR_TOO_LARGE = -7
+NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _TORCH_TO_CODE = {
     torch.float32: F32,
@@ -43,6 +45,7 @@ EXPORTED_SYMBOLS = (
     "w8a8_pack_rows",
     "w8a8_gemm_i32",
     "w8a8_linear",
+    "w8a8_linear_noalloc",
     "w8a8_linear_i8in",
     "w8a8_linear_i8in_requant",
     "w8a8_prologue_quant",
@@ -71,6 +74,8 @@ _SIGNATURES = {
     "w8a8_gemm_i32": (_int, [_vp, _i64, _vp, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "w8a8_linear": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _int, _vp, _int, _i64, _f32, _int,
                            _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
+    "w8a8_linear_noalloc": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _int, _vp, _int, _i64, _f32,
+                                   _int, _i64, _i64, _i64, _vp, _vp]),
     "w8a8_linear_i8in": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _int, _vp, _int, _i64, _f32,
                                 _int, _i64, _i64, _i64, _vp, _i64, _vp]),
     "w8a8_linear_i8in_requant": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
