@@ -14,10 +14,11 @@ once in a HIP graph and replayed.  Inputs are resident in HBM before timing.
 N*K + 2N + 2MK + 2M*N_out per linear.  The `roofline` object is for the
 dominant kernel (the packed gate/up linear: per-token quantization, int8 GEMV and
 SiLU*mul in one kernel at M <= 8), timed with HIP
-events on the stream it is launched on.  `cpu_baseline` times the numpy
-restatement of the reference CPU integer path on a bounded sample (rank 0,
-N=1 only).  `extra` carries per-projection decode GB/s at M=1,4,8 and the
-prefill GEMM TOPS at M=560.
+events on the stream it is launched on.  `cpu_baseline` times the torch-CPU
+restatement of the reference's integer path on all host cores (rank 0, N=1
+only), and `parity` reports the GPU outputs' max-abs / max-relative error
+against it.  `extra` carries per-projection decode GB/s at M=1,4,8, the
+prefill GEMM TOPS at M=560/768/1024 and the stack with the fp16 LM head.
 
     python bench.py [--steps K] [--warmup W] [--m 8] [--no-extra] [--no-cpu]
 """
@@ -56,7 +57,6 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=32)
     ap.add_argument("--no-extra", action="store_true", help="skip the per-projection sweeps")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    ap.add_argument("--cpu-layers", type=int, default=16, help="layers in the CPU sample (~10 s)")
     ap.add_argument("--profile-gateup", action="store_true",
                     help="only the counter-calibration copy and the gate/up linear loop "
                          "(the region rocprofv3 --pmc runs measure)")
@@ -424,37 +424,127 @@ def stack_with_lm_head(layers, m: int, device) -> dict:
     return {"ms": round(ms, 4), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes}
 
 
-def cpu_baseline(layers, m: int, n_layers: int) -> dict:
-    """Reference CPU integer path (numpy restatement) on `n_layers` layers."""
-    import numpy as np
+def _median_s(fn, reps: int = 5) -> float:
+    """Median wall time of fn over reps runs, after one untimed run."""
+    fn()
+    times = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def _host_weight(layer, name: str, n: int, k: int):
+    """A layer's packed int8 weight back in row-major order on the host."""
+    import torch
+
+    p = layer.weights[name]
+    return (torch.from_numpy(_unpack_rows(p.packed.cpu().numpy(), n, k)), p.scale.cpu())
+
+
+def cpu_baseline(layers, m: int) -> dict:
+    """The reference CPU integer path (the torch restatement of
+    integer_linear_per_output_reference with per-token activation scales,
+    w8a8.py:106-139, in oracle/torch_path.py) on all host cores, median of 5
+    runs per configuration: config 1 ([16, 4096] x [4096, 4096]), the four
+    decode projections at M = m on one layer's weights (gate/up with
+    SiLU*mul), and O at M = 560.  `value` is the decode layer's rate in the
+    headline's unit."""
     import torch
 
     from nanopointllm_amd import workloads as W
-    from oracle import w8a8_oracle as O
+    from oracle import torch_path as T, w8a8_oracle as O
 
-    sample = []
-    for layer in layers[:n_layers]:
-        for spec in W.PROJECTIONS:
-            # Unpack the layer's int8 weight rows back to row-major on the host.
-            q = _unpack_rows(layer.weights[spec.name].packed.cpu().numpy(), spec.n, spec.k)
-            s = layer.weights[spec.name].scale.cpu().numpy()
-            x = (layer.x[spec.name] if spec.name in layer.x else
-                 W.decode_activations(m, spec.k, seed=5).to(torch.float16))
-            sample.append((spec, x.cpu().numpy(), q, s))
-    nbytes = 0
-    t0 = time.perf_counter()
-    for spec, x, q, s in sample:
-        out, _, _, _ = O.w8a8_linear_dynamic(x, q, s, exact_int=True)
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    configs = {}
+
+    def record(name, fn, nbytes, ops):
+        t = _median_s(fn)
+        configs[name] = {"ms": round(t * 1e3, 3), "GBps": round(nbytes / t / 1e9, 3),
+                         "GOPS": round(ops / t / 1e9, 2)}
+        return t
+
+    x1, w1 = W.config1()
+    _, q1, s1 = O.per_output_weight_qdq(w1.float().numpy())
+    q1, s1 = torch.from_numpy(q1), torch.from_numpy(s1)
+    record("config1_m16_n4096_k4096", lambda: T.per_token_linear(x1, q1, s1)[0].half(),
+           W.algorithmic_bytes(16, 4096, 4096), W.algorithmic_ops(16, 4096, 4096))
+    layer_bytes, layer_s = 0, 0.0
+    for spec in W.PROJECTIONS:
+        q, sc = _host_weight(layers[0], spec.name, spec.n, spec.k)
+        x = W.decode_activations(m, spec.k, seed=5)
         if spec.silu:
-            O.silu_mul_hf(out[:, 0::2].astype(np.float16), out[:, 1::2].astype(np.float16))
+            fn = (lambda x=x, q=q, sc=sc: T.silu_mul(T.per_token_linear(x, q, sc)[0].half()))
         else:
-            out.astype(np.float16)
-        nbytes += W.algorithmic_bytes(m, spec.n, spec.k, silu=spec.silu)
-    dt = time.perf_counter() - t0
-    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"{n_layers} of 32 layers (4 projections each) at M={m}: numpy int32 "
-                      f"matmul restatement of integer_linear_per_output_reference, "
-                      f"{nbytes / 1e6:.1f} MB in {dt:.1f} s"}
+            fn = (lambda x=x, q=q, sc=sc: T.per_token_linear(x, q, sc)[0].half())
+        nbytes = W.algorithmic_bytes(m, spec.n, spec.k, silu=spec.silu)
+        layer_s += record(f"decode_m{m}_{spec.name}", fn, nbytes,
+                          W.algorithmic_ops(m, spec.n, spec.k))
+        layer_bytes += nbytes
+    q, sc = _host_weight(layers[0], "o", W.HIDDEN, W.HIDDEN)
+    xo = W.prefill_activations(560, W.HIDDEN, seed=11)
+    record("prefill_m560_o", lambda: T.per_token_linear(xo, q, sc)[0].half(),
+           W.algorithmic_bytes(560, W.HIDDEN, W.HIDDEN), W.algorithmic_ops(560, W.HIDDEN, W.HIDDEN))
+    return {"value": round(layer_bytes / layer_s / 1e9, 4), "unit": "GB/s", "cores": cores,
+            "kind": "port",
+            "sample": (f"torch CPU int32 restatement of integer_linear_per_output_reference "
+                       f"(per-token A8, w8a8.py:106-139), {cores} threads, median of 5 runs; "
+                       f"value = one layer's 4 decode projections at M={m} "
+                       f"({layer_bytes / 1e6:.1f} MB in {layer_s * 1e3:.1f} ms); per-config "
+                       f"rates in 'configs'"),
+            "configs": configs}
+
+
+def _error_stats(got: "torch.Tensor", ref32: "torch.Tensor") -> dict:
+    """max-abs and max-relative error (denominator clamped at 1e-8, as
+    _tensor_error in w8a8.py:254-262) of a 16-bit output against binary32."""
+    diff = (got.double() - ref32.double()).abs()
+    rel = diff / ref32.double().abs().clamp_min(1e-8)
+    return {"max_abs": float(diff.max()), "max_rel": float(rel.max()),
+            "mean_abs": float(diff.mean())}
+
+
+def parity_report(layers, m: int, device) -> dict:
+    """The GPU's outputs against the CPU path (oracle/torch_path.py) on the
+    same inputs: config 1 (dequant to fp16) and the packed gate/up with fused
+    SiLU*mul at M = m (the dominant kernel).  int32 accumulators compared for
+    equality; fp16 outputs with max-abs / max-relative error against the CPU
+    path's binary32 values and the fraction bit-equal to its fp16 result."""
+    import torch
+
+    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd.linear import PackedW8A8Weight
+    from oracle import torch_path as T, w8a8_oracle as O
+
+    out = {}
+    x1, w1 = W.config1()
+    _, q1, s1 = O.per_output_weight_qdq(w1.float().numpy())
+    q1, s1 = torch.from_numpy(q1), torch.from_numpy(s1)
+    p = PackedW8A8Weight.from_int8(q1.to(device), s1.to(device))
+    y = w8a8.linear_dynamic(x1.to(device), p.packed, p.scale, None, 4096).cpu()
+    acc = w8a8.linear_dynamic(x1.to(device), p.packed, p.scale, None, 4096,
+                              epilogue=_lib.EPI_I32).cpu()
+    ref, eacc = T.per_token_linear(x1, q1, s1)
+    out["config1"] = {"int32_equal": bool(torch.equal(acc, eacc)),
+                      "fp16_bit_equal_frac": float((y == ref.half()).float().mean()),
+                      **_error_stats(y, ref)}
+    q, sc = _host_weight(layers[0], "gateup", 2 * W.INTERMEDIATE, W.HIDDEN)
+    x = layers[0].x["gateup"]
+    p = layers[0].weights["gateup"]
+    h = w8a8.linear_dynamic(x, p.packed, p.scale, None, p.out_features,
+                            epilogue=_lib.EPI_SILU_MUL).cpu()
+    acc = w8a8.linear_dynamic(x, p.packed, p.scale, None, p.out_features,
+                              epilogue=_lib.EPI_I32).cpu()
+    gu32, eacc = T.per_token_linear(x.cpu(), q, sc)
+    pairs = gu32.half().view(m, -1, 2)
+    ref32 = torch.nn.functional.silu(pairs[..., 0]).float() * pairs[..., 1].float()
+    out[f"gateup_silu_m{m}"] = {"int32_equal": bool(torch.equal(acc, eacc)),
+                                "fp16_bit_equal_frac": float(
+                                    (h == T.silu_mul(gu32.half())).float().mean()),
+                                **_error_stats(h, ref32)}
+    return out
 
 
 def _unpack_rows(packed, rows: int, k: int):
@@ -528,11 +618,14 @@ def main() -> int:
         log("decode step with the int8 MLP chain")
         extra["decode_step_int8_mlp_chain"] = decode_step_int8_mlp(layers, m, device)
 
-    cpu = None
+    cpu = parity = None
     if not args.no_cpu:
-        log(f"cpu baseline on {args.cpu_layers} layers")
-        cpu = cpu_baseline(layers, m, args.cpu_layers)
-        log(f"cpu {cpu['value']} GB/s")
+        log("cpu baseline (torch int32 restatement, all host cores)")
+        cpu = cpu_baseline(layers, m)
+        log(f"cpu {cpu['value']} GB/s on {cpu['cores']} cores")
+        log("parity against the CPU path")
+        parity = parity_report(layers, m, device)
+        log(f"parity {json.dumps(parity)}")
 
     result = {
         "metric": "W8A8 GEMV HBM GB/s & GEMM int8 TOPS (% roofline) at M=1,8,560, LLaMA-7B",
@@ -547,13 +640,14 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
-        "config": {"workload": f"llama7b_decode_w8a8_linear_stack_{args.layers}L",
+        "config": {"workload": f"llama7b_decode_w8a8_linear_stack_{args.layers}L_without_lm_head",
                    "m": m, "layers": args.layers,
                    "projections": {p.name: [p.n, p.k] for p in W.PROJECTIONS},
                    "weights": "random-init ~N(0,0.02), per-output int8, packed",
                    "bytes_per_step": nbytes, "graph": True},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "parity": parity,
         "extra": extra,
     }
     print(json.dumps(result), flush=True)

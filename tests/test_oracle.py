@@ -470,3 +470,59 @@ def test_groupwise_weight_qdq_closed_forms():
     _, q128, s128 = O.groupwise_weight_qdq(w, group_size=128)       # 128 + 128 + 44
     assert s128.shape == (9, 3)
     np.testing.assert_array_equal(q128[:, 256:], O.per_output_weight_qdq(w[:, 256:])[1])
+
+
+# --------------------------------------- torch-CPU restatement (cpu baseline)
+def test_torch_path_equals_numpy_oracle():
+    """oracle/torch_path.py (the timed CPU baseline) against the numpy oracle:
+    scales, int8 values, int32 accumulators and binary32 outputs bit-equal on
+    activations with x20 outlier channels, binary16 and binary32 inputs."""
+    import torch
+
+    from oracle import torch_path as T
+
+    rng = np.random.default_rng(31)
+    for m, n, k, dt in ((13, 90, 700, np.float16), (4, 33, 4096, np.float32),
+                        (1, 16, 64, np.float16)):
+        x = rng.standard_normal((m, k)).astype(np.float32)
+        x[:, rng.permutation(k)[:8]] *= 20
+        x = x.astype(dt)
+        w = (rng.standard_normal((n, k)) * 0.02).astype(np.float32)
+        b = rng.standard_normal(n).astype(np.float32)
+        _, qw, sw = O.per_output_weight_qdq(w)
+        eout, eacc, exq, esx = O.w8a8_linear_dynamic(x, qw, sw, b, exact_int=True)
+        xt = torch.from_numpy(x)
+        sx = T.scale_from_absmax(xt.float().abs().amax(-1, keepdim=True))
+        np.testing.assert_array_equal(sx.numpy(), esx)
+        np.testing.assert_array_equal(T.quantize_symmetric(xt, sx).numpy(), exq)
+        out, acc = T.per_token_linear(xt, torch.from_numpy(qw), torch.from_numpy(sw),
+                                      torch.from_numpy(b))
+        assert acc.dtype == torch.int32
+        np.testing.assert_array_equal(acc.numpy(), eacc)
+        np.testing.assert_array_equal(out.numpy(), eout)
+
+
+def test_torch_path_tiny_kat_and_silu():
+    import torch
+
+    from oracle import torch_path as T
+
+    kat = GOLDEN["tiny_int32_linear"]
+    x = torch.tensor(kat["values"], dtype=torch.float32)
+    w = np.array(kat["weight"], np.float32)
+    _, qw, sw = O.per_output_weight_qdq(w)
+    out, acc = T.per_token_linear(x, torch.from_numpy(qw), torch.from_numpy(sw),
+                                  torch.tensor(kat["bias"], dtype=torch.float32))
+    eout, eacc = O.integer_linear_per_output(
+        x.numpy(), w, activation_scale=O.static_activation_scale(np.abs(x.numpy()).max()),
+        bias=np.array(kat["bias"], np.float32))
+    np.testing.assert_array_equal(acc.numpy(), eacc)
+    np.testing.assert_array_equal(out.numpy(), eout)
+    # SiLU*mul on an interleaved gate/up row: within one binary16 ulp of the
+    # numpy restatement (both round SiLU(g) to binary16, then the product).
+    g = np.random.default_rng(2).standard_normal((3, 64)).astype(np.float16) * 4
+    gu = np.stack([g[:, :32], g[:, 32:]], axis=-1).reshape(3, 64)
+    h = T.silu_mul(torch.from_numpy(gu)).numpy()
+    eh = O.silu_mul_hf(g[:, :32], g[:, 32:])
+    assert np.max(np.abs(h.astype(np.float32) - eh.astype(np.float32))
+                  / np.maximum(np.abs(eh.astype(np.float32)), 2 ** -14)) <= 2 ** -10
