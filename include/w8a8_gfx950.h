@@ -215,6 +215,34 @@ int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
                      int64_t workspace_bytes, hipStream_t stream);
 
 /*
+ * Packed gate/up with SiLU*mul and the two-phase per-token dynamic int8
+ * requantization of its output h (the dynamic_per_token_activation_qdq
+ * contract, w8a8.py:106-115, applied to the down projection's input of the
+ * LightweightMLP packed branch, lightweight_runner.py:344-379; the survey's
+ * w8a8_gateup_silu_mul, with the row absmax kept as per-block partial maxima
+ * in the workspace instead of a zeroed atomic buffer).
+ *   Phase 1: h [m, ldh] (h_dtype F16/BF16, n/2 columns) = SiLU(g) * u as
+ *            W8A8_EPI_SILU_MUL of w8a8_linear (x of F32/F16/BF16, quantized
+ *            per token) or of w8a8_linear_i8in (x_dtype W8A8_I8 with per-row
+ *            x_scale); the epilogue also writes each row's max |h| over each
+ *            16-row weight block to the workspace.
+ *   Phase 2: h_scale[r] = scale_from_absmax(max over the row's blocks),
+ *            hq [m, ldhq] = quantize_symmetric(h, h_scale[r]): exactly
+ *            dynamic per-token quantization of h, without a second read of h
+ *            for its absmax.
+ * Workspace: w8a8_gateup_workspace_bytes(m, n, k) bytes, 256-byte aligned,
+ * always required (no state survives the call).
+ */
+int w8a8_gateup_silu_mul(const void* x, int x_dtype, int64_t ldx, const float* x_scale,
+                         const int8_t* w_packed, const float* w_scale, const float* bias, void* h,
+                         int h_dtype, int64_t ldh, int8_t* hq, int64_t ldhq, float* h_scale,
+                         int64_t m, int64_t n, int64_t k, void* workspace,
+                         int64_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes of w8a8_gateup_silu_mul for an m x n x k problem. */
+int64_t w8a8_gateup_workspace_bytes(int64_t m, int64_t n, int64_t k);
+
+/*
  * Activation prologue fused into the quantization, one pass per row of x
  * (F16/BF16 [m, ldx]), each step optional:
  *   residual add   s = x + residual (x's dtype), written to residual_out

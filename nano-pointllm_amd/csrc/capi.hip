@@ -72,6 +72,10 @@ inline int64_t scale_region(int64_t m) { return round_up(4 * m, 256); }
 inline int64_t act_region(int64_t m, int64_t k) {
   return round_up(m, kTileRows) * round_up(k, kTileK);
 }
+// Per-row, per-16-row-block partial maxima of the two-phase requantization.
+inline int64_t parts_region(int64_t m, int64_t n) {
+  return round_up(4 * m * ceil_div(n, kTileRows), 256);
+}
 
 // Checks an epilogue / output dtype pair and returns the number of output
 // columns, or -1 when the combination is unsupported.
@@ -172,6 +176,76 @@ inline hipError_t stage_i8(const int8_t* xq, int64_t ldq, int64_t m, int64_t n, 
   *a = act;
   *lda = kp;
   return launch_pack_rows(xq, m, k, ldq, W8A8_ROWS_AS_IS, act, st);
+}
+
+// w8a8_linear; absmax_parts (nullable, W8A8_EPI_SILU_MUL only, [m][ceil(n/16)]
+// binary32) receives the first phase of the two-phase per-token
+// requantization of the output.
+int linear_impl(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
+                const float* w_scale, const float* bias, int epilogue, void* y, int y_dtype,
+                int64_t ldy, float y_scale, int inter_dtype, int64_t m, int64_t n, int64_t k,
+                float* x_scale_out, void* workspace, int64_t workspace_bytes,
+                float* absmax_parts, hipStream_t stream) {
+  if (!float_dtype(x_dtype)) return W8A8_ERR_DTYPE;
+  // The integer requant needs int8 activations with a static scale
+  // (w8a8_linear_i8in_requant); the single-rounding bf16 dequant has no bias.
+  if (epilogue == W8A8_EPI_REQUANT) return W8A8_ERR_DTYPE;
+  if (epilogue == W8A8_EPI_DEQUANT_BF16_EXACT && bias != nullptr) return W8A8_ERR_DTYPE;
+  int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
+                        n, k);
+  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
+  if (x == nullptr) return W8A8_ERR_NULL;
+  if (ldx < k) return W8A8_ERR_SHAPE;
+  if (!aligned(x, static_cast<uintptr_t>(elem_size(x_dtype)))) return W8A8_ERR_ALIGN;
+  if (x_scale_out != nullptr && !aligned(x_scale_out, 4)) return W8A8_ERR_ALIGN;
+  if (k > 0 && epilogue <= W8A8_EPI_SILU_MUL_Q8 && fused_gemv_supported(x, x_dtype, ldx, m, n, k)) {
+    // Decode: quantization fused into the GEMV, no workspace.
+    LinearOperands op = make_ops(nullptr, 0, nullptr, w_packed, w_scale, bias, epilogue, y,
+                                 y_dtype, ldy, y_scale, inter_dtype, m, n, k);
+    op.absmax_parts = absmax_parts;
+    return status_of(launch_gemv_fused(x, x_dtype, ldx, op, x_scale_out, stream));
+  }
+  if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
+    return W8A8_ERR_WORKSPACE;
+  if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
+  float* sx = x_scale_out != nullptr ? x_scale_out : static_cast<float*>(workspace);
+  int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
+  const int64_t kp = round_up(k, kTileK);
+  const bool gemv = use_gemv(m, n);
+  hipError_t e = launch_quant_rows(x, x_dtype, ldx, m, k, nullptr, 0, act, kp, kp, !gemv, sx,
+                                   stream);
+  if (e != hipSuccess) return status_of(e);
+  LinearOperands op = make_ops(act, kp, sx, w_packed, w_scale, bias, epilogue, y, y_dtype, ldy,
+                               y_scale, inter_dtype, m, n, k);
+  op.absmax_parts = absmax_parts;
+  return status_of(run_product(op, stream));
+}
+
+// w8a8_linear_i8in; absmax_parts as in linear_impl.
+int linear_i8in_impl(const int8_t* xq, int64_t ldq, const float* x_scale,
+                     const int8_t* w_packed, const float* w_scale, const float* bias,
+                     int epilogue, void* y, int y_dtype, int64_t ldy, float y_scale,
+                     int inter_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                     int64_t workspace_bytes, float* absmax_parts, hipStream_t stream) {
+  if (epilogue == W8A8_EPI_REQUANT) return W8A8_ERR_DTYPE;  // w8a8_linear_i8in_requant
+  if (epilogue == W8A8_EPI_DEQUANT_BF16_EXACT && bias != nullptr) return W8A8_ERR_DTYPE;
+  int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
+                        n, k);
+  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
+  if (xq == nullptr || (epilogue != W8A8_EPI_I32 && x_scale == nullptr)) return W8A8_ERR_NULL;
+  if (ldq < k) return W8A8_ERR_SHAPE;
+  if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
+    return W8A8_ERR_WORKSPACE;
+  if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
+  int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
+  const int8_t* a = nullptr;
+  int64_t lda = 0;
+  hipError_t e = stage_i8(xq, ldq, m, n, k, act, &a, &lda, stream);
+  if (e != hipSuccess) return status_of(e);
+  LinearOperands op = make_ops(a, lda, x_scale, w_packed, w_scale, bias, epilogue, y, y_dtype,
+                               ldy, y_scale, inter_dtype, m, n, k);
+  op.absmax_parts = absmax_parts;
+  return status_of(run_product(op, stream));
 }
 
 // Looks up (once per device) the current device's address of `scratch`.
@@ -302,37 +376,61 @@ int w8a8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
                 int64_t ldy, float y_scale, int inter_dtype, int64_t m, int64_t n, int64_t k,
                 float* x_scale_out, void* workspace, int64_t workspace_bytes,
                 hipStream_t stream) {
-  if (!float_dtype(x_dtype)) return W8A8_ERR_DTYPE;
-  // The integer requant needs int8 activations with a static scale
-  // (w8a8_linear_i8in_requant); the single-rounding bf16 dequant has no bias.
-  if (epilogue == W8A8_EPI_REQUANT) return W8A8_ERR_DTYPE;
-  if (epilogue == W8A8_EPI_DEQUANT_BF16_EXACT && bias != nullptr) return W8A8_ERR_DTYPE;
-  int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
+  return linear_impl(x, x_dtype, ldx, w_packed, w_scale, bias, epilogue, y, y_dtype, ldy,
+                     y_scale, inter_dtype, m, n, k, x_scale_out, workspace, workspace_bytes,
+                     nullptr, stream);
+}
+
+int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
+                     const int8_t* w_packed, const float* w_scale, const float* bias,
+                     int epilogue, void* y, int y_dtype, int64_t ldy, float y_scale,
+                     int inter_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
+                     int64_t workspace_bytes, hipStream_t stream) {
+  return linear_i8in_impl(xq, ldq, x_scale, w_packed, w_scale, bias, epilogue, y, y_dtype, ldy,
+                          y_scale, inter_dtype, m, n, k, workspace, workspace_bytes, nullptr,
+                          stream);
+}
+
+int64_t w8a8_gateup_workspace_bytes(int64_t m, int64_t n, int64_t k) {
+  if (m < 0 || n < 0 || k < 0) return -1;
+  return parts_region(m, n) + w8a8_workspace_bytes(m, k);
+}
+
+int w8a8_gateup_silu_mul(const void* x, int x_dtype, int64_t ldx, const float* x_scale,
+                         const int8_t* w_packed, const float* w_scale, const float* bias, void* h,
+                         int h_dtype, int64_t ldh, int8_t* hq, int64_t ldhq, float* h_scale,
+                         int64_t m, int64_t n, int64_t k, void* workspace,
+                         int64_t workspace_bytes, hipStream_t stream) {
+  if (!half_dtype(h_dtype)) return W8A8_ERR_DTYPE;
+  if (m < 0 || n < 0 || k < 0) return W8A8_ERR_SHAPE;
+  if (m == 0 || n == 0)
+    return check_linear(w_packed, w_scale, W8A8_EPI_SILU_MUL, h, h_dtype, ldh, 0.0f, h_dtype, m,
                         n, k);
-  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
-  if (x == nullptr) return W8A8_ERR_NULL;
-  if (ldx < k) return W8A8_ERR_SHAPE;
-  if (!aligned(x, static_cast<uintptr_t>(elem_size(x_dtype)))) return W8A8_ERR_ALIGN;
-  if (x_scale_out != nullptr && !aligned(x_scale_out, 4)) return W8A8_ERR_ALIGN;
-  if (k > 0 && epilogue <= W8A8_EPI_SILU_MUL_Q8 && fused_gemv_supported(x, x_dtype, ldx, m, n, k)) {
-    // Decode: quantization fused into the GEMV, no workspace.
-    LinearOperands op = make_ops(nullptr, 0, nullptr, w_packed, w_scale, bias, epilogue, y,
-                                 y_dtype, ldy, y_scale, inter_dtype, m, n, k);
-    return status_of(launch_gemv_fused(x, x_dtype, ldx, op, x_scale_out, stream));
-  }
-  if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
+  if (h == nullptr || hq == nullptr || h_scale == nullptr) return W8A8_ERR_NULL;
+  if (ldhq < n / 2) return W8A8_ERR_SHAPE;
+  if (!aligned(h_scale, 4)) return W8A8_ERR_ALIGN;
+  if (workspace == nullptr || workspace_bytes < w8a8_gateup_workspace_bytes(m, n, k))
     return W8A8_ERR_WORKSPACE;
-  if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
-  float* sx = x_scale_out != nullptr ? x_scale_out : static_cast<float*>(workspace);
-  int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
-  const int64_t kp = round_up(k, kTileK);
-  const bool gemv = use_gemv(m, n);
-  hipError_t e = launch_quant_rows(x, x_dtype, ldx, m, k, nullptr, 0, act, kp, kp, !gemv, sx,
-                                   stream);
-  if (e != hipSuccess) return status_of(e);
-  LinearOperands op = make_ops(act, kp, sx, w_packed, w_scale, bias, epilogue, y, y_dtype, ldy,
-                               y_scale, inter_dtype, m, n, k);
-  return status_of(run_product(op, stream));
+  if (!aligned(workspace, 256)) return W8A8_ERR_ALIGN;
+  // Workspace: [partial maxima, m x ceil(n/16) binary32][w8a8_linear's].
+  float* parts = static_cast<float*>(workspace);
+  void* ws = static_cast<int8_t*>(workspace) + parts_region(m, n);
+  const int64_t ws_bytes = workspace_bytes - parts_region(m, n);
+  // Phase 1: the SiLU*mul linear; its epilogue leaves every row's max |h|
+  // per 16-row weight block in `parts`.
+  int rc;
+  if (x_dtype == W8A8_I8) {
+    rc = linear_i8in_impl(static_cast<const int8_t*>(x), ldx, x_scale, w_packed, w_scale, bias,
+                          W8A8_EPI_SILU_MUL, h, h_dtype, ldh, 0.0f, h_dtype, m, n, k, ws, ws_bytes,
+                          parts, stream);
+  } else {
+    rc = linear_impl(x, x_dtype, ldx, w_packed, w_scale, bias, W8A8_EPI_SILU_MUL, h, h_dtype, ldh,
+                     0.0f, h_dtype, m, n, k, nullptr, ws, ws_bytes, parts, stream);
+  }
+  if (rc != W8A8_OK) return rc;
+  // Phase 2: per-token int8 h with scale_from_absmax of each row's max.
+  return status_of(launch_quant_rows_parts(h, h_dtype, ldh, m, n / 2, parts,
+                                           ceil_div(n, kTileRows), hq, ldhq, h_scale, stream));
 }
 
 int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
@@ -355,31 +453,6 @@ int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w
   return w8a8_linear(x, x_dtype, ldx, w_packed, w_scale, bias, epilogue, y, y_dtype, ldy,
                      y_scale, inter_dtype, m, n, k, x_scale_out, ws,
                      W8A8_NOALLOC_SCRATCH_BYTES, stream);
-}
-
-int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
-                     const int8_t* w_packed, const float* w_scale, const float* bias,
-                     int epilogue, void* y, int y_dtype, int64_t ldy, float y_scale,
-                     int inter_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
-                     int64_t workspace_bytes, hipStream_t stream) {
-  if (epilogue == W8A8_EPI_REQUANT) return W8A8_ERR_DTYPE;  // w8a8_linear_i8in_requant
-  if (epilogue == W8A8_EPI_DEQUANT_BF16_EXACT && bias != nullptr) return W8A8_ERR_DTYPE;
-  int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
-                        n, k);
-  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
-  if (xq == nullptr || (epilogue != W8A8_EPI_I32 && x_scale == nullptr)) return W8A8_ERR_NULL;
-  if (ldq < k) return W8A8_ERR_SHAPE;
-  if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
-    return W8A8_ERR_WORKSPACE;
-  if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
-  int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
-  const int8_t* a = nullptr;
-  int64_t lda = 0;
-  hipError_t e = stage_i8(xq, ldq, m, n, k, act, &a, &lda, stream);
-  if (e != hipSuccess) return status_of(e);
-  LinearOperands op = make_ops(a, lda, x_scale, w_packed, w_scale, bias, epilogue, y, y_dtype,
-                               ldy, y_scale, inter_dtype, m, n, k);
-  return status_of(run_product(op, stream));
 }
 
 int w8a8_prologue_quant(const void* x, int x_dtype, int64_t ldx, const void* residual,

@@ -43,6 +43,7 @@ struct GemmParams {
   const uint32_t* rq_mult;
   const int32_t* rq_shift;
   const int32_t* rq_bias;
+  float* absmax_parts;  // kEpiSilu: [M][NB] per-block row |h|max (nullable)
   int M;
   int N;
   int MB;
@@ -224,6 +225,8 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
       }
     }
     if constexpr (kHalfCols) {
+      // kEpiSilu with absmax_parts: |h| of this lane's output for row pair r / 2.
+      [[maybe_unused]] float habs[2] = {0.0f, 0.0f};
       // Interleaved gate/up: even column = gate, odd column = up of output
       // n / 2.  Every lane dequantizes its own column at rows r and r + 1;
       // then the even lane forms output row r from its gate and the odd
@@ -253,8 +256,26 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
         const TH h = from_f32<TH>(silu_mul<TH>(g, u));
         if constexpr (EPI == kEpiSilu) {
           put(ml, nl / 2, ok, m, n / 2, h);
+          if (ok) habs[r >> 1] = fabsf(to_f32(h));
         } else {
           put(ml, nl / 2, ok, m, n / 2, static_cast<int8_t>(quant1(to_f32(h), p.out_scale)));
+        }
+      }
+      if constexpr (EPI == kEpiSilu) {
+        if (p.absmax_parts != nullptr) {
+          // Lanes of one parity in a 16-lane group hold the same output row
+          // (even lanes row r, odd lanes row r + 1) over the 8 outputs of
+          // packed block nb: reduce over them, then one store per row.
+          const int64_t nb = static_cast<int64_t>(nb0) + wn * BC + j;
+#pragma unroll
+          for (int h2 = 0; h2 < 2; ++h2) {
+            float v = habs[h2];
+#pragma unroll
+            for (int off = 2; off < 16; off <<= 1) v = fmaxf(v, __shfl_xor(v, off));
+            const int64_t m = static_cast<int64_t>(mb0) * 16 + 16 * (wm * BR + i) +
+                              4 * (lane >> 4) + 2 * h2 + (lane & 1);
+            if ((lane & 15) < 2 && m < p.M && nb < p.NB) p.absmax_parts[m * p.NB + nb] = v;
+          }
         }
       }
     } else {
@@ -405,6 +426,7 @@ hipError_t launch_gemm(const LinearOperands& op, hipStream_t st) {
   p.rq_mult = op.rq_mult;
   p.rq_shift = op.rq_shift;
   p.rq_bias = op.rq_bias;
+  p.absmax_parts = op.absmax_parts;
   p.M = static_cast<int>(op.M);
   p.N = static_cast<int>(op.N);
   p.MB = static_cast<int>(ceil_div(op.M, kTileRows));

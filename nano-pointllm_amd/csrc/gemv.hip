@@ -35,6 +35,7 @@ struct GemvParams {
   const uint32_t* rq_mult;
   const int32_t* rq_shift;
   const int32_t* rq_bias;
+  float* absmax_parts;  // kEpiSilu: [M][NB] per-block row |h|max (nullable)
   int M;
   int N;
   int KB;
@@ -148,30 +149,44 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
     // Interleaved gate/up: packed rows 2c (gate) and 2c+1 (up) of this block
     // produce output column nb*8 + c.
     const int64_t n_out_total = p.N / 2;
+    // MT * 128 and NT are multiples of 64, so every wavefront runs the same
+    // trip count and the shuffles below run in uniform control flow.
     for (int e = tid; e < MT * 128; e += NT) {
       const int mt = e >> 7;
       const int i = (e & 127) >> 3;
       const int c = e & 7;
       const int m = mt * 16 + i;
       const int64_t n_out = nb * 8 + c;
-      if (m >= p.M || n_out >= n_out_total) continue;
-      const int base = mt * 256 + i * 16 + 2 * c;
-      int32_t sg = 0, su = 0;
+      float habs = 0.0f;
+      if (m < p.M && n_out < n_out_total) {
+        const int base = mt * 256 + i * 16 + 2 * c;
+        int32_t sg = 0, su = 0;
 #pragma unroll
-      for (int w = 0; w < WAVES; ++w) {
-        sg += red[w][base];
-        su += red[w][base + 1];
+        for (int w = 0; w < WAVES; ++w) {
+          sg += red[w][base];
+          su += red[w][base + 1];
+        }
+        const int64_t ng = nb * 16 + 2 * c;
+        const float sxm = p.sx[m];
+        const float g = to_f32(from_f32<TH>(dequant1(sg, sxm, p.sw[ng], p.bias, ng)));
+        const float u = to_f32(from_f32<TH>(dequant1(su, sxm, p.sw[ng + 1], p.bias, ng + 1)));
+        const TH h = from_f32<TH>(silu_mul<TH>(g, u));
+        TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n_out;
+        if constexpr (EPI == kEpiSilu) {
+          *y = h;
+          habs = fabsf(to_f32(h));
+        } else {
+          *y = static_cast<int8_t>(quant1(to_f32(h), p.out_scale));
+        }
       }
-      const int64_t ng = nb * 16 + 2 * c;
-      const float sxm = p.sx[m];
-      const float g = to_f32(from_f32<TH>(dequant1(sg, sxm, p.sw[ng], p.bias, ng)));
-      const float u = to_f32(from_f32<TH>(dequant1(su, sxm, p.sw[ng + 1], p.bias, ng + 1)));
-      const TH h = from_f32<TH>(silu_mul<TH>(g, u));
-      TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n_out;
       if constexpr (EPI == kEpiSilu) {
-        *y = h;
-      } else {
-        *y = static_cast<int8_t>(quant1(to_f32(h), p.out_scale));
+        if (p.absmax_parts != nullptr) {
+          // Row m's 8 outputs of this block sit in 8 consecutive lanes.
+#pragma unroll
+          for (int off = 1; off < 8; off <<= 1) habs = fmaxf(habs, __shfl_xor(habs, off));
+          if (c == 0 && m < p.M)
+            p.absmax_parts[static_cast<int64_t>(m) * gridDim.x + nb] = habs;
+        }
       }
     }
   }
@@ -217,6 +232,7 @@ hipError_t launch_gemv(const LinearOperands& op, hipStream_t st) {
   p.rq_mult = op.rq_mult;
   p.rq_shift = op.rq_shift;
   p.rq_bias = op.rq_bias;
+  p.absmax_parts = op.absmax_parts;
   p.M = static_cast<int>(op.M);
   p.N = static_cast<int>(op.N);
   p.KB = static_cast<int>(ceil_div(op.K, kTileK));

@@ -66,6 +66,7 @@ struct FusedParams {
   int64_t ldy;
   float* sx_out;
   const float* sx_in;  // int8 x: its per-row scales
+  float* absmax_parts;  // kEpiSilu: [M][NB] per-block row |h|max (nullable)
   float out_scale;
   int M;
   int N;
@@ -116,10 +117,13 @@ __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
   } else {
     // Interleaved gate/up: packed rows 2c (gate) and 2c+1 (up) of the block
     // produce output column nb*8 + c.
+    // Threads below 128 fill whole wavefronts, so the shuffles below run in
+    // uniform control flow.
     if (tid < 128) {
       const int m = tid >> 3;
       const int cc = tid & 7;
       const int64_t n_out = nb * 8 + cc;
+      float habs = 0.0f;
       if (m < M && n_out < p.N / 2) {
         const int base = m * 16 + 2 * cc;
         int32_t sg = 0, su = 0;
@@ -137,8 +141,17 @@ __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
         TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n_out;
         if constexpr (EPI == kEpiSilu) {
           *y = h;
+          habs = fabsf(to_f32(h));
         } else {
           *y = static_cast<int8_t>(quant1(to_f32(h), p.out_scale));
+        }
+      }
+      if constexpr (EPI == kEpiSilu) {
+        if (p.absmax_parts != nullptr) {
+          // Row m's 8 outputs of this block sit in 8 consecutive lanes.
+#pragma unroll
+          for (int off = 1; off < 8; off <<= 1) habs = fmaxf(habs, __shfl_xor(habs, off));
+          if (cc == 0 && m < M) p.absmax_parts[static_cast<int64_t>(m) * p.NB + nb] = habs;
         }
       }
     }
@@ -524,6 +537,7 @@ hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const Line
   p.ldy = op.ldy;
   p.sx_out = sx_out;
   p.sx_in = nullptr;
+  p.absmax_parts = op.absmax_parts;
   p.out_scale = op.out_scale;
   p.M = static_cast<int>(op.M);
   p.N = static_cast<int>(op.N);
@@ -567,6 +581,7 @@ hipError_t launch_gemv_fused_i8(const LinearOperands& op, hipStream_t st) {
   p.ldy = op.ldy;
   p.sx_out = nullptr;
   p.sx_in = op.sx;
+  p.absmax_parts = op.absmax_parts;
   p.out_scale = op.out_scale;
   p.M = static_cast<int>(op.M);
   p.N = static_cast<int>(op.N);

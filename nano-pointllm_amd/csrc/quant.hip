@@ -147,6 +147,77 @@ __global__ __launch_bounds__(NT) void quant_rows_kernel(
   }
 }
 
+// Second phase of the two-phase per-token requantization (one workgroup per
+// row): the producing epilogue left the row's |x|max split over nparts
+// partial maxima, parts[row * nparts + i]; their max gives the binary16
+// scale (scale_from_absmax, w8a8.py:46-50) without a reduction over x, and
+// the row is quantized (quantize_symmetric, w8a8.py:33-43) into row-major q.
+// The row's chunks (REG per thread, or a second pass when REG is 0) are
+// requested before the partials, so both reads are in flight together.
+template <typename TX, int REG, int NT>
+__global__ __launch_bounds__(NT) void quant_rows_parts_kernel(
+    const TX* __restrict__ x, int64_t ldx, int64_t K, int vec_in,
+    const float* __restrict__ parts, int64_t nparts, int8_t* __restrict__ q, int64_t ldq,
+    int vec_out, float* __restrict__ scales_out) {
+  __shared__ float red[NT / 64];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x;
+  const TX* xr = x + row * ldx;
+  const int64_t nchunk = (K + 7) / 8;
+  float v[REG > 0 ? REG : 1][8];
+  if constexpr (REG > 0) {
+#pragma unroll
+    for (int c = 0; c < REG; ++c) {
+      const int64_t k0 = (tid + static_cast<int64_t>(c) * NT) * 8;
+      const int64_t rem = K - k0;
+      if (rem > 0) {
+        load8(xr + k0, v[c], vec_in != 0, static_cast<int>(rem < 8 ? rem : 8));
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[c][j] = 0.0f;
+      }
+    }
+  }
+  const float* pr = parts + row * nparts;
+  float amax = 0.0f;
+  for (int64_t i = tid; i < nparts; i += NT) amax = fmaxf(amax, pr[i]);
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < NT / 64; ++w) amax = fmaxf(amax, red[w]);
+  const float s = scale_from_absmax(amax);
+  const float r = 1.0f / s;
+  if (tid == 0) scales_out[row] = s;
+  if constexpr (REG > 0) {
+#pragma unroll
+    for (int c = 0; c < REG; ++c) {
+      const int64_t chunk = tid + static_cast<int64_t>(c) * NT;
+      if (chunk < nchunk) {
+        const int64_t k0 = chunk * 8;
+        const int valid = static_cast<int>(K - k0 < 8 ? K - k0 : 8);
+        int32_t qi[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) qi[j] = (j < valid) ? quant_elem<TX>(v[c][j], s, r, true) : 0;
+        store8<false>(q, row, k0, ldq, K, vec_out, 0, qi);
+      }
+    }
+  } else {
+    for (int64_t c = tid; c < nchunk; c += NT) {
+      const int64_t k0 = c * 8;
+      const int valid = static_cast<int>(K - k0 < 8 ? K - k0 : 8);
+      float t[8];
+      load8(xr + k0, t, vec_in != 0, valid);
+      int32_t qi[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qi[j] = (j < valid) ? quant_elem<TX>(t[j], s, r, true) : 0;
+      store8<false>(q, row, k0, ldq, K, vec_out, 0, qi);
+    }
+  }
+}
+
 // Packs a row-major int8 [rows, K] matrix into 16x64 tiles.  One thread per
 // 16-byte lane slot.  layout 1 maps packed row p to source row p/2 (p even)
 // or rows/2 + p/2 (p odd): the gate/up "interleave" order of
@@ -317,6 +388,67 @@ hipError_t launch_quant_rows(const void* x, int x_dtype, int64_t ldx, int64_t ro
     case kBF16:
       return quant_dispatch(static_cast<const __hip_bfloat16*>(x), ldx, rows, K, scale_in,
                             scale_stride, q, ldq, ncols_out, packed, scales_out, st);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+template <typename TX, int NT>
+void quant_parts_launch(dim3 g, hipStream_t st, int64_t chunks, const TX* x, int64_t ldx,
+                        int64_t K, int vec_in, const float* parts, int64_t nparts, int8_t* q,
+                        int64_t ldq, int vec_out, float* scales) {
+  const int64_t per = ceil_div(chunks, NT);
+#define W8A8_PARTS_REG(R)                                                                     \
+  hipLaunchKernelGGL((quant_rows_parts_kernel<TX, R, NT>), g, dim3(NT), 0, st, x, ldx, K,       \
+                     vec_in, parts, nparts, q, ldq, vec_out, scales)
+  if (per <= 1)
+    W8A8_PARTS_REG(1);
+  else if (per <= 2)
+    W8A8_PARTS_REG(2);
+  else if (per <= 4)
+    W8A8_PARTS_REG(4);
+  else if (per <= kRegChunksMax)
+    W8A8_PARTS_REG(kRegChunksMax);
+  else
+    W8A8_PARTS_REG(0);
+#undef W8A8_PARTS_REG
+}
+
+template <typename TX>
+hipError_t quant_parts_dispatch(const TX* x, int64_t ldx, int64_t rows, int64_t K,
+                                const float* parts, int64_t nparts, int8_t* q, int64_t ldq,
+                                float* scales, hipStream_t st) {
+  const int vec_in = aligned16(x) && (ldx % 8 == 0) && (K % 8 == 0);
+  const int vec_out = aligned8(q) && (ldq % 8 == 0);
+  const int64_t chunks = ceil_div(K, 8);
+  const dim3 g(static_cast<unsigned>(rows));
+  // Few rows (decode) get wide workgroups, as in quant_launch.
+  if (rows <= kGemvMaxRows && chunks > 2 * kQuantThreads)
+    quant_parts_launch<TX, 4 * kQuantThreads>(g, st, chunks, x, ldx, K, vec_in, parts, nparts, q,
+                                              ldq, vec_out, scales);
+  else if (rows <= kGemvMaxRows && chunks > kQuantThreads)
+    quant_parts_launch<TX, 2 * kQuantThreads>(g, st, chunks, x, ldx, K, vec_in, parts, nparts, q,
+                                              ldq, vec_out, scales);
+  else
+    quant_parts_launch<TX, kQuantThreads>(g, st, chunks, x, ldx, K, vec_in, parts, nparts, q,
+                                          ldq, vec_out, scales);
+  return hipGetLastError();
+}
+
+hipError_t launch_quant_rows_parts(const void* x, int x_dtype, int64_t ldx, int64_t rows,
+                                   int64_t K, const float* parts, int64_t nparts, int8_t* q,
+                                   int64_t ldq, float* scales_out, hipStream_t st) {
+  if (rows == 0) return hipSuccess;
+  switch (x_dtype) {
+    case kF32:
+      return quant_parts_dispatch(static_cast<const float*>(x), ldx, rows, K, parts, nparts, q,
+                                  ldq, scales_out, st);
+    case kF16:
+      return quant_parts_dispatch(static_cast<const __half*>(x), ldx, rows, K, parts, nparts, q,
+                                  ldq, scales_out, st);
+    case kBF16:
+      return quant_parts_dispatch(static_cast<const __hip_bfloat16*>(x), ldx, rows, K, parts,
+                                  nparts, q, ldq, scales_out, st);
     default:
       return hipErrorInvalidValue;
   }

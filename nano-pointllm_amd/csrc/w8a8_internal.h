@@ -34,6 +34,12 @@ struct LinearOperands {
   const uint32_t* rq_mult = nullptr;
   const int32_t* rq_shift = nullptr;
   const int32_t* rq_bias = nullptr;
+  // kEpiSilu only (nullable): absmax_parts[m * NB + nb] (NB = ceil(N/16))
+  // receives the max |h| of row m over the 8 outputs of packed block nb; the
+  // first phase of the two-phase per-token requantization of h.  Every
+  // (m, nb) with m < M is written by exactly one thread, so no atomics and no
+  // initialization are needed.
+  float* absmax_parts = nullptr;
   int64_t M, N, K;
   int epi;
 };
@@ -71,6 +77,14 @@ hipError_t launch_quant_rows(const void* x, int x_dtype, int64_t ldx, int64_t ro
                              const float* scale_in, int64_t scale_stride, int8_t* q,
                              int64_t ldq, int64_t ncols_out, bool packed, float* scales_out,
                              hipStream_t st);
+
+// Second phase of the two-phase per-token requantization: row r of 16-bit x
+// is quantized with scale_from_absmax of max(parts[r * nparts + i], i <
+// nparts), the maxima the first phase left; scales_out[r] receives the
+// scale.  Row-major q [rows, ldq] (K columns).
+hipError_t launch_quant_rows_parts(const void* x, int x_dtype, int64_t ldx, int64_t rows,
+                                   int64_t K, const float* parts, int64_t nparts, int8_t* q,
+                                   int64_t ldq, float* scales_out, hipStream_t st);
 
 hipError_t launch_pack_rows(const int8_t* src, int64_t rows, int64_t K, int64_t ld, int layout,
                             int8_t* dst, hipStream_t st);

@@ -48,6 +48,8 @@ EXPORTED_SYMBOLS = (
     "w8a8_linear_noalloc",
     "w8a8_linear_i8in",
     "w8a8_linear_i8in_requant",
+    "w8a8_gateup_silu_mul",
+    "w8a8_gateup_workspace_bytes",
     "w8a8_prologue_quant",
     "w8a8_requantize_i32",
     "w8a8_dequant_i32_bf16",
@@ -80,6 +82,9 @@ _SIGNATURES = {
                                 _int, _i64, _i64, _i64, _vp, _i64, _vp]),
     "w8a8_linear_i8in_requant": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
                                         _i64, _vp, _i64, _vp]),
+    "w8a8_gateup_silu_mul": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _vp, _vp, _int, _i64, _vp,
+                                    _i64, _vp, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "w8a8_gateup_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "w8a8_prologue_quant": (_int, [_vp, _int, _i64, _vp, _i64, _vp, _i64, _vp, _int, _f32, _vp,
                                    _vp, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp]),
     "w8a8_requantize_i32": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),

@@ -335,13 +335,15 @@ def calibrate_h_scales(model: nn.Module, run: Callable[[], Any]) -> dict[int, fl
             if isinstance(getattr(getattr(layer, "mlp", None), "w8a8_mlp", None), W8A8MLP)}
     if not mlps:
         raise RuntimeError("no injected W8A8 MLPs to calibrate")
-    saved = {idx: m.h_scale for idx, m in mlps.items()}
+    # The 16-bit h must reach each down projection through its module call
+    # (the hooked path): no static scale, no two-phase int8 h.
+    saved = {idx: (m.h_scale, m.two_phase) for idx, m in mlps.items()}
     for m in mlps.values():
-        m.h_scale = None
+        m.h_scale, m.two_phase = None, False
     try:
         with ActivationAbsmaxCollector({str(i): m.down for i, m in mlps.items()}) as col:
             run()
     finally:
         for idx, m in mlps.items():
-            m.h_scale = saved[idx]
+            m.h_scale, m.two_phase = saved[idx]
     return {int(name): float(scale) for name, scale in col.static_scales().items()}

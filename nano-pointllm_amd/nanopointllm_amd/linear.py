@@ -253,6 +253,20 @@ class W8A8GateUpSiluMul(nn.Module):
                               y_scale=h_scale, inter_dtype=out_dtype,
                               in_features=p.in_features)
 
+    def forward_two_phase(self, x: torch.Tensor, x_scale: torch.Tensor | None = None, *,
+                          out_dtype: torch.dtype | None = None) -> "_w.TwoPhaseOutput":
+        """``SiLU(g) * u`` and its per-token dynamic int8 quantization in two
+        phases (the epilogue keeps each row's |h|max per weight block, a
+        second kernel quantizes): ``(h, hq, scale)``, ``hq``/``scale`` exactly
+        ``dynamic_per_token_activation_qdq``'s integer part of ``h``.  ``x``
+        is 16-bit (quantized per token) or int8 with ``x_scale``."""
+        p = self.weight_q
+        if out_dtype is None and x.dtype == torch.int8:
+            out_dtype = torch.float16
+        return _w.gateup_silu_mul_two_phase(x, p.packed, p.scale, p.bias, p.out_features,
+                                            x_scale=x_scale, h_dtype=out_dtype,
+                                            in_features=p.in_features)
+
     def accumulators(self, x: torch.Tensor) -> torch.Tensor:
         """int32 accumulators in packed (interleaved) column order."""
         p = self.weight_q
@@ -265,14 +279,19 @@ class W8A8MLP(nn.Module):
 
     With ``h_scale`` (a calibrated static scale for ``h``, e.g. from
     ``static_activation_scale``) the gate/up kernel writes int8 ``h`` and the
-    down projection consumes it directly (int8-in chain); otherwise ``h`` is
-    kept in the activation dtype and quantized per token by the down
-    projection.
+    down projection consumes it directly (int8-in chain).  Otherwise ``h`` is
+    quantized per token (dynamic): by default the down projection quantizes
+    the 16-bit ``h`` itself (inside its one launch at M <= 4); with
+    ``two_phase`` the gate/up epilogue keeps each row's |h|max per weight
+    block and a second kernel writes int8 ``h`` for the int8-in down
+    projection.  Both dynamic forms give the same bits; measured on MI355X at
+    LLaMA-7B shapes the two-phase chain ties at M = 8 and is 2-3 us slower
+    per layer at M <= 4, where it adds a launch.
     """
 
     def __init__(self, gate_proj: nn.Module, up_proj: nn.Module, down_proj: nn.Module, *,
                  h_scale: float | None = None, weight_cache=None, cache_prefix: str = "",
-                 verify_source: bool = False) -> None:
+                 verify_source: bool = False, two_phase: bool = False) -> None:
         super().__init__()
         self.gate_up = W8A8GateUpSiluMul(gate_proj, up_proj, weight_cache=weight_cache,
                                          cache_key=cache_prefix + "packed_gate_up",
@@ -281,9 +300,13 @@ class W8A8MLP(nn.Module):
                                            cache_key=cache_prefix + "down_proj",
                                            verify_source=verify_source)
         self.h_scale = h_scale
+        self.two_phase = two_phase
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.h_scale is None:
+            if self.two_phase:
+                out = self.gate_up.forward_two_phase(x)
+                return self.down.forward_i8(out.hq, out.scale.reshape(-1), out_dtype=x.dtype)
             return self.down(self.gate_up(x))
         hq = self.gate_up.forward_q8(x, self.h_scale)
         s = torch.full((1,), self.h_scale, dtype=torch.float32, device=x.device)
@@ -294,6 +317,9 @@ class W8A8MLP(nn.Module):
         """The MLP on int8 rows with per-row scales (the output of the fused
         residual-add + RMSNorm + quantization prologue)."""
         if self.h_scale is None:
+            if self.two_phase:
+                out = self.gate_up.forward_two_phase(xq, x_scale, out_dtype=out_dtype)
+                return self.down.forward_i8(out.hq, out.scale.reshape(-1), out_dtype=out_dtype)
             return self.down(self.gate_up.forward_i8(xq, x_scale, out_dtype=out_dtype))
         hq = self.gate_up.forward_i8(xq, x_scale, out_dtype=out_dtype, h_scale=self.h_scale)
         s = torch.full((1,), self.h_scale, dtype=torch.float32, device=xq.device)

@@ -245,6 +245,59 @@ def linear_i8in(xq: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor,
     return y.reshape(*xq.shape[:-1], cols)
 
 
+class TwoPhaseOutput(NamedTuple):
+    h: torch.Tensor      # SiLU(g) * u, 16-bit [..., n/2]
+    hq: torch.Tensor     # int8 [..., n/2], per-token dynamic quantization of h
+    scale: torch.Tensor  # f32 [...], its per-row scales
+
+
+def gateup_silu_mul_two_phase(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
+                              bias: torch.Tensor | None, n: int, *,
+                              x_scale: torch.Tensor | None = None,
+                              h_dtype: torch.dtype | None = None,
+                              in_features: int | None = None) -> TwoPhaseOutput:
+    """Packed gate/up with SiLU*mul, then the per-token dynamic int8
+    quantization of h in two phases (``w8a8_gateup_silu_mul``): the epilogue
+    leaves each row's |h|max per 16-row weight block in the workspace, and a
+    second kernel quantizes h with ``scale_from_absmax`` of their max.  ``x``
+    is 16/32-bit (quantized per token) or int8 with per-row ``x_scale``.
+    ``hq`` and ``scale`` equal ``dynamic_per_token_activation_qdq``'s integer
+    part of ``h`` (w8a8.py:106-115)."""
+    device = _lib.require_cuda(x, w_packed, w_scale, bias, x_scale)
+    x2, ldx = _rows_view(x)
+    m, k = x2.shape
+    _check_operands(k, w_packed, w_scale, bias, n, in_features)
+    if n % 2:
+        raise ValueError("packed gate/up needs an even number of rows")
+    sx = None
+    if x.dtype == torch.int8:
+        if x_scale is None:
+            raise ValueError("int8 activations need their per-row scales")
+        sx = x_scale.detach().to(dtype=torch.float32).reshape(-1)
+        if sx.numel() == 1 and m != 1:
+            sx = sx.expand(m)
+        sx = sx.contiguous()
+        if sx.numel() != m:
+            raise ValueError("x_scale must be per-tensor or one value per row")
+    if h_dtype is None:
+        h_dtype = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else torch.float16
+    cols = n // 2
+    h = torch.empty((m, cols), dtype=h_dtype, device=device)
+    hq = torch.empty((m, cols), dtype=torch.int8, device=device)
+    hs = torch.empty((m,), dtype=torch.float32, device=device)
+    if m and n:
+        lib = _lib.load()
+        ws = torch.empty((max(int(lib.w8a8_gateup_workspace_bytes(m, n, k)), 256),),
+                         dtype=torch.uint8, device=device)
+        _lib.check(lib.w8a8_gateup_silu_mul(
+            x2.data_ptr(), _lib.dtype_code(x2.dtype), ldx, _lib.ptr(sx), w_packed.data_ptr(),
+            w_scale.data_ptr(), _lib.ptr(bias), h.data_ptr(), _lib.dtype_code(h_dtype), cols,
+            hq.data_ptr(), cols, hs.data_ptr(), m, n, k, ws.data_ptr(), ws.numel(),
+            _lib.stream_handle(device)), "w8a8_gateup_silu_mul")
+    lead = x.shape[:-1]
+    return TwoPhaseOutput(h.reshape(*lead, cols), hq.reshape(*lead, cols), hs.reshape(lead))
+
+
 class PrologueOutput(NamedTuple):
     q: torch.Tensor                  # int8 [..., K]
     scale: torch.Tensor              # f32 [...] per row (dynamic) or the static scale

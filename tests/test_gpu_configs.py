@@ -248,3 +248,31 @@ def test_mixed_step_int8_mlp_chain_full_shape(cuda):
     np.testing.assert_array_equal(y, ref32.astype(np.float16))
     dacc_gpu = w8a8.gemm_i32(hq, wd, HIDDEN, in_features=INTER).cpu().numpy()
     np.testing.assert_array_equal(dacc_gpu, dacc)
+
+
+@pytest.mark.parametrize("m", [1, 8])
+def test_decode_mlp_two_phase_full_shape(cuda, m):
+    """The decode MLP with the two-phase per-token requantization of h at the
+    LLaMA-7B shapes: gate/up 22016 x 4096 (fused decode kernel folding |h|max)
+    -> per-token int8 h -> down 4096 x 11008 on it, checked stage by stage."""
+    from nanopointllm_amd import w8a8, workloads as W
+
+    x = W.decode_activations(m, HIDDEN, seed=90 + m)
+    wgu, swgu = _device_weight("gateup", cuda)
+    note(f"decode MLP two-phase m={m}")
+    out = w8a8.gateup_silu_mul_two_phase(x.to(cuda), wgu, swgu, None, 2 * INTER,
+                                         in_features=HIDDEN)
+    h = out.h.cpu().numpy()
+    qgu, sgu = _weights("gateup")
+    xq, sx = O.dynamic_per_token_quant(x.float().numpy())
+    ulps = _ulps16(h, O.gateup_silu_mul_from_acc(O.int32_matmul_f64(xq, qgu), sx, sgu))
+    assert ulps.max() <= 2 and np.mean(ulps == 0) > 0.999
+    eq, es = O.dynamic_per_token_quant(h.astype(np.float32))
+    np.testing.assert_array_equal(out.hq.cpu().numpy(), eq)
+    np.testing.assert_array_equal(out.scale.cpu().numpy(), es[:, 0])
+    qd, sd = _weights("down")
+    wd, swd = _device_weight("down", cuda)
+    y = w8a8.linear_i8in(out.hq, out.scale, wd, swd, None, HIDDEN, out_dtype=torch.float16,
+                         in_features=INTER).cpu().numpy()
+    ref32, _ = O.linear_from_quantized(eq, es, qd, sd)
+    np.testing.assert_array_equal(y, ref32.astype(np.float16))
