@@ -203,6 +203,32 @@ int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w
                         int64_t n, int64_t k, float* x_scale_out, hipStream_t stream);
 
 /*
+ * LightweightRMSNorm (lightweight_runner.py:239-257) in front of a W8A8
+ * linear with per-token dynamic quantization of the normalized rows: the W8A8
+ * form of the reference's fused RMSNorm + packed QKV decode projection
+ * (_rmsnorm_packed_qkv_kernel, paged_attention.py:163-234, used by
+ * _rmsnorm_staged_packed_qkv_decode, :283-305).
+ *   x [m, ldx] F16/BF16; residual (nullable, same dtype): x <- x + residual,
+ *   written to residual_out (residual_norm); norm_weight [k] of x's dtype:
+ *   y = w * dtype(x / sqrt(mean(x^2) + eps)); x_out (nullable) receives y;
+ *   then w8a8_linear on y (epilogues I32 / DEQUANT / SILU_MUL / SILU_MUL_Q8 /
+ *   DEQUANT_BF16_EXACT), x_scale_out (nullable) its per-row scales.
+ * Decode rows only (1 <= m <= 16, k <= 32768).  Shapes of the fused decode
+ * route with m <= 8 and k <= 4096 (and enough weight per CU to cover reading
+ * x and the residual on every CU) run as one kernel and need no workspace; the
+ * others run the activation prologue (w8a8_prologue_quant) and the int8 GEMV
+ * and need w8a8_workspace_bytes(m, k).  Both routes sum the binary32 squares
+ * in the same order, so they give the same bits.
+ */
+int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* residual,
+                        int64_t ld_residual, void* residual_out, int64_t ld_residual_out,
+                        const void* norm_weight, float eps, const int8_t* w_packed,
+                        const float* w_scale, const float* bias, int epilogue, void* y,
+                        int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,
+                        int64_t n, int64_t k, float* x_scale_out, void* x_out, int64_t ld_x_out,
+                        void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
  * As w8a8_linear for already-quantized activations xq (int8 [m, ldq]) with
  * per-row scales x_scale[m]: the int8-in down projection fed by
  * W8A8_EPI_SILU_MUL_Q8 or w8a8_quant_rows (w8a8.py:118-139 with a given

@@ -433,6 +433,62 @@ int w8a8_gateup_silu_mul(const void* x, int x_dtype, int64_t ldx, const float* x
                                            ceil_div(n, kTileRows), hq, ldhq, h_scale, stream));
 }
 
+int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* residual,
+                        int64_t ld_residual, void* residual_out, int64_t ld_residual_out,
+                        const void* norm_weight, float eps, const int8_t* w_packed,
+                        const float* w_scale, const float* bias, int epilogue, void* y,
+                        int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,
+                        int64_t n, int64_t k, float* x_scale_out, void* x_out, int64_t ld_x_out,
+                        void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  if (!half_dtype(x_dtype)) return W8A8_ERR_DTYPE;
+  if (epilogue == W8A8_EPI_REQUANT) return W8A8_ERR_DTYPE;
+  if (epilogue == W8A8_EPI_DEQUANT_BF16_EXACT && bias != nullptr) return W8A8_ERR_DTYPE;
+  int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
+                        n, k);
+  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
+  if (m > 16 || k > prologue_max_k()) return W8A8_ERR_SHAPE;  // decode rows only
+  if (x == nullptr || norm_weight == nullptr) return W8A8_ERR_NULL;
+  if (residual != nullptr && residual_out == nullptr) return W8A8_ERR_NULL;
+  if (ldx < k || (residual != nullptr && (ld_residual < k || ld_residual_out < k)) ||
+      (x_out != nullptr && ld_x_out < k))
+    return W8A8_ERR_SHAPE;
+  if (!(eps >= 0.0f)) return W8A8_ERR_SHAPE;
+  const uintptr_t xs = static_cast<uintptr_t>(elem_size(x_dtype));
+  if (!aligned(x, xs) || !aligned(residual, xs) || !aligned(residual_out, xs) ||
+      !aligned(norm_weight, xs) || !aligned(x_out, xs) || !aligned(x_scale_out, 4))
+    return W8A8_ERR_ALIGN;
+  LinearOperands op = make_ops(nullptr, 0, nullptr, w_packed, w_scale, bias, epilogue, y, y_dtype,
+                               ldy, y_scale, inter_dtype, m, n, k);
+  if (k > 0 && epilogue <= W8A8_EPI_SILU_MUL &&
+      fused_norm_supported(x, x_dtype, ldx, residual, ld_residual, residual_out,
+                           ld_residual_out, norm_weight, x_out, ld_x_out, m, n, k)) {
+    // One kernel: residual add, RMSNorm, per-token quantization, GEMV, epilogue.
+    return status_of(launch_gemv_fused_norm(x, x_dtype, ldx, residual, ld_residual, residual_out,
+                                            ld_residual_out, norm_weight, eps, x_out, ld_x_out,
+                                            op, x_scale_out, stream));
+  }
+  // Otherwise the activation prologue writes int8 rows for the int8 GEMV.
+  if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
+    return W8A8_ERR_WORKSPACE;
+  if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
+  float* sx = x_scale_out != nullptr ? x_scale_out : static_cast<float*>(workspace);
+  int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
+  const int64_t kp = round_up(k, kTileK);
+  hipError_t e = launch_prologue_quant(x, x_dtype, ldx, residual, ld_residual, residual_out,
+                                       ld_residual_out, norm_weight, x_dtype, eps, nullptr,
+                                       nullptr, m, k, act, kp, sx, x_out, ld_x_out, stream);
+  if (e != hipSuccess) return status_of(e);
+  if (kp > k) {
+    // The GEMV reads whole 64-column blocks: zero the pad columns.
+    e = launch_pad_rows(act, m, k, kp, act, kp, stream);
+    if (e != hipSuccess) return status_of(e);
+  }
+  op.a = act;
+  op.lda = kp;
+  op.sx = sx;
+  return status_of(launch_gemv(op, stream));
+}
+
 int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
                         const float* w_scale, const float* bias, int epilogue, void* y,
                         int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,

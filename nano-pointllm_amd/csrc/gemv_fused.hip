@@ -66,6 +66,18 @@ struct FusedParams {
   int64_t ldy;
   float* sx_out;
   const float* sx_in;  // int8 x: its per-row scales
+  // RMSNorm prologue (NORM kernels only): x <- dtype(x + residual) when a
+  // residual is given (written to residual_out by workgroup 0), then
+  // x <- dtype(w * dtype(x / sqrt(mean(x^2) + eps))) (written to x_out, when
+  // given, by workgroup 0).
+  const void* residual;
+  int64_t ld_res;
+  void* residual_out;
+  int64_t ld_res_out;
+  const void* norm_w;
+  float eps;
+  void* x_out;
+  int64_t ld_xout;
   float* absmax_parts;  // kEpiSilu: [M][NB] per-block row |h|max (nullable)
   float out_scale;
   int M;
@@ -158,16 +170,22 @@ __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
   }
 }
 
+// NORM: the activation prologue of LightweightRMSNorm (residual add and
+// RMSNorm, lightweight_runner.py:239-257) runs on the x chunks first, as in
+// the reference's fused RMSNorm + packed QKV decode kernel
+// (paged_attention.py:163-234); M <= 8 and NCH <= 4 only.
 // NCH: 16-byte x chunks each thread holds while quantizing (sized to the
 // shape, so small shapes keep their registers for the ring).  RING: register
 // buffers of the weight stream; RING - 1 steps are in flight in the main
 // loop, kFusedPreSteps of them during the quantization.  ROWS: activation
 // rows per A fragment in LDS, 8 (M <= 8, half a fragment; the other half is
 // zero) or 16 (M <= 16, K <= 6144).
-template <int EPI, typename TX, typename TY, typename TH, int NCH, int RING, int ROWS>
+template <int EPI, typename TX, typename TY, typename TH, int NCH, int RING, int ROWS,
+          bool NORM = false>
 __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p) {
   static_assert(NCH <= kFusedMaxChunks && RING >= 2 && kFusedPreSteps < RING,
                 "fused kernel shape");
+  static_assert(!NORM || (NCH <= 4 && ROWS == kFusedMaxRows), "RMSNorm prologue shape");
   static_assert(ROWS == kFusedMaxRows || ROWS == kFusedMaxRows16, "8 or 16 rows");
   // TX = int8_t: x comes quantized, with per-row scales (no quantization).
   constexpr bool kI8 = std::is_same<TX, int8_t>::value;
@@ -179,6 +197,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       int8_t a_lds[ROWS == kFusedMaxRows ? kFusedMaxKB * 512 : kFusedMaxKB16 * 1024];
   __shared__ int32_t red[2][kFusedWaves][256];
   __shared__ uint32_t amax_w[kFusedWaves];
+  __shared__ float ss_g[NORM ? kFusedMaxRows : 1][8];  // RMSNorm: per row, 8 groups
   __shared__ float row_s[ROWS];
   __shared__ float ops_lds[kFusedMaxBlocks * 32];  // per block: 16 scales, 16 biases
 
@@ -322,7 +341,104 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       raw[i] = u32x4{0u, 0u, 0u, 0u};
     }
   }
+  // RMSNorm operands, loaded with x (before any weight load is queued).
+  [[maybe_unused]] u32x4 rraw[NORM ? NCH : 1];
+  [[maybe_unused]] u32x4 wraw[NORM ? NCH : 1];
+  if constexpr (NORM) {
+    const uint16_t* rr =
+        p.residual == nullptr
+            ? nullptr
+            : static_cast<const uint16_t*>(p.residual) + static_cast<int64_t>(row_live ? row : 0) * p.ld_res;
+    const uint16_t* wr = static_cast<const uint16_t*>(p.norm_w);
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = j0 + i * tpr;
+      const bool ok = row_live && c < nchunk && c * 8 < p.K;
+      rraw[i] = (ok && rr != nullptr) ? *reinterpret_cast<const u32x4*>(rr + static_cast<int64_t>(c) * 8)
+                                      : u32x4{0u, 0u, 0u, 0u};
+      wraw[i] = ok ? *reinterpret_cast<const u32x4*>(wr + static_cast<int64_t>(c) * 8)
+                   : u32x4{0u, 0u, 0u, 0u};
+    }
+  }
   load_ops();
+  if constexpr (NORM) {
+    // Every workgroup normalizes the same rows identically; workgroup 0
+    // writes the summed and the normalized rows out.
+    const bool writer = blockIdx.x == 0;
+    auto pack2 = [](float lo, float hi) {
+      return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<TX>(lo))) |
+             (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<TX>(hi))) << 16);
+    };
+    // The binary32 sum of squares follows the activation prologue kernel's
+    // order exactly (prologue.hip, 512 threads of one 8-element chunk each
+    // for K <= 4096): per chunk in element order, a butterfly over 64
+    // consecutive chunks, then the 8 groups of 64 in order.  Chunk c of the
+    // row is held here by thread c % TPR as its chunk c / TPR, and TPR is a
+    // multiple of 64, so lane l of a wavefront holds chunk 64 g + l of some
+    // group g and the butterfly is the same.
+    float sq[NCH];
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = j0 + i * tpr;
+      const bool ok = row_live && c < nchunk && c * 8 < p.K;
+      if (p.residual != nullptr) {
+        // summed = dtype(x + residual)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          raw[i][q] = pack2(bits_to_f32<TX>(raw[i][q] & 0xffffu) + bits_to_f32<TX>(rraw[i][q] & 0xffffu),
+                            bits_to_f32<TX>(raw[i][q] >> 16) + bits_to_f32<TX>(rraw[i][q] >> 16));
+        }
+        if (ok && writer) {
+          *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.residual_out) +
+                                    static_cast<int64_t>(row) * p.ld_res_out +
+                                    static_cast<int64_t>(c) * 8) = raw[i];
+        }
+      }
+      float ss = 0.0f;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float lo = bits_to_f32<TX>(raw[i][q] & 0xffffu);
+        const float hi = bits_to_f32<TX>(raw[i][q] >> 16);
+        ss = __fadd_rn(ss, __fmul_rn(lo, lo));
+        ss = __fadd_rn(ss, __fmul_rn(hi, hi));
+      }
+#pragma unroll
+      for (int off = 32; off > 0; off >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, off));
+      sq[i] = ss;
+    }
+    if (lane == 0 && row_live) {
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const int c = j0 + i * tpr;  // lane 0's chunk: the group's first
+        if (c < 512) ss_g[row][c >> 6] = sq[i];
+      }
+    }
+    __syncthreads();
+    // Groups past the row's chunks hold zeros in the prologue kernel: adding
+    // them changes nothing, so only the written groups are summed.
+    const int ngroups = min(8, (tpr >> 6) * NCH);
+    float tot = ss_g[row_live ? row : 0][0];
+    for (int g = 1; g < ngroups; ++g) tot = __fadd_rn(tot, ss_g[row_live ? row : 0][g]);
+    const float var = tot / static_cast<float>(p.K);
+    const float rstd = 1.0f / sqrtf(__fadd_rn(var, p.eps));
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = j0 + i * tpr;
+      const bool ok = row_live && c < nchunk && c * 8 < p.K;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const float lo = to_f32(from_f32<TX>(__fmul_rn(bits_to_f32<TX>(raw[i][q] & 0xffffu), rstd)));
+        const float hi = to_f32(from_f32<TX>(__fmul_rn(bits_to_f32<TX>(raw[i][q] >> 16), rstd)));
+        raw[i][q] = pack2(__fmul_rn(bits_to_f32<TX>(wraw[i][q] & 0xffffu), lo),
+                          __fmul_rn(bits_to_f32<TX>(wraw[i][q] >> 16), hi));
+      }
+      if (ok && writer && p.x_out != nullptr) {
+        *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.x_out) +
+                                  static_cast<int64_t>(row) * p.ld_xout +
+                                  static_cast<int64_t>(c) * 8) = raw[i];
+      }
+    }
+  }
   // |x| patterns of both halves at once (v_pk_max_u16).
   u16x2 am2 = {0, 0};
 #pragma unroll
@@ -455,6 +571,39 @@ hipError_t launch_f(const FusedParams& p, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <int EPI, typename TX, typename TY, typename TH>
+hipError_t launch_norm_f(const FusedParams& p, hipStream_t st) {
+  const int mpad = p.M <= 1 ? 1 : (p.M <= 2 ? 2 : (p.M <= 4 ? 4 : 8));
+  const int per_thread = static_cast<int>(ceil_div(static_cast<int64_t>(p.KB) * 8,
+                                                   kFusedThreads / mpad));
+  const dim3 grid(p.G), block(kFusedThreads);
+  constexpr int R8 = kFusedMaxRows;
+  if (per_thread <= 2)
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 2, 3, R8, true>), grid, block, 0, st, p);
+  else
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 4, 3, R8, true>), grid, block, 0, st, p);
+  return hipGetLastError();
+}
+
+template <typename TX>
+hipError_t dispatch_norm_f(const FusedParams& p, int epi, int y_dtype, hipStream_t st) {
+  switch (epi) {
+    case kEpiI32:
+      return launch_norm_f<kEpiI32, TX, int32_t, float>(p, st);
+    case kEpiDequant:
+      if (y_dtype == kF16) return launch_norm_f<kEpiDequant, TX, __half, float>(p, st);
+      if (y_dtype == kBF16) return launch_norm_f<kEpiDequant, TX, __hip_bfloat16, float>(p, st);
+      if (y_dtype == kF32) return launch_norm_f<kEpiDequant, TX, float, float>(p, st);
+      return hipErrorInvalidValue;
+    case kEpiSilu:
+      if (y_dtype == kF16) return launch_norm_f<kEpiSilu, TX, __half, __half>(p, st);
+      if (y_dtype == kBF16) return launch_norm_f<kEpiSilu, TX, __hip_bfloat16, __hip_bfloat16>(p, st);
+      return hipErrorInvalidValue;
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
 template <typename TX>
 hipError_t dispatch_f(const FusedParams& p, int epi, int y_dtype, int h_dtype, hipStream_t st) {
   switch (epi) {
@@ -537,6 +686,14 @@ hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const Line
   p.ldy = op.ldy;
   p.sx_out = sx_out;
   p.sx_in = nullptr;
+  p.residual = nullptr;
+  p.ld_res = 0;
+  p.residual_out = nullptr;
+  p.ld_res_out = 0;
+  p.norm_w = nullptr;
+  p.eps = 0.0f;
+  p.x_out = nullptr;
+  p.ld_xout = 0;
   p.absmax_parts = op.absmax_parts;
   p.out_scale = op.out_scale;
   p.M = static_cast<int>(op.M);
@@ -548,6 +705,72 @@ hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const Line
   if (p.NB == 0 || p.M == 0) return hipSuccess;
   if (x_dtype == kF16) return dispatch_f<__half>(p, op.epi, op.y_dtype, op.h_dtype, st);
   if (x_dtype == kBF16) return dispatch_f<__hip_bfloat16>(p, op.epi, op.y_dtype, op.h_dtype, st);
+  return hipErrorInvalidValue;
+}
+
+// The RMSNorm prologue variant (residual add + RMSNorm + quantization + GEMV
+// in one launch) takes the fused decode route's shapes with M <= 8, at most
+// four x chunks per thread (K <= 512 * mpad(M)) and K <= 4096 (the row sums
+// its squares in the activation prologue kernel's order), a norm weight of x's dtype,
+// 16-byte aligned rows for every 16-bit operand, and, with a residual, 2 more
+// bytes of weights per CU and activation element (every CU reads x and the
+// residual).
+bool fused_norm_supported(const void* x, int x_dtype, int64_t ldx, const void* residual,
+                          int64_t ld_res, const void* residual_out, int64_t ld_res_out,
+                          const void* norm_w, const void* x_out, int64_t ld_xout, int64_t M,
+                          int64_t N, int64_t K) {
+  // K <= 4096: the prologue kernel's one-chunk-per-thread summation order.
+  if (M > kFusedMaxRows || K > 4096 || !fused_gemv_supported(x, x_dtype, ldx, M, N, K))
+    return false;
+  const int64_t mpad = M <= 1 ? 1 : (M <= 2 ? 2 : (M <= 4 ? 4 : 8));
+  if (ceil_div(ceil_div(K, kTileK) * 8, kFusedThreads / mpad) > 4) return false;
+  auto a16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15u) == 0; };
+  if (norm_w == nullptr || !a16(norm_w)) return false;
+  if (x_out != nullptr && (!a16(x_out) || ld_xout % 8 != 0)) return false;
+  if (residual != nullptr) {
+    if (!a16(residual) || !a16(residual_out) || ld_res % 8 != 0 || ld_res_out % 8 != 0)
+      return false;
+    const int64_t nb = ceil_div(N, kTileRows);
+    const int64_t g = nb < cu_count() ? nb : cu_count();
+    const int64_t weight_bytes_per_cu = ceil_div(nb, g) * kTileRows * ceil_div(K, kTileK) * kTileK;
+    if (weight_bytes_per_cu < 6 * M * K) return false;
+  }
+  return true;
+}
+
+hipError_t launch_gemv_fused_norm(const void* x, int x_dtype, int64_t ldx, const void* residual,
+                                  int64_t ld_res, void* residual_out, int64_t ld_res_out,
+                                  const void* norm_w, float eps, void* x_out, int64_t ld_xout,
+                                  const LinearOperands& op, float* sx_out, hipStream_t st) {
+  FusedParams p;
+  p.x = x;
+  p.ldx = ldx;
+  p.w = reinterpret_cast<const i32x4*>(op.w);
+  p.sw = op.sw;
+  p.bias = op.bias;
+  p.y = op.y;
+  p.ldy = op.ldy;
+  p.sx_out = sx_out;
+  p.sx_in = nullptr;
+  p.absmax_parts = op.absmax_parts;
+  p.residual = residual;
+  p.ld_res = ld_res;
+  p.residual_out = residual_out;
+  p.ld_res_out = ld_res_out;
+  p.norm_w = norm_w;
+  p.eps = eps;
+  p.x_out = x_out;
+  p.ld_xout = ld_xout;
+  p.out_scale = op.out_scale;
+  p.M = static_cast<int>(op.M);
+  p.N = static_cast<int>(op.N);
+  p.K = static_cast<int>(op.K);
+  p.KB = static_cast<int>(ceil_div(op.K, kTileK));
+  p.NB = static_cast<int>(ceil_div(op.N, kTileRows));
+  p.G = static_cast<int>(p.NB < cu_count() ? p.NB : cu_count());
+  if (p.NB == 0 || p.M == 0) return hipSuccess;
+  if (x_dtype == kF16) return dispatch_norm_f<__half>(p, op.epi, op.y_dtype, st);
+  if (x_dtype == kBF16) return dispatch_norm_f<__hip_bfloat16>(p, op.epi, op.y_dtype, st);
   return hipErrorInvalidValue;
 }
 
@@ -581,6 +804,14 @@ hipError_t launch_gemv_fused_i8(const LinearOperands& op, hipStream_t st) {
   p.ldy = op.ldy;
   p.sx_out = nullptr;
   p.sx_in = op.sx;
+  p.residual = nullptr;
+  p.ld_res = 0;
+  p.residual_out = nullptr;
+  p.ld_res_out = 0;
+  p.norm_w = nullptr;
+  p.eps = 0.0f;
+  p.x_out = nullptr;
+  p.ld_xout = 0;
   p.absmax_parts = op.absmax_parts;
   p.out_scale = op.out_scale;
   p.M = static_cast<int>(op.M);

@@ -127,5 +127,16 @@ bool fused_gemv_i8_supported(int64_t M, int64_t N, int64_t K, int64_t lda, int e
 hipError_t launch_gemv_fused_i8(const LinearOperands& op, hipStream_t st);
 hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const LinearOperands& op,
                              float* sx_out, hipStream_t st);
+// The fused decode linear with LightweightRMSNorm's residual add and RMSNorm
+// (norm_w of x's dtype) in front of the quantization; residual_out and x_out
+// (nullable) receive the summed and normalized rows.  Decode shapes only.
+bool fused_norm_supported(const void* x, int x_dtype, int64_t ldx, const void* residual,
+                          int64_t ld_res, const void* residual_out, int64_t ld_res_out,
+                          const void* norm_w, const void* x_out, int64_t ld_xout, int64_t M,
+                          int64_t N, int64_t K);
+hipError_t launch_gemv_fused_norm(const void* x, int x_dtype, int64_t ldx, const void* residual,
+                                  int64_t ld_res, void* residual_out, int64_t ld_res_out,
+                                  const void* norm_w, float eps, void* x_out, int64_t ld_xout,
+                                  const LinearOperands& op, float* sx_out, hipStream_t st);
 
 }  // namespace w8a8

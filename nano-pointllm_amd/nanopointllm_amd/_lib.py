@@ -46,6 +46,7 @@ EXPORTED_SYMBOLS = (
     "w8a8_gemm_i32",
     "w8a8_linear",
     "w8a8_linear_noalloc",
+    "w8a8_rmsnorm_linear",
     "w8a8_linear_i8in",
     "w8a8_linear_i8in_requant",
     "w8a8_gateup_silu_mul",
@@ -78,6 +79,9 @@ _SIGNATURES = {
                            _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
     "w8a8_linear_noalloc": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _int, _vp, _int, _i64, _f32,
                                    _int, _i64, _i64, _i64, _vp, _vp]),
+    "w8a8_rmsnorm_linear": (_int, [_vp, _int, _i64, _vp, _i64, _vp, _i64, _vp, _f32, _vp, _vp,
+                                   _vp, _int, _vp, _int, _i64, _f32, _int, _i64, _i64, _i64,
+                                   _vp, _vp, _i64, _vp, _i64, _vp]),
     "w8a8_linear_i8in": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _int, _vp, _int, _i64, _f32,
                                 _int, _i64, _i64, _i64, _vp, _i64, _vp]),
     "w8a8_linear_i8in_requant": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,

@@ -133,14 +133,14 @@ def gateup_silu_mul(hidden_states: torch.Tensor, gate_up: W8A8GateUpSiluMul) -> 
 def rmsnorm_packed_qkv_decode(hidden_states: torch.Tensor, norm: nn.Module, qkv: W8A8PackedQKV
                               ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """``_rmsnorm_staged_packed_qkv_decode`` (llama/paged_attention.py:283-305):
-    RMSNorm of ``hidden_states[0]`` fused with its per-token quantization (one
-    kernel), then the packed QKV product on the int8 rows.  Returns q, k, v
-    views like the reference."""
+    RMSNorm of ``hidden_states[0]``, its per-token quantization and the packed
+    QKV product, one kernel at decode shapes (``w8a8_rmsnorm_linear``, the W8A8
+    form of ``_rmsnorm_packed_qkv_kernel``, :163-234).  Returns q, k, v views
+    like the reference."""
     rows = hidden_states[0] if hidden_states.dim() == 3 else hidden_states
     if not rows.is_contiguous():
         rows = rows.contiguous()
-    xq, sx = W8A8RMSNormQuant(norm)(rows)
-    return qkv.project_i8(xq, sx, out_dtype=rows.dtype)
+    return qkv.project_rmsnorm(rows, norm)
 
 
 def residual_rmsnorm_mlp_decode(hidden_states: torch.Tensor, residual: torch.Tensor,
@@ -153,8 +153,7 @@ def residual_rmsnorm_mlp_decode(hidden_states: torch.Tensor, residual: torch.Ten
     three_d = hidden_states.dim() == 3
     rows = hidden_states[0] if three_d else hidden_states
     res = residual[0] if three_d else residual
-    summed, xq, sx = W8A8RMSNormQuant(norm).residual_norm(rows.contiguous(), res.contiguous())
-    out = mlp.forward_i8(xq, sx, out_dtype=rows.dtype)
+    summed, out = mlp.forward_residual_rmsnorm(rows.contiguous(), res.contiguous(), norm)
     if three_d:
         return summed.unsqueeze(0), out.unsqueeze(0)
     return summed, out

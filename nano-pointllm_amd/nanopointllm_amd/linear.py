@@ -92,6 +92,10 @@ def _interleave_halves(v: torch.Tensor) -> torch.Tensor:
     return torch.stack([v[:half], v[half:]], dim=1).reshape(-1)
 
 
+def _norm_eps(norm: nn.Module) -> float:
+    return float(getattr(norm, "variance_epsilon", getattr(norm, "eps", 1.0e-6)))
+
+
 def _linear_parts(module: nn.Module) -> tuple[torch.Tensor, torch.Tensor | None]:
     return module.weight, getattr(module, "bias", None)
 
@@ -192,6 +196,17 @@ class W8A8PackedQKV(nn.Module):
         """As :meth:`project` for int8 rows with per-row scales (the output of
         the fused RMSNorm + quantization prologue)."""
         return self._split(self.linear.forward_i8(xq, x_scale, out_dtype=out_dtype))
+
+    def project_rmsnorm(self, hidden_states: torch.Tensor, norm: nn.Module
+                        ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """``_rmsnorm_staged_packed_qkv_decode`` (paged_attention.py:283-305):
+        ``norm`` (a LightweightRMSNorm / LlamaRMSNorm) applied to the rows,
+        then the packed QKV projection, one kernel at decode shapes."""
+        staged = hidden_states[0] if hidden_states.dim() == 3 else hidden_states
+        lin = self.linear.weight_q
+        out = _w.rmsnorm_linear(staged, norm.weight, _norm_eps(norm), lin.packed, lin.scale,
+                                lin.bias, lin.out_features, in_features=lin.in_features)
+        return self._split(out.y)
 
     def _split(self, qkv: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         q_size = self.num_heads * self.head_dim
@@ -311,6 +326,23 @@ class W8A8MLP(nn.Module):
         hq = self.gate_up.forward_q8(x, self.h_scale)
         s = torch.full((1,), self.h_scale, dtype=torch.float32, device=x.device)
         return self.down.forward_i8(hq, s, out_dtype=x.dtype)
+
+    def forward_residual_rmsnorm(self, hidden_states: torch.Tensor, residual: torch.Tensor,
+                                 norm: nn.Module) -> tuple[torch.Tensor, torch.Tensor]:
+        """``post_attention_layernorm.residual_norm`` then the MLP
+        (lightweight_runner.py:247-257, 320-383), with the residual add and
+        RMSNorm inside the gate/up launch at decode shapes.  Returns
+        ``(hidden_states + residual, mlp output)``."""
+        p = self.gate_up.weight_q
+        epi = _lib.EPI_SILU_MUL if self.h_scale is None else _lib.EPI_SILU_MUL_Q8
+        first = _w.rmsnorm_linear(hidden_states, norm.weight, _norm_eps(norm), p.packed, p.scale,
+                                  p.bias, p.out_features, residual=residual, epilogue=epi,
+                                  y_scale=0.0 if self.h_scale is None else self.h_scale,
+                                  in_features=p.in_features)
+        if self.h_scale is None:
+            return first.residual, self.down(first.y)
+        s = torch.full((1,), self.h_scale, dtype=torch.float32, device=hidden_states.device)
+        return first.residual, self.down.forward_i8(first.y, s, out_dtype=hidden_states.dtype)
 
     def forward_i8(self, xq: torch.Tensor, x_scale: torch.Tensor, *,
                    out_dtype: torch.dtype = torch.float16) -> torch.Tensor:

@@ -70,6 +70,8 @@ class W8A8LlamaLayer(nn.Module):
                 or not isinstance(w8a8_mlp, W8A8MLP):
             raise ValueError(f"layer {layer_index} has no W8A8 modules; run inject_w8a8 first")
         self.layer_index = layer_index
+        self.input_norm = hf_layer.input_layernorm
+        self.post_attention_norm = hf_layer.post_attention_layernorm
         self.input_layernorm = W8A8RMSNormQuant(hf_layer.input_layernorm)
         self.post_attention_layernorm = W8A8RMSNormQuant(hf_layer.post_attention_layernorm)
         self.qkv = qkv
@@ -80,12 +82,14 @@ class W8A8LlamaLayer(nn.Module):
     @torch.no_grad()
     def forward(self, hidden_states: torch.Tensor, attention_state: Any = None) -> torch.Tensor:
         rows = _rows(hidden_states)
-        xq, sx = self.input_layernorm(rows)
-        q, k, v = self.qkv.project_i8(xq, sx, out_dtype=rows.dtype)
+        # RMSNorm -> packed QKV and residual add + RMSNorm -> gate/up each run
+        # as one launch at decode shapes (w8a8_rmsnorm_linear).
+        q, k, v = self.qkv.project_rmsnorm(rows, self.input_norm)
         context = self.attention_core(q, k, v, self.layer_index, attention_state)
         attn_out = self.o_proj(context)
-        residual, xq, sx = self.post_attention_layernorm.residual_norm(attn_out, rows)
-        out = residual + self.mlp.forward_i8(xq, sx, out_dtype=rows.dtype)
+        residual, mlp_out = self.mlp.forward_residual_rmsnorm(attn_out, rows,
+                                                              self.post_attention_norm)
+        out = residual + mlp_out
         return out.unsqueeze(0) if hidden_states.dim() == 3 else out
 
 

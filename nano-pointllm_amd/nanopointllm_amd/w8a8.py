@@ -366,6 +366,75 @@ def prologue_quant(x: torch.Tensor, *, norm_weight: torch.Tensor | None = None,
         None if rows is None else rows.reshape(*lead, k))
 
 
+class NormLinearOutput(NamedTuple):
+    y: torch.Tensor                  # the linear's output
+    residual: torch.Tensor | None    # hidden + residual, when a residual was given
+    rows: torch.Tensor | None        # the normalized rows, when asked for
+
+
+def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
+                   w_packed: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None,
+                   n: int, *, residual: torch.Tensor | None = None,
+                   epilogue: int = _lib.EPI_DEQUANT, out_dtype: torch.dtype | None = None,
+                   y_scale: float = 0.0, return_rows: bool = False,
+                   in_features: int | None = None) -> NormLinearOutput:
+    """``LightweightRMSNorm`` (lightweight_runner.py:239-257, with the
+    residual add of ``residual_norm`` when ``residual`` is given) in front of a
+    W8A8 linear with per-token dynamic quantization of the normalized rows:
+    the W8A8 form of the reference's fused RMSNorm + packed QKV decode
+    projection (paged_attention.py:163-234, 283-305).  Decode rows (up to 16)
+    with a norm weight of x's dtype run through ``w8a8_rmsnorm_linear`` (one
+    kernel at decode shapes); other cases run the activation prologue and the
+    int8-in linear."""
+    device = _lib.require_cuda(x, norm_weight, w_packed, w_scale, bias, residual)
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("the activation prologue takes float16 / bfloat16 rows")
+    x2, ldx = _rows_view(x)
+    m, k = x2.shape
+    _check_operands(k, w_packed, w_scale, bias, n, in_features)
+    w = norm_weight.detach().reshape(-1)
+    if w.numel() != k:
+        raise ValueError("RMSNorm weight must have one value per hidden channel")
+    if out_dtype is None:
+        out_dtype = _default_out_dtype(epilogue, x.dtype)
+    if m > 16 or w.dtype not in (x.dtype,):
+        # Prefill rows, or a weight of another dtype: prologue + int8 linear.
+        pro = prologue_quant(x, norm_weight=norm_weight, eps=eps, residual=residual,
+                             return_rows=return_rows)
+        y = linear_i8in(pro.q, pro.scale.reshape(-1), w_packed, w_scale, bias, n,
+                        epilogue=epilogue, out_dtype=out_dtype, y_scale=y_scale,
+                        inter_dtype=x.dtype, in_features=in_features)
+        return NormLinearOutput(y, pro.residual, pro.rows)
+    w = w.contiguous()
+    res2 = res_out = None
+    ld_res = 0
+    if residual is not None:
+        if residual.shape != x.shape or residual.dtype != x.dtype:
+            raise ValueError("residual must match the hidden states' shape and dtype")
+        res2, ld_res = _rows_view(residual)
+        res_out = torch.empty((m, k), dtype=x.dtype, device=device)
+    rows = torch.empty((m, k), dtype=x.dtype, device=device) if return_rows else None
+    cols = _out_cols(epilogue, n)
+    y = torch.empty((m, cols), dtype=out_dtype, device=device)
+    if m and n:
+        lib = _lib.load()
+        args = [x2.data_ptr(), _lib.dtype_code(x.dtype), ldx, _lib.ptr(res2), ld_res,
+                _lib.ptr(res_out), k, w.data_ptr(), float(eps), w_packed.data_ptr(),
+                w_scale.data_ptr(), _lib.ptr(bias), epilogue, y.data_ptr(),
+                _lib.dtype_code(out_dtype), cols, float(y_scale), _lib.dtype_code(x.dtype), m, n,
+                k, None, _lib.ptr(rows), k]
+        stream = _lib.stream_handle(device)
+        rc = lib.w8a8_rmsnorm_linear(*args, None, 0, stream)
+        if rc == _lib.ERR_WORKSPACE:
+            ws = _workspace(m, k, device)
+            rc = lib.w8a8_rmsnorm_linear(*args, ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, "w8a8_rmsnorm_linear")
+    lead = x.shape[:-1]
+    return NormLinearOutput(y.reshape(*lead, cols),
+                            None if res_out is None else res_out.reshape(x.shape),
+                            None if rows is None else rows.reshape(x.shape))
+
+
 def rmsnorm_quant(hidden_states: torch.Tensor, norm_weight: torch.Tensor, eps: float, *,
                   residual: torch.Tensor | None = None):
     """``LightweightRMSNorm`` (lightweight_runner.py:239-257) fused with the

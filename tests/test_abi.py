@@ -120,6 +120,36 @@ def test_integer_epilogue_arguments_rejected_without_launch():
     assert lib.w8a8_dequant_i32_bf16(None, 16, None, None, None, 16, 0, 16, None) == _lib.OK
 
 
+def test_rmsnorm_linear_arguments_rejected_without_launch():
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+
+    def call(*, x=fake, x_dtype=_lib.F16, residual=None, residual_out=None, norm=fake,
+             eps=1e-6, epi=_lib.EPI_DEQUANT, bias=None, m=1, n=16, k=64, ldx=64, x_out=None):
+        return lib.w8a8_rmsnorm_linear(x, x_dtype, ldx, residual, k, residual_out, k, norm, eps,
+                                       fake, fake, bias, epi, fake, _lib.F16, n, 0.0, _lib.F16,
+                                       m, n, k, None, x_out, k, None, 0, None)
+
+    # decode rows only
+    assert call(m=17) == _lib.ERR_SHAPE
+    # 16-bit rows only, and no integer requant epilogue
+    assert call(x_dtype=_lib.F32) == _lib.ERR_DTYPE
+    assert call(epi=_lib.EPI_REQUANT) == _lib.ERR_DTYPE
+    # the RMSNorm weight, and residual_out with a residual, are required
+    assert call(norm=None) == _lib.ERR_NULL
+    assert call(residual=fake) == _lib.ERR_NULL
+    assert call(x=None) == _lib.ERR_NULL
+    # leading dimension, epsilon
+    assert call(ldx=32) == _lib.ERR_SHAPE
+    assert call(eps=-1.0) == _lib.ERR_SHAPE
+    assert call(eps=float("nan")) == _lib.ERR_SHAPE
+    # misaligned 16-bit operands
+    assert call(norm=ctypes.c_void_p(0x1001)) == _lib.ERR_ALIGN
+    assert call(x_out=ctypes.c_void_p(0x1003)) == _lib.ERR_ALIGN
+    # empty problems are valid no-ops
+    assert call(x=None, norm=None, m=0) == _lib.OK
+
+
 def test_status_errors_map_to_python_exceptions():
     with pytest.raises(ValueError, match="workspace"):
         _lib.check(_lib.ERR_WORKSPACE, "w8a8_linear")
