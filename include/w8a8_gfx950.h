@@ -213,12 +213,14 @@ int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w
  *   y = w * dtype(x / sqrt(mean(x^2) + eps)); x_out (nullable) receives y;
  *   then w8a8_linear on y (epilogues I32 / DEQUANT / SILU_MUL / SILU_MUL_Q8 /
  *   DEQUANT_BF16_EXACT), x_scale_out (nullable) its per-row scales.
- * Decode rows only (1 <= m <= 16, k <= 32768).  Shapes of the fused decode
- * route with m <= 8 and k <= 4096 (and enough weight per CU to cover reading
- * x and the residual on every CU) run as one kernel and need no workspace; the
- * others run the activation prologue (w8a8_prologue_quant) and the int8 GEMV
- * and need w8a8_workspace_bytes(m, k).  Both routes sum the binary32 squares
- * in the same order, so they give the same bits.
+ * Any m, k <= 32768.  Decode shapes of the fused decode route with m <= 8
+ * and k <= 4096 (and enough weight per CU to cover reading x and the
+ * residual on every CU) run as one kernel and need no workspace; the others
+ * run the activation prologue (w8a8_prologue_quant), which writes the int8
+ * rows straight into the layout the product reads (row-major for the GEMV,
+ * the packed tiles for the GEMM: no packing pass), then the product, and
+ * need w8a8_workspace_bytes(m, k).  Every route sums the binary32 squares in
+ * the same order, so a row gets the same bits whatever batch it is in.
  */
 int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* residual,
                         int64_t ld_residual, void* residual_out, int64_t ld_residual_out,

@@ -446,7 +446,7 @@ int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* res
   int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
                         n, k);
   if (rc != W8A8_OK || m == 0 || n == 0) return rc;
-  if (m > 16 || k > prologue_max_k()) return W8A8_ERR_SHAPE;  // decode rows only
+  if (k > prologue_max_k()) return W8A8_ERR_SHAPE;
   if (x == nullptr || norm_weight == nullptr) return W8A8_ERR_NULL;
   if (residual != nullptr && residual_out == nullptr) return W8A8_ERR_NULL;
   if (ldx < k || (residual != nullptr && (ld_residual < k || ld_residual_out < k)) ||
@@ -467,18 +467,20 @@ int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* res
                                             ld_residual_out, norm_weight, eps, x_out, ld_x_out,
                                             op, x_scale_out, stream));
   }
-  // Otherwise the activation prologue writes int8 rows for the int8 GEMV.
+  // Otherwise the activation prologue writes the int8 rows the product
+  // reads: row-major for the GEMV, the packed tiles for the GEMM.
   if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
     return W8A8_ERR_WORKSPACE;
   if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
   float* sx = x_scale_out != nullptr ? x_scale_out : static_cast<float*>(workspace);
   int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
   const int64_t kp = round_up(k, kTileK);
+  const bool gemv = use_gemv(m, n);
   hipError_t e = launch_prologue_quant(x, x_dtype, ldx, residual, ld_residual, residual_out,
                                        ld_residual_out, norm_weight, x_dtype, eps, nullptr,
-                                       nullptr, m, k, act, kp, sx, x_out, ld_x_out, stream);
+                                       nullptr, m, k, act, kp, sx, x_out, ld_x_out, stream, !gemv);
   if (e != hipSuccess) return status_of(e);
-  if (kp > k) {
+  if (gemv && kp > k) {
     // The GEMV reads whole 64-column blocks: zero the pad columns.
     e = launch_pad_rows(act, m, k, kp, act, kp, stream);
     if (e != hipSuccess) return status_of(e);
@@ -486,7 +488,7 @@ int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* res
   op.a = act;
   op.lda = kp;
   op.sx = sx;
-  return status_of(launch_gemv(op, stream));
+  return status_of(gemv ? launch_gemv(op, stream) : launch_gemm(op, stream));
 }
 
 int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,

@@ -47,6 +47,10 @@ struct PrologueParams {
   float* scales_out;
   void* x_out;  // TY [M, ld_xout] or null
   int64_t ld_xout;
+  // 0: q is row-major [M, ldq].  Otherwise q is the packed 16x64 tiles of
+  // the GEMM with KB k-blocks; the grid then covers ceil(M/16)*16 rows and
+  // every row writes all KB*64 columns (zeros past K and in the pad rows).
+  int64_t KB;
 };
 
 __device__ inline bool aligned16(const void* p) {
@@ -86,6 +90,16 @@ __global__ __launch_bounds__(kProThreads) void prologue_quant_kernel(ProloguePar
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t K = p.K;
+  if (p.KB > 0 && row >= p.M) {
+    // Pad row of a packed tile: zeros.
+#pragma unroll
+    for (int c = 0; c < REG; ++c) {
+      const int64_t k0 = (tid + static_cast<int64_t>(c) * kProThreads) * 8;
+      if (k0 < p.KB * kTileK)
+        *reinterpret_cast<u32x2*>(p.q + packed_offset(row, k0, p.KB)) = u32x2{0u, 0u};
+    }
+    return;
+  }
   const TX* xr = static_cast<const TX*>(p.x) + row * p.ldx;
 
   float v[REG][8];
@@ -161,6 +175,28 @@ __global__ __launch_bounds__(kProThreads) void prologue_quant_kernel(ProloguePar
   const bool fast = sizeof(TY) == 2 && __half2float(__float2half_rn(s)) == s;
   if (tid == 0 && p.scales_out != nullptr) p.scales_out[row] = s;
 
+  if (p.KB > 0) {
+    // Packed tiles: an aligned 8-element chunk is 8 contiguous bytes of one
+    // 16-byte lane slot; columns from K to KB*64 are zeros.
+#pragma unroll
+    for (int c = 0; c < REG; ++c) {
+      const int64_t k0 = (tid + static_cast<int64_t>(c) * kProThreads) * 8;
+      if (k0 >= p.KB * kTileK) continue;
+      int32_t qi[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        qi[j] = k0 + j < K ? (fast ? quant1_h(v[c][j], s, r) : quant1(v[c][j], s)) : 0;
+      *reinterpret_cast<u32x2*>(p.q + packed_offset(row, k0, p.KB)) =
+          u32x2{pack4_i8(qi[0], qi[1], qi[2], qi[3]), pack4_i8(qi[4], qi[5], qi[6], qi[7])};
+      if (p.x_out != nullptr && k0 < K) {
+        TY* xo = static_cast<TY*>(p.x_out) + row * p.ld_xout + k0;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          if (k0 + j < K) xo[j] = from_f32<TY>(v[c][j]);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int c = 0; c < REG; ++c) {
     const int64_t k0 = (tid + static_cast<int64_t>(c) * kProThreads) * 8;
@@ -180,7 +216,8 @@ __global__ __launch_bounds__(kProThreads) void prologue_quant_kernel(ProloguePar
 template <typename TX, typename TW>
 hipError_t launch_reg(const PrologueParams& p, hipStream_t st) {
   const int64_t per_pass = static_cast<int64_t>(kProThreads) * 8;
-  const dim3 grid(static_cast<unsigned>(p.M)), block(kProThreads);
+  const int64_t rows = p.KB > 0 ? ceil_div(p.M, kTileRows) * kTileRows : p.M;
+  const dim3 grid(static_cast<unsigned>(rows)), block(kProThreads);
   if (p.K <= per_pass)
     hipLaunchKernelGGL((prologue_quant_kernel<TX, TW, 1>), grid, block, 0, st, p);
   else if (p.K <= 2 * per_pass)
@@ -203,10 +240,10 @@ hipError_t launch_prologue_quant(const void* x, int x_dtype, int64_t ldx, const 
                                  const void* norm_weight, int w_dtype, float eps,
                                  const void* smooth, const float* static_scale, int64_t M,
                                  int64_t K, int8_t* q, int64_t ldq, float* scales_out,
-                                 void* x_out, int64_t ld_xout, hipStream_t st) {
+                                 void* x_out, int64_t ld_xout, hipStream_t st, bool packed) {
   PrologueParams p{x,          ldx, residual, ld_res, residual_out, ld_res_out, norm_weight,
                    eps,        smooth, static_scale, M, K, q, ldq, scales_out, x_out,
-                   ld_xout};
+                   ld_xout,    packed ? ceil_div(K, kTileK) : 0};
   if (M == 0 || K == 0) return hipSuccess;
   const bool w32 = norm_weight != nullptr && w_dtype == kF32;
   if (x_dtype == kF16)

@@ -48,16 +48,19 @@ struct LinearOperands {
 // residual add (written to residual_out), RMSNorm with a weight of x's dtype
 // or F32 (w_dtype), division by a per-channel smooth scale of x's dtype, then
 // int8 quantization with a per-row dynamic or one static scale.  Row-major
-// q [M, ldq] (K columns), scales_out [M] (nullable), x_out [M, ld_xout]
-// (nullable) receives the rows before quantization (x's dtype, or F32 with
-// an F32 RMSNorm weight).  K <= prologue_max_k().
+// q [M, ldq] (K columns), or with `packed` the GEMM's 16x64 tiles
+// (ceil(M/16)*16 rows x ceil(K/64)*64 columns, zero padded; ldq unused),
+// scales_out [M] (nullable), x_out [M, ld_xout] (nullable) receives the rows
+// before quantization (x's dtype, or F32 with an F32 RMSNorm weight).
+// K <= prologue_max_k().
 int64_t prologue_max_k();
 hipError_t launch_prologue_quant(const void* x, int x_dtype, int64_t ldx, const void* residual,
                                  int64_t ld_res, void* residual_out, int64_t ld_res_out,
                                  const void* norm_weight, int w_dtype, float eps,
                                  const void* smooth, const float* static_scale, int64_t M,
                                  int64_t K, int8_t* q, int64_t ldq, float* scales_out,
-                                 void* x_out, int64_t ld_xout, hipStream_t st);
+                                 void* x_out, int64_t ld_xout, hipStream_t st,
+                                 bool packed = false);
 
 // Elementwise epilogues over caller int32 accumulators acc[m, ld_acc]:
 // requant1 per element with per-column multiplier / shift / bias (nullable)

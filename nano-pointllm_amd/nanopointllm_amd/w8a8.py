@@ -382,10 +382,11 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     residual add of ``residual_norm`` when ``residual`` is given) in front of a
     W8A8 linear with per-token dynamic quantization of the normalized rows:
     the W8A8 form of the reference's fused RMSNorm + packed QKV decode
-    projection (paged_attention.py:163-234, 283-305).  Decode rows (up to 16)
-    with a norm weight of x's dtype run through ``w8a8_rmsnorm_linear`` (one
-    kernel at decode shapes); other cases run the activation prologue and the
-    int8-in linear."""
+    projection (paged_attention.py:163-234, 283-305).  A norm weight of x's
+    dtype runs through ``w8a8_rmsnorm_linear`` (one kernel at decode shapes;
+    otherwise the prologue writes the int8 rows in the product's own layout);
+    a binary32 norm weight runs the activation prologue and the int8-in
+    linear."""
     device = _lib.require_cuda(x, norm_weight, w_packed, w_scale, bias, residual)
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("the activation prologue takes float16 / bfloat16 rows")
@@ -397,8 +398,8 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
         raise ValueError("RMSNorm weight must have one value per hidden channel")
     if out_dtype is None:
         out_dtype = _default_out_dtype(epilogue, x.dtype)
-    if m > 16 or w.dtype not in (x.dtype,):
-        # Prefill rows, or a weight of another dtype: prologue + int8 linear.
+    if w.dtype != x.dtype:
+        # A binary32 weight promotes the normalized rows: prologue + int8 linear.
         pro = prologue_quant(x, norm_weight=norm_weight, eps=eps, residual=residual,
                              return_rows=return_rows)
         y = linear_i8in(pro.q, pro.scale.reshape(-1), w_packed, w_scale, bias, n,

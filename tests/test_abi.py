@@ -130,8 +130,8 @@ def test_rmsnorm_linear_arguments_rejected_without_launch():
                                        fake, fake, bias, epi, fake, _lib.F16, n, 0.0, _lib.F16,
                                        m, n, k, None, x_out, k, None, 0, None)
 
-    # decode rows only
-    assert call(m=17) == _lib.ERR_SHAPE
+    # rows of at most 32768 channels (the prologue holds a row in registers)
+    assert call(k=32832, ldx=32832) == _lib.ERR_SHAPE
     # 16-bit rows only, and no integer requant epilogue
     assert call(x_dtype=_lib.F32) == _lib.ERR_DTYPE
     assert call(epi=_lib.EPI_REQUANT) == _lib.ERR_DTYPE

@@ -7,9 +7,11 @@ w8a8.py:106-115, and the per-output linear, w8a8.py:118-139; the W8A8 form of
 Bars:
 * at decode shapes (m <= 8, k <= 4096, enough weight per CU) the call needs
   no workspace: it is the one fused kernel;
-* the fused kernel and the activation prologue + int8 GEMV give the same bits
-  (outputs, summed residual, normalized rows, per-row scales), so a row's
-  result does not depend on the batch it runs in;
+* every route (the fused kernel; the prologue writing the GEMV's rows or the
+  GEMM's packed tiles, then the product) gives the same bits as the
+  activation prologue + the int8-in linear (outputs, summed residual,
+  normalized rows, per-row scales), so a row's result does not depend on the
+  batch it runs in;
 * the residual add is bit-exact against the oracle; the normalized rows are
   bit-exact where the binary32 sum of squares is exact in any order, and on
   general inputs > 99.9 % bit-equal: torch's CPU ``mean`` sums in another
@@ -130,6 +132,10 @@ CASES = [
     ("qkv-12rows", "qkv", 12, "f16", True, False),
     ("qkv-16rows", "qkv", 16, "bf16", False, False),
     ("small-res", "small", 8, "f16", True, False),   # too little weight per CU
+    # prefill rows: the prologue writes the GEMV's rows or the GEMM's tiles
+    ("small-gemv-40", "small", 40, "f16", True, False),
+    ("qkv-gemm-96", "qkv", 96, "f16", False, False),
+    ("gateup-gemm-567", "gateup", 567, "bf16", True, False),
 ]
 
 
