@@ -65,7 +65,42 @@ def parse_args():
                          "560 rows of int8 activations, 4 layers x 5 repetitions, after the "
                          "counter-calibration copy (the region rocprofv3 --pmc runs of the "
                          "GEMM measure)")
+    ap.add_argument("--profile-proj", choices=["qkv", "o", "gateup", "down"],
+                    help="only one projection's W8A8 linear (16-bit x, per-token quantization "
+                         "inside the call, as in the decode step) at --profile-m rows, 4 layers "
+                         "x 5 repetitions, after the counter-calibration copy (the region "
+                         "rocprofv3 runs of that projection measure)")
+    ap.add_argument("--profile-m", type=int, default=8)
     return ap.parse_args()
+
+
+def profile_proj(device, name: str, m: int) -> dict:
+    """One projection's linear over four layers' cold weights, five times,
+    after a 256 MiB copy that calibrates the traffic counters."""
+    import torch
+
+    from nanopointllm_amd import _lib, w8a8, workloads as W
+
+    src = torch.empty(CALIBRATION_COPY_BYTES, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    del src, dst
+    layers = [Layer(i, 8, device) for i in range(4)]
+    spec = {p.name: p for p in W.PROJECTIONS}[name]
+    x = (W.decode_activations(m, spec.k, seed=11) if m <= 16 else
+         W.prefill_activations(m, spec.k, seed=11)).to(device)
+    epi = _lib.EPI_SILU_MUL if spec.silu else _lib.EPI_DEQUANT
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        for layer in layers:
+            p = layer.weights[name]
+            w8a8.linear_dynamic(x, p.packed, p.scale, None, p.out_features, epilogue=epi)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / 20
+    return {"projection": name, "m": m, "n": spec.n, "k": spec.k, "launches": 20,
+            "host_ms_per_call": round(ms, 4),
+            "algorithmic_bytes": W.algorithmic_bytes(m, spec.n, spec.k, silu=spec.silu)}
 
 
 def profile_gemm(device) -> dict:
@@ -573,6 +608,10 @@ def main() -> int:
     device = torch.device("cuda:0")
     if args.profile_gemm:
         print(json.dumps({"profile_gemm": profile_gemm(device)}))
+        return 0
+    if args.profile_proj:
+        print(json.dumps({"profile_proj": profile_proj(device, args.profile_proj,
+                                                        args.profile_m)}))
         return 0
     m = args.m
     log(f"building {args.layers} layers of packed W8A8 weights (M={m})")
