@@ -24,7 +24,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from .linear import W8A8GateUpSiluMul, W8A8Linear, W8A8MLP, W8A8PackedQKV, W8A8RMSNormQuant
+from .linear import W8A8GateUpSiluMul, W8A8Linear, W8A8MLP, W8A8PackedQKV
 
 _ATTN_LINEARS = ("q_proj", "k_proj", "v_proj", "o_proj")
 _MLP_LINEARS = ("gate_proj", "up_proj", "down_proj")

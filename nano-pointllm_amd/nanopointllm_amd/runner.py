@@ -5,21 +5,26 @@
 Per layer, every projection runs on int8 and every norm feeding one is fused
 with the quantization of its output:
 
-1. ``input_layernorm`` + per-token int8 quantization - one kernel
-   (``_rmsnorm_staged_packed_qkv_decode``, llama/paged_attention.py:283-305);
-2. packed ``[Wq; Wk; Wv]`` projection on the int8 rows, for decode and for
-   prefill alike (the reference's prefill runs three projections,
-   paged_attention.py:1349-1352; one packed product is the same numbers,
-   since quantization is per token and per output row);
+1-2. ``input_layernorm``, per-token int8 quantization and the packed
+   ``[Wq; Wk; Wv]`` projection (``w8a8_rmsnorm_linear``): one kernel at decode
+   shapes, the W8A8 form of ``_rmsnorm_packed_qkv_kernel`` /
+   ``_rmsnorm_staged_packed_qkv_decode`` (llama/paged_attention.py:163-234,
+   283-305); for prefill the norm kernel writes the int8 rows in the GEMM's
+   tiles.  The packed product serves prefill too (the reference's prefill
+   runs three projections, paged_attention.py:1349-1352; one packed product
+   is the same numbers, since quantization is per token and per output row).
+   Every route sums the norm's squares in the same order, so a row's result
+   does not depend on the batch it runs in;
 3. the attention core, supplied by the caller (rotary, KV cache and the
    attention kernel are not part of the W8A8 path):
    ``core(q [T, H, D], k [T, Hkv, D], v [T, Hkv, D], layer_index, state)``
    returns the context ``[T, H * D]``;
 4. ``o_proj`` as a W8A8 linear (paged_attention.py:1376, 1488);
-5. residual add + ``post_attention_layernorm`` + int8 quantization - one
-   kernel (``residual_norm``, lightweight_runner.py:247-257);
-6. packed gate/up with the SiLU*mul epilogue, then down (binary16 ``h``, or
-   the int8 chain with a calibrated ``h`` scale) (lightweight_runner.py:320-383);
+5-6. residual add + ``post_attention_layernorm`` (``residual_norm``,
+   lightweight_runner.py:247-257) + int8 quantization + packed gate/up with
+   the SiLU*mul epilogue, one kernel at decode shapes, then down (binary16
+   ``h``, or the int8 chain with a calibrated ``h`` scale)
+   (lightweight_runner.py:320-383);
 7. the final residual add in the activation dtype, as the reference does.
 
 The stack is inference-only (no autograd).  Nothing on it synchronizes with
@@ -36,7 +41,7 @@ import torch
 import torch.nn as nn
 
 from .inject import inject_w8a8
-from .linear import W8A8Linear, W8A8MLP, W8A8PackedQKV, W8A8RMSNormQuant
+from .linear import W8A8Linear, W8A8MLP, W8A8PackedQKV
 
 AttentionCore = Callable[[torch.Tensor, torch.Tensor, torch.Tensor, int, Any], torch.Tensor]
 
@@ -70,10 +75,8 @@ class W8A8LlamaLayer(nn.Module):
                 or not isinstance(w8a8_mlp, W8A8MLP):
             raise ValueError(f"layer {layer_index} has no W8A8 modules; run inject_w8a8 first")
         self.layer_index = layer_index
-        self.input_norm = hf_layer.input_layernorm
-        self.post_attention_norm = hf_layer.post_attention_layernorm
-        self.input_layernorm = W8A8RMSNormQuant(hf_layer.input_layernorm)
-        self.post_attention_layernorm = W8A8RMSNormQuant(hf_layer.post_attention_layernorm)
+        self.input_layernorm = hf_layer.input_layernorm
+        self.post_attention_layernorm = hf_layer.post_attention_layernorm
         self.qkv = qkv
         self.o_proj = attn.o_proj
         self.mlp = w8a8_mlp
@@ -84,11 +87,11 @@ class W8A8LlamaLayer(nn.Module):
         rows = _rows(hidden_states)
         # RMSNorm -> packed QKV and residual add + RMSNorm -> gate/up each run
         # as one launch at decode shapes (w8a8_rmsnorm_linear).
-        q, k, v = self.qkv.project_rmsnorm(rows, self.input_norm)
+        q, k, v = self.qkv.project_rmsnorm(rows, self.input_layernorm)
         context = self.attention_core(q, k, v, self.layer_index, attention_state)
         attn_out = self.o_proj(context)
         residual, mlp_out = self.mlp.forward_residual_rmsnorm(attn_out, rows,
-                                                              self.post_attention_norm)
+                                                              self.post_attention_layernorm)
         out = residual + mlp_out
         return out.unsqueeze(0) if hidden_states.dim() == 3 else out
 
