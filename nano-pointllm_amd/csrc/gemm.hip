@@ -372,7 +372,12 @@ hipError_t launch_cfg(GemmParams p, hipStream_t st) {
 //     8% faster than 430 tiles of 128x256;
 //   * else (several rounds) 128x256, except just past one round of those
 //     (1 to 1.25 tiles per slot), where the few tiles of the second round cost
-//     more than the wider tile saves and 128x128 is kept.
+//     more than the wider tile saves and 128x128 is kept, and except from two
+//     full rounds of 256x256 tiles (one per CU, 16 waves of 64x64, 2-stage
+//     ring of two k-blocks) when those add no row padding: the square tile
+//     reads a third fewer operand bytes per MAC (2048 x 22016 x 4096: 1.94
+//     against 1.71 POPS; 8192^3: 2.03 against 1.99), while at 1.3-1.5 rounds
+//     it gains nothing.
 template <int EPI, typename TY, typename TH>
 hipError_t launch_t(const GemmParams& p, hipStream_t st) {
   switch (gemm_tile_choice(p.MB, p.NB, cu_count())) {
@@ -388,6 +393,8 @@ hipError_t launch_t(const GemmParams& p, hipStream_t st) {
       return launch_cfg<4, 2, 2, 6, 3, 2, 1, EPI, TY, TH>(p, st);
     case kGemmW224:
       return launch_cfg<4, 2, 2, 7, 3, 2, 1, EPI, TY, TH>(p, st);
+    case kGemmW256Sq:
+      return launch_cfg<4, 4, 4, 4, 2, 1, 2, EPI, TY, TH>(p, st);
     default:
       return launch_cfg<2, 4, 4, 4, 3, 2, 1, EPI, TY, TH>(p, st);
   }
@@ -410,7 +417,10 @@ int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus) {
   if (tiles_m * ceil_div(NB, 14) <= slots) return kGemmW224;
   const int64_t wide_tiles = tiles_m * ceil_div(NB, 16);
   const bool short_second_round = wide_tiles > slots && wide_tiles * 100 < slots * 125;
-  return short_second_round ? kGemmBig : kGemmW256;
+  if (short_second_round) return kGemmBig;
+  const int64_t sq_tiles_m = ceil_div(MB, 16);
+  if (sq_tiles_m * ceil_div(NB, 16) >= 2 * cus && sq_tiles_m * 2 == tiles_m) return kGemmW256Sq;
+  return kGemmW256;
 }
 
 hipError_t launch_gemm(const LinearOperands& op, hipStream_t st) {

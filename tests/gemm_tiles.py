@@ -5,7 +5,8 @@ the MI355X's 256 CUs.  The query makes no device call, so it also answers on a
 machine without a GPU."""
 from __future__ import annotations
 
-CONFIG_NAMES = ("tiny-deep", "small-deep", "big-deep", "big", "w192", "w224", "w256")
+CONFIG_NAMES = ("tiny-deep", "small-deep", "big-deep", "big", "w192", "w224", "w256",
+                "w256sq")
 
 
 def gemm_config(m: int, n: int, cus: int = 256) -> str:

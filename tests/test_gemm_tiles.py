@@ -17,7 +17,9 @@ QKV, O, GATEUP, DOWN = 12288, 4096, 22016, 4096
     (560, O, "big-deep"), (768, O, "big-deep"), (1024, O, "big-deep"),
     (560, GATEUP, "w224"), (768, GATEUP, "big"), (1024, GATEUP, "w256"),
     (64, QKV, "tiny-deep"), (128, O, "tiny-deep"), (256, O, "small-deep"),
-    (256, QKV, "big-deep"), (384, GATEUP, "w192"), (8192, 8192, "w256"),
+    (256, QKV, "big-deep"), (384, GATEUP, "w192"), (8192, 8192, "w256sq"),
+    (2048, GATEUP, "w256sq"), (2040, GATEUP, "w256sq"),
+    (2050, GATEUP, "w256"), (4096, O, "w256"), (4096, QKV, "w256sq"),
 ])
 def test_llama7b_prefill_tiles(m, n, cfg):
     assert gemm_config(m, n) == cfg
@@ -25,7 +27,8 @@ def test_llama7b_prefill_tiles(m, n, cfg):
 
 def test_every_config_fits_one_round_or_is_the_widest():
     """Within one round of 512 workgroup slots the rule never leaves a config
-    that would also fit with more tiles; past it, only 128x256 or 128x128."""
+    that would also fit with more tiles; past it, only 128x256, 128x128, or
+    256x256 from two full rounds of those with no extra row padding."""
     for m in range(65, 4097, 37):
         for n in (4096, 11008, 12288, 22016, 32000):
             cfg = gemm_config(m, n)
@@ -37,6 +40,9 @@ def test_every_config_fits_one_round_or_is_the_widest():
                 assert tiles[cfg] <= 512 and tiles["big"] > 512
             if cfg == "w224":
                 assert tiles["w192"] > 512
+            if cfg == "w256sq":
+                assert tiles["w256"] > 512 and -(-mb // 16) * -(-nb // 16) >= 512
+                assert 2 * -(-mb // 16) == tm
 
 
 def test_query_rejects_empty_or_oversized_problems():

@@ -1,7 +1,8 @@
 """Prefill GEMM shapes past one round of 128x128 tiles, which select the
 128-row tiles of 192, 224 or 256 columns (8 waves each, three LDS stages):
 the widest whose tiles still fit in one round of workgroup slots, else (for
-several rounds) 128x256.
+several rounds) 128x256, or from two full rounds of them the 256x256 tile
+(16 waves, one workgroup per CU).
 
 Bars as for every GEMM path: int32 accumulators bit-exact against the
 oracle's integer product; binary16 / bfloat16 / binary32 dequant outputs
@@ -50,7 +51,8 @@ def _case(m, n, k, seed):
 
 
 @pytest.mark.parametrize("m,n,k,cfg", [(1000, 14005, 200, "w224"), (2100, 6200, 320, "w224"),
-                                        (1100, 20000, 576, "w256"), (1000, 12000, 330, "w192")])
+                                        (1100, 20000, 576, "w256"), (1000, 12000, 330, "w192"),
+                                        (2040, 16380, 200, "w256sq")])
 def test_wide_tile_int32_and_dequant(cuda, m, n, k, cfg):
     from nanopointllm_amd import w8a8
 
@@ -74,7 +76,7 @@ def test_wide_tile_int32_and_dequant(cuda, m, n, k, cfg):
 
 
 @pytest.mark.parametrize("m,inter,k,cfg", [(1000, 7002, 320, "w224"), (1100, 10000, 200, "w256"),
-                                            (1000, 6000, 330, "w192")])
+                                            (1000, 6000, 330, "w192"), (2040, 8190, 136, "w256sq")])
 def test_wide_tile_silu_mul_and_int8_chain(cuda, m, inter, k, cfg):
     from nanopointllm_amd import _lib, w8a8
 
@@ -99,7 +101,8 @@ def test_wide_tile_silu_mul_and_int8_chain(cuda, m, inter, k, cfg):
     np.testing.assert_array_equal(hq.cpu().numpy(), eq)
 
 
-@pytest.mark.parametrize("m,n,k,cfg", [(1000, 14005, 200, "w224"), (1100, 20000, 200, "w256")])
+@pytest.mark.parametrize("m,n,k,cfg", [(1000, 14005, 200, "w224"), (1100, 20000, 200, "w256"),
+                                        (2048, 16384, 264, "w256sq")])
 def test_requant1_epilogue_at_a_wide_shape(cuda, m, n, k, cfg):
     """The integer requant epilogue on the wide tiles: equal to
     requantize_int32 of the exact product (that kernel is pinned to the
