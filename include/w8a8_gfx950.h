@@ -222,6 +222,9 @@ int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w
  * the packed tiles for the GEMM: no packing pass), then the product, and
  * need w8a8_workspace_bytes(m, k).  Every route sums the binary32 squares in
  * the same order, so a row gets the same bits whatever batch it is in.
+ * residual_out may be residual (an in-place residual update) and x_out may
+ * overlap x: such calls take the prologue route.  y must not overlap any
+ * input.
  */
 int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* residual,
                         int64_t ld_residual, void* residual_out, int64_t ld_residual_out,

@@ -48,6 +48,17 @@ inline bool aligned(const void* p, uintptr_t a) {
 
 inline int64_t round_up(int64_t v, int64_t m) { return ceil_div(v, m) * m; }
 
+// Whether the byte ranges of two [rows, ld] matrices of `elem`-byte values
+// (k used columns) overlap; a null pointer overlaps nothing.
+inline bool overlap(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t rows,
+                    int64_t k, int64_t elem) {
+  if (a == nullptr || b == nullptr || rows == 0 || k == 0) return false;
+  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+  const uintptr_t a1 = a0 + static_cast<uintptr_t>(((rows - 1) * lda + k) * elem);
+  const uintptr_t b1 = b0 + static_cast<uintptr_t>(((rows - 1) * ldb + k) * elem);
+  return a0 < b1 && b0 < a1;
+}
+
 inline bool float_dtype(int d) { return d == kF32 || d == kF16 || d == kBF16; }
 inline bool half_dtype(int d) { return d == kF16 || d == kBF16; }
 
@@ -459,7 +470,17 @@ int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* res
     return W8A8_ERR_ALIGN;
   LinearOperands op = make_ops(nullptr, 0, nullptr, w_packed, w_scale, bias, epilogue, y, y_dtype,
                                ldy, y_scale, inter_dtype, m, n, k);
-  if (k > 0 && epilogue <= W8A8_EPI_SILU_MUL &&
+  // The one-kernel route has workgroup 0 write the summed and normalized rows
+  // while the others still read x and the residual, so it is taken only when
+  // those outputs overlap neither input (an in-place residual update runs the
+  // prologue, which reads each row before writing it).
+  const int64_t es = elem_size(x_dtype);
+  const bool in_place =
+      overlap(residual_out, ld_residual_out, x, ldx, m, k, es) ||
+      overlap(residual_out, ld_residual_out, residual, ld_residual, m, k, es) ||
+      overlap(x_out, ld_x_out, x, ldx, m, k, es) ||
+      overlap(x_out, ld_x_out, residual, ld_residual, m, k, es);
+  if (k > 0 && epilogue <= W8A8_EPI_SILU_MUL && !in_place &&
       fused_norm_supported(x, x_dtype, ldx, residual, ld_residual, residual_out,
                            ld_residual_out, norm_weight, x_out, ld_x_out, m, n, k)) {
     // One kernel: residual add, RMSNorm, per-token quantization, GEMV, epilogue.

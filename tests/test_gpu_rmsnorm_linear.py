@@ -293,3 +293,38 @@ def test_fused_rmsnorm_graph_replays(cuda):
         torch.cuda.synchronize()
         assert torch.equal(out.y, eager.y) and torch.equal(out.residual, eager.residual), rep
         _ = (x.float() * 2).sum().item()   # eager work between replays
+
+
+def test_in_place_residual_update_takes_the_prologue_route(cuda):
+    """residual_out == residual (and x_out == x) at a shape the one-kernel
+    route would take: the call asks for a workspace (the prologue route, which
+    reads each row before writing it) and gives the non-aliased call's bits."""
+    from nanopointllm_amd import _lib
+
+    wp, sw, bias = _device("gateup", cuda)
+    n, m = 2 * INTER, 8
+    x = _rows(m, HIDDEN, "f16", seed=21).to(cuda)
+    r = _rows(m, HIDDEN, "f16", seed=22, scale=0.3).to(cuda)
+    nw = _norm_weight(HIDDEN, "f16", seed=23).to(cuda)
+    y_ref = torch.empty(m, INTER, dtype=torch.float16, device=cuda)
+    res_ref = torch.empty_like(x)
+    rows_ref = torch.empty_like(x)
+    note("rmsnorm_linear in place")
+    assert _c_call(x, r, nw, wp, sw, bias, n, _lib.EPI_SILU_MUL, y_ref, res_out=res_ref,
+                   rows=rows_ref) == _lib.OK
+    ws = torch.empty(_lib.load().w8a8_workspace_bytes(m, HIDDEN), dtype=torch.uint8,
+                     device=cuda)
+    r2, y2 = r.clone(), torch.empty_like(y_ref)
+    assert _c_call(x, r2, nw, wp, sw, bias, n, _lib.EPI_SILU_MUL, y2,
+                   res_out=r2) == _lib.ERR_WORKSPACE
+    assert _c_call(x, r2, nw, wp, sw, bias, n, _lib.EPI_SILU_MUL, y2, res_out=r2,
+                   workspace=ws) == _lib.OK
+    assert torch.equal(y2, y_ref) and torch.equal(r2, res_ref)
+    x3, y3 = x.clone(), torch.empty_like(y_ref)
+    assert _c_call(x3, None, nw, wp, sw, bias, n, _lib.EPI_SILU_MUL, y3,
+                   rows=x3) == _lib.ERR_WORKSPACE
+    assert _c_call(x3, None, nw, wp, sw, bias, n, _lib.EPI_SILU_MUL, y3, rows=x3,
+                   workspace=ws) == _lib.OK
+    y4, rows4 = torch.empty_like(y_ref), torch.empty_like(x)
+    assert _c_call(x, None, nw, wp, sw, bias, n, _lib.EPI_SILU_MUL, y4, rows=rows4) == _lib.OK
+    assert torch.equal(y3, y4) and torch.equal(x3, rows4)
