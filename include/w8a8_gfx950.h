@@ -20,6 +20,10 @@
  *    nanopointllm/compression/w8a8.py:14-30).
  *  - Packed weights use the 16x64 tile layout described at
  *    w8a8_pack_rows; their size is w8a8_packed_bytes(rows, k).
+ *  - Outputs (y, scales, workspace) must not overlap the inputs, as for
+ *    F.linear, which always writes a new tensor: the product kernels read x
+ *    in every workgroup while others already write y.  The one exception,
+ *    residual_out and x_out of w8a8_rmsnorm_linear, is stated there.
  */
 #ifndef W8A8_GFX950_H
 #define W8A8_GFX950_H
