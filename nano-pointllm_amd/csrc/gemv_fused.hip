@@ -427,10 +427,11 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       const bool ok = row_live && c < nchunk && c * 8 < p.K;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const float lo = to_f32(from_f32<TX>(__fmul_rn(bits_to_f32<TX>(raw[i][q] & 0xffffu), rstd)));
-        const float hi = to_f32(from_f32<TX>(__fmul_rn(bits_to_f32<TX>(raw[i][q] >> 16), rstd)));
-        raw[i][q] = pack2(__fmul_rn(bits_to_f32<TX>(wraw[i][q] & 0xffffu), lo),
-                          __fmul_rn(bits_to_f32<TX>(wraw[i][q] >> 16), hi));
+        // mul_keep_sign: a -0 element stays -0, as in the prologue kernel.
+        const float lo = to_f32(from_f32<TX>(mul_keep_sign(bits_to_f32<TX>(raw[i][q] & 0xffffu), rstd)));
+        const float hi = to_f32(from_f32<TX>(mul_keep_sign(bits_to_f32<TX>(raw[i][q] >> 16), rstd)));
+        raw[i][q] = pack2(mul_keep_sign(bits_to_f32<TX>(wraw[i][q] & 0xffffu), lo),
+                          mul_keep_sign(bits_to_f32<TX>(wraw[i][q] >> 16), hi));
       }
       if (ok && writer && p.x_out != nullptr) {
         *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.x_out) +

@@ -140,8 +140,9 @@ __global__ __launch_bounds__(kProThreads) void prologue_quant_kernel(ProloguePar
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         if (k0 + j < K) {
-          const float xn = round_to<TX>(__fmul_rn(v[c][j], rr));
-          v[c][j] = round_to<TY>(__fmul_rn(to_f32(w[k0 + j]), xn));
+          // mul_keep_sign: a -0 element stays -0 through both roundings.
+          const float xn = round_to<TX>(mul_keep_sign(v[c][j], rr));
+          v[c][j] = round_to<TY>(mul_keep_sign(to_f32(w[k0 + j]), xn));
         }
       }
     }

@@ -195,6 +195,16 @@ __device__ inline float dequant1(int32_t acc, float sx, float sw, const float* _
   return v;
 }
 
+// a * b in binary32, kept a value of its own.  A binary32 multiply feeding a
+// 16-bit conversion is otherwise merged by the backend into a mixed-precision
+// FMA with a +0 addend, which turns a -0 product into +0; the empty asm (no
+// instruction) stops the merge, so the conversion sees the exact product.
+__device__ inline float mul_keep_sign(float a, float b) {
+  float p = __fmul_rn(a, b);
+  asm volatile("" : "+v"(p));
+  return p;
+}
+
 // SiLU(g) * u on binary16 operands (llama/lightweight_runner.py:358):
 // SiLU in binary32, rounded to the activation type, then the product
 // (exact in binary32) rounded once.
@@ -202,7 +212,8 @@ template <typename T>
 __device__ inline float silu_mul(float g, float u) {
   float s = g / (1.0f + expf(-g));
   s = to_f32(from_f32<T>(s));
-  return __fmul_rn(s, u);
+  // SiLU of a very negative gate is -0, and so is its product.
+  return mul_keep_sign(s, u);
 }
 
 // INT32 -> A8 requantization of the hardware model

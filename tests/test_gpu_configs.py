@@ -13,8 +13,9 @@ LightweightMLP packed branch, lightweight_runner.py:344-379):
 * int32 accumulators bit-exact against an exact float64 matmul of the
   oracle's int8 operands;
 * fp16 dequant outputs bit-equal to the oracle's binary32 result rounded once;
-* SiLU*mul within 2 binary16 ulps and > 99.9 % bit-equal to the oracle (GPU
-  and numpy ``exp`` may differ by an ulp);
+* SiLU*mul equal to the oracle's, which applies the reference's ``act_fn``
+  (torch's CPU ``F.silu``) to the oracle's gate and up; the device SiLU is
+  bit-identical to torch's on every finite binary16 and bfloat16 gate;
 * int8 ``h`` bit-exact against the oracle's quantization of the GPU's own
   ``h``, and the down projection bit-exact on that int8 ``h``.
 Each fp16 comparison also reports max-abs and max-relative error against the
@@ -96,6 +97,77 @@ def _c_linear(x: torch.Tensor, wp: torch.Tensor, sw: torch.Tensor, n: int, epilo
                            _lib.stream_handle(x.device))
 
 
+def _torch_silu_mul(g16: np.ndarray, u16: np.ndarray) -> np.ndarray:
+    """``act_fn(gate) * up`` of the reference (lightweight_runner.py:358) with
+    torch's own CPU ``F.silu`` on binary16 tensors."""
+    g, u = torch.from_numpy(g16), torch.from_numpy(u16)
+    return (torch.nn.functional.silu(g) * u).numpy()
+
+
+@pytest.mark.parametrize("m", [8, 560])
+def test_silu_mul_against_torch_cpu_silu(cuda, m):
+    """The SiLU*mul epilogue (fused decode kernel at M = 8, GEMM at M = 560)
+    against torch's CPU ``F.silu`` applied to the kernel's own dequantized
+    gate and up (the same product with the dequant epilogue): bit-equal,
+    the sign of zero included."""
+    from nanopointllm_amd import _lib, workloads as W
+
+    n = 2 * INTER
+    x = (W.decode_activations(m, HIDDEN, seed=60) if m <= 16 else
+         W.prefill_activations(m, HIDDEN, seed=60)).to(cuda)
+    wp, sw = _device_weight("gateup", cuda)
+    ws = torch.empty(max(16, _lib.load().w8a8_workspace_bytes(m, HIDDEN)), dtype=torch.uint8,
+                     device=cuda)
+    gu = torch.empty(m, n, dtype=torch.float16, device=cuda)
+    h = torch.empty(m, INTER, dtype=torch.float16, device=cuda)
+    note(f"SiLU*mul vs torch CPU silu m={m}")
+    assert _c_linear(x, wp, sw, n, _lib.EPI_DEQUANT, gu, workspace=ws) == 0
+    assert _c_linear(x, wp, sw, n, _lib.EPI_SILU_MUL, h, workspace=ws) == 0
+    g16 = gu.cpu().numpy()
+    ref = _torch_silu_mul(np.ascontiguousarray(g16[:, 0::2]), np.ascontiguousarray(g16[:, 1::2]))
+    got = h.cpu().numpy()
+    ulps = _ulps16(got, ref)
+    note(f"  vs torch: exact {np.mean(ulps == 0):.6f}, max ulp {ulps.max()}")
+    np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("m", [1, 80])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_silu_mul_every_16bit_gate_against_torch(cuda, m, dtype):
+    """Every finite binary16 gate value through the SiLU*mul epilogue (GEMV
+    at M = 1, GEMM at M = 80): int8 rows [1, 0, ...] with x_scale 1 and a
+    weight row [1, 0, ...] with scale t dequantize to exactly t, so gate row
+    2j carries value t_j and up row 2j + 1 carries u_j (1, then random).
+    Compared with torch's CPU ``F.silu(g) * u`` on the same binary16 values
+    (the reference's ``act_fn(gate) * up``, lightweight_runner.py:358)."""
+    from nanopointllm_amd import _lib, w8a8
+
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(dtype)
+    tt = bits[torch.isfinite(bits.float())]
+    t = tt.float().numpy()
+    inter, k = t.size, 64
+    w = torch.zeros(2 * inter, k, dtype=torch.int8)
+    w[:, 0] = 1
+    wp = w8a8.pack_rows(w.to(cuda))
+    xq = torch.zeros(m, k, dtype=torch.int8)
+    xq[:, 0] = 1
+    sx = torch.ones(m, dtype=torch.float32, device=cuda)
+    rng = np.random.default_rng(7)
+    for u in (torch.ones(inter, dtype=dtype),
+              torch.from_numpy(rng.standard_normal(inter).astype(np.float32)).to(dtype)):
+        sw = np.empty(2 * inter, np.float32)
+        sw[0::2], sw[1::2] = t, u.float().numpy()
+        note(f"SiLU*mul over every {dtype} gate, m={m}")
+        h = w8a8.linear_i8in(xq.to(cuda), sx, wp, torch.from_numpy(sw).to(cuda), None,
+                             2 * inter, epilogue=_lib.EPI_SILU_MUL, out_dtype=dtype)
+        got = h.cpu()
+        assert m == 1 or bool((got == got[0]).all())
+        ref = torch.nn.functional.silu(tt) * u
+        same = (got[0].view(torch.int16) == ref.view(torch.int16))
+        note(f"  vs torch: {int((~same).sum())} of {inter} differ")
+        assert bool(same.all())
+
+
 # --------------------------------------------- the bench's dominant kernel
 @pytest.mark.parametrize("m", [1, 4, 8])
 def test_decode_gateup_fused_silu_full_shape(cuda, m):
@@ -127,7 +199,7 @@ def test_decode_gateup_fused_silu_full_shape(cuda, m):
     max_abs, max_rel = _errors(hh, ref32)
     note(f"  h: exact {np.mean(ulps == 0):.6f}, max ulp {ulps.max()}, "
          f"max_abs {max_abs:.3e}, max_rel {max_rel:.3e}")
-    assert ulps.max() <= 2 and np.mean(ulps == 0) > 0.999
+    assert ulps.max() == 0
     # int8 requant twin (EPI_SILU_MUL_Q8) with a static scale from the GPU's h.
     h_scale = float(O.static_activation_scale(np.float32(np.abs(hh.astype(np.float32)).max())))
     hq = torch.empty(m, INTER, dtype=torch.int8, device=cuda)
@@ -183,7 +255,7 @@ def test_prefill_projections(cuda, proj, m):
                             in_features=k).cpu().numpy()
     ulps = _ulps16(h, O.gateup_silu_mul_from_acc(eacc, sx, s, layout="interleave"))
     note(f"  h: exact {np.mean(ulps == 0):.6f}, max ulp {ulps.max()}")
-    assert ulps.max() <= 2 and np.mean(ulps == 0) > 0.999
+    assert ulps.max() == 0
 
 
 # ------------------------------------------------------------- config 5
@@ -229,7 +301,7 @@ def test_mixed_step_int8_mlp_chain_full_shape(cuda):
     hh = h.cpu().numpy()
     ulps = _ulps16(hh, O.gateup_silu_mul_from_acc(eacc, sx, sgu, layout="interleave"))
     note(f"  h: exact {np.mean(ulps == 0):.6f}, max ulp {ulps.max()}")
-    assert ulps.max() <= 2 and np.mean(ulps == 0) > 0.999
+    assert ulps.max() == 0
     h_scale = float(O.static_activation_scale(np.float32(np.abs(hh.astype(np.float32)).max())))
     hq = w8a8.linear_dynamic(xc, wgu, swgu, None, 2 * INTER, epilogue=_lib.EPI_SILU_MUL_Q8,
                              y_scale=h_scale, in_features=HIDDEN)
@@ -266,7 +338,7 @@ def test_decode_mlp_two_phase_full_shape(cuda, m):
     qgu, sgu = _weights("gateup")
     xq, sx = O.dynamic_per_token_quant(x.float().numpy())
     ulps = _ulps16(h, O.gateup_silu_mul_from_acc(O.int32_matmul_f64(xq, qgu), sx, sgu))
-    assert ulps.max() <= 2 and np.mean(ulps == 0) > 0.999
+    assert ulps.max() == 0
     eq, es = O.dynamic_per_token_quant(h.astype(np.float32))
     np.testing.assert_array_equal(out.hq.cpu().numpy(), eq)
     np.testing.assert_array_equal(out.scale.cpu().numpy(), es[:, 0])

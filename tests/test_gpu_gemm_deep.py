@@ -6,8 +6,8 @@ tile with stages of two k-blocks (128 K) and one workgroup per CU.
 
 Bars as for every GEMM path: int32 accumulators bit-exact against the
 oracle's integer product; binary16 / bfloat16 dequant outputs bit-equal to the
-oracle's dequant (w8a8.py:118-139) rounded once; SiLU*mul within two binary16
-ulps and >99.9% bit-equal, its int8 requant bit-exact against the oracle
+oracle's dequant (w8a8.py:118-139) rounded once; SiLU*mul equal to the oracle's
+(torch's ``F.silu``, the reference's ``act_fn``), its int8 requant bit-exact against the oracle
 applied to the kernel's own binary16 h; the integer requant epilogue equal to
 requantize_int32 of the exact product.  K is ragged against the stages: last
 stages with fewer k-blocks than the others, a K that is not a multiple of 64,
@@ -104,7 +104,7 @@ def test_deep_stage_silu_mul_and_int8_chain(cuda, m, inter, k):
     eh = O.gateup_silu_mul_from_acc(O.int32_matmul_f64(xq.numpy(), qp), sx, sp,
                                     layout="interleave")
     u = _ulps16(h.cpu().numpy(), eh)
-    assert u.max() <= 2 and np.mean(u == 0) > 0.999
+    assert u.max() == 0
     h_scale = float(O.static_activation_scale(float(h.float().abs().max().item())))
     hq = w8a8.linear_i8in(xd, sxt, wp, spt, None, 2 * inter, epilogue=_lib.EPI_SILU_MUL_Q8,
                           out_dtype=torch.int8, y_scale=h_scale)

@@ -7,7 +7,7 @@ several rounds) 128x256, or from two full rounds of them the 256x256 tile
 Bars as for every GEMM path: int32 accumulators bit-exact against the
 oracle's integer product; binary16 / bfloat16 / binary32 dequant outputs
 bit-equal to the oracle's dequant (w8a8.py:118-139) rounded once; SiLU*mul
-within two binary16 ulps and >99.9% bit-equal; the int8 requant of SiLU*mul
+equal to the oracle's (torch's ``F.silu``, the reference's ``act_fn``); the int8 requant of SiLU*mul
 bit-exact against the oracle applied to the kernel's own binary16 h.  Shapes
 are ragged in M, N and K (partial tiles, a partial last 16-row block, K not a
 multiple of 64).  The integer requant epilogue (requant1) takes the same
@@ -93,7 +93,7 @@ def test_wide_tile_silu_mul_and_int8_chain(cuda, m, inter, k, cfg):
     eh = O.gateup_silu_mul_from_acc(O.int32_matmul_f64(xq.numpy(), qp), sx, sp,
                                     layout="interleave")
     u = _ulps16(h.cpu().numpy(), eh)
-    assert u.max() <= 2 and np.mean(u == 0) > 0.999
+    assert u.max() == 0
     h_scale = float(O.static_activation_scale(float(h.float().abs().max().item())))
     hq = w8a8.linear_i8in(xd, sxt, wp, spt, None, 2 * inter, epilogue=_lib.EPI_SILU_MUL_Q8,
                           out_dtype=torch.int8, y_scale=h_scale)

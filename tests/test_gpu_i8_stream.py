@@ -5,8 +5,8 @@ projection of lightweight_runner.py:362-379 and the int8 MLP chain).
 
 Bars: int32 accumulators bit-exact against the oracle's integer product;
 binary16 / bfloat16 / binary32 outputs bit-equal to the oracle's dequant
-(w8a8.py:118-139) rounded once; SiLU*mul within two binary16 ulps and >99.9%
-bit-equal; the int8 requant of SiLU*mul bit-exact against the oracle applied
+(w8a8.py:118-139) rounded once; SiLU*mul equal to the oracle's (torch's
+``F.silu``, the reference's ``act_fn``); the int8 requant of SiLU*mul bit-exact against the oracle applied
 to the kernel's own binary16 h.  Covered: K just above the threshold, K at its
 maximum, K not a multiple of 64 (padded staging), strided rows, a partial last
 output block, bias, every supported epilogue, and the K <= 8192 shapes that
@@ -93,7 +93,7 @@ def test_i8_stream_silu_and_int8_chain(cuda, m):
     eacc = O.int32_matmul_f64(xq.numpy(), qp)
     eh = O.gateup_silu_mul_from_acc(eacc, sx, sp, layout="interleave")
     u = _ulps16(h.cpu().numpy(), eh)
-    assert u.max() <= 2 and np.mean(u == 0) > 0.999
+    assert u.max() == 0
     h_scale = float(O.static_activation_scale(float(h.float().abs().max().item())))
     hq = w8a8.linear_i8in(xd, sxt, wp, spt, None, 2 * inter, epilogue=_lib.EPI_SILU_MUL_Q8,
                           out_dtype=torch.int8, y_scale=h_scale)
