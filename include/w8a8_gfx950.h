@@ -254,9 +254,9 @@ int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
  * Packed gate/up with SiLU*mul and the two-phase per-token dynamic int8
  * requantization of its output h (the dynamic_per_token_activation_qdq
  * contract, w8a8.py:106-115, applied to the down projection's input of the
- * LightweightMLP packed branch, lightweight_runner.py:344-379; the survey's
- * w8a8_gateup_silu_mul, with the row absmax kept as per-block partial maxima
- * in the workspace instead of a zeroed atomic buffer).
+ * LightweightMLP packed branch, lightweight_runner.py:344-379), with each
+ * row's absmax kept as per-block partial maxima in the workspace (no atomics,
+ * nothing to zero), and h and hq not overlapping.
  *   Phase 1: h [m, ldh] (h_dtype F16/BF16, n/2 columns) = SiLU(g) * u as
  *            W8A8_EPI_SILU_MUL of w8a8_linear (x of F32/F16/BF16, quantized
  *            per token) or of w8a8_linear_i8in (x_dtype W8A8_I8 with per-row
