@@ -1,5 +1,5 @@
 """The GEMM tile rule (the library's ``w8a8_gemm_tile_config`` query) on the
-LLaMA-7B prefill shapes that the measurements in the design notes quote:
+LLaMA-7B prefill shapes whose tile choices were measured on MI355X:
 which configuration each shape takes on the MI355X's 256 CUs.  The GPU tests
 run every configuration for exactness; this pins the shape-to-configuration
 map, and the rule's invariants over a sweep of shapes."""
