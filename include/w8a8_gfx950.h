@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 3
+#define W8A8_ABI_VERSION 4
 
 typedef enum w8a8_dtype {
   W8A8_F32 = 0,
@@ -53,7 +53,8 @@ typedef enum w8a8_status {
   W8A8_ERR_ALIGN = -4,     /* pointer or leading dimension misaligned */
   W8A8_ERR_WORKSPACE = -5, /* workspace missing or too small */
   W8A8_ERR_HIP = -6,       /* kernel launch failed; see w8a8_last_hip_error */
-  W8A8_ERR_TOO_LARGE = -7  /* w8a8_linear_noalloc: more than its static scratch */
+  W8A8_ERR_TOO_LARGE = -7, /* w8a8_linear_noalloc: more than its static scratch */
+  W8A8_ERR_OVERLAP = -8    /* an output overlaps an input other than row for row */
 } w8a8_status;
 
 /* Bytes of the static device scratch of w8a8_linear_noalloc (per GPU). */
@@ -227,9 +228,10 @@ int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w
  * the packed tiles for the GEMM: no packing pass), then the product, and
  * need w8a8_workspace_bytes(m, k).  Every route sums the binary32 squares in
  * the same order, so a row gets the same bits whatever batch it is in.
- * residual_out may be residual (an in-place residual update) and x_out may
- * overlap x: such calls take the prologue route.  y must not overlap any
- * input.
+ * residual_out and x_out may each be the very rows of x or of the residual
+ * (the same pointer and leading dimension: an in-place update, which takes
+ * the prologue route); any other overlap with an input, or between the two,
+ * returns W8A8_ERR_OVERLAP before any launch.  y must not overlap any input.
  */
 int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* residual,
                         int64_t ld_residual, void* residual_out, int64_t ld_residual_out,
@@ -294,7 +296,10 @@ int64_t w8a8_gateup_workspace_bytes(int64_t m, int64_t n, int64_t k);
  *                  scales_out [m] (nullable with a static scale).
  * x_out (nullable, [m, ld_x_out], x's dtype or F32 as y) receives y.  The
  * binary32 sum of squares is summed in the kernel's order; every other step
- * is exactly rounded.  k <= 32768.
+ * is exactly rounded.  k <= 32768.  residual_out and x_out may each be the
+ * very rows of x or of the residual (same pointer, leading dimension and
+ * element size: each row is read before it is written); any other overlap
+ * with an input, or between the two, returns W8A8_ERR_OVERLAP.
  */
 int w8a8_prologue_quant(const void* x, int x_dtype, int64_t ldx, const void* residual,
                         int64_t ld_residual, void* residual_out, int64_t ld_residual_out,

@@ -50,13 +50,26 @@ inline int64_t round_up(int64_t v, int64_t m) { return ceil_div(v, m) * m; }
 
 // Whether the byte ranges of two [rows, ld] matrices of `elem`-byte values
 // (k used columns) overlap; a null pointer overlaps nothing.
-inline bool overlap(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t rows,
-                    int64_t k, int64_t elem) {
-  if (a == nullptr || b == nullptr || rows == 0 || k == 0) return false;
-  const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
-  const uintptr_t a1 = a0 + static_cast<uintptr_t>(((rows - 1) * lda + k) * elem);
-  const uintptr_t b1 = b0 + static_cast<uintptr_t>(((rows - 1) * ldb + k) * elem);
+// Whether the [rows, k] row sets at a (leading dimension lda, elements of ea
+// bytes) and b (ldb, eb) share a byte of their address ranges.
+inline bool overlap(const void* a, int64_t lda, int64_t ea, const void* b, int64_t ldb, int64_t eb,
+                    int64_t rows, int64_t k) {
+  if (a == nullptr || b == nullptr || rows <= 0 || k <= 0) return false;
+  // 128-bit ends: a huge leading dimension cannot wrap the comparison.
+  using u128 = unsigned __int128;
+  const u128 a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+  const u128 a1 = a0 + (static_cast<u128>(rows - 1) * static_cast<u128>(lda) + k) * ea;
+  const u128 b1 = b0 + (static_cast<u128>(rows - 1) * static_cast<u128>(ldb) + k) * eb;
   return a0 < b1 && b0 < a1;
+}
+
+// Whether a row-wise kernel, which reads each row of its inputs before it
+// writes that row of an output, may write output rows `out` over input rows
+// `in`: they are disjoint, or they are the very same rows (in place).
+inline bool rows_alias_ok(const void* out, int64_t ld_out, int64_t e_out, const void* in,
+                          int64_t ld_in, int64_t e_in, int64_t rows, int64_t k) {
+  if (!overlap(out, ld_out, e_out, in, ld_in, e_in, rows, k)) return true;
+  return out == in && e_out == e_in && (rows == 1 || ld_out == ld_in);
 }
 
 inline bool float_dtype(int d) { return d == kF32 || d == kF16 || d == kBF16; }
@@ -301,6 +314,8 @@ const char* w8a8_status_string(int status) {
       return "HIP kernel launch failed";
     case W8A8_ERR_TOO_LARGE:
       return "problem needs more than the static scratch of w8a8_linear_noalloc";
+    case W8A8_ERR_OVERLAP:
+      return "an output overlaps an input other than row for row";
     default:
       return "unknown status";
   }
@@ -470,16 +485,23 @@ int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* res
     return W8A8_ERR_ALIGN;
   LinearOperands op = make_ops(nullptr, 0, nullptr, w_packed, w_scale, bias, epilogue, y, y_dtype,
                                ldy, y_scale, inter_dtype, m, n, k);
-  // The one-kernel route has workgroup 0 write the summed and normalized rows
-  // while the others still read x and the residual, so it is taken only when
-  // those outputs overlap neither input (an in-place residual update runs the
-  // prologue, which reads each row before writing it).
+  // residual_out and x_out are written row by row after the row is read
+  // (the prologue), so each may be the very rows of an input; no other
+  // overlap is allowed.  The one-kernel route has workgroup 0 write them
+  // while the others still read x and the residual, so it is taken only
+  // when they overlap neither input.
   const int64_t es = elem_size(x_dtype);
-  const bool in_place =
-      overlap(residual_out, ld_residual_out, x, ldx, m, k, es) ||
-      overlap(residual_out, ld_residual_out, residual, ld_residual, m, k, es) ||
-      overlap(x_out, ld_x_out, x, ldx, m, k, es) ||
-      overlap(x_out, ld_x_out, residual, ld_residual, m, k, es);
+  const void* r_out = residual != nullptr ? residual_out : nullptr;  // written only with a residual
+  if (!rows_alias_ok(r_out, ld_residual_out, es, x, ldx, es, m, k) ||
+      !rows_alias_ok(r_out, ld_residual_out, es, residual, ld_residual, es, m, k) ||
+      !rows_alias_ok(x_out, ld_x_out, es, x, ldx, es, m, k) ||
+      !rows_alias_ok(x_out, ld_x_out, es, residual, ld_residual, es, m, k) ||
+      overlap(r_out, ld_residual_out, es, x_out, ld_x_out, es, m, k))
+    return W8A8_ERR_OVERLAP;
+  const bool in_place = overlap(r_out, ld_residual_out, es, x, ldx, es, m, k) ||
+                        overlap(r_out, ld_residual_out, es, residual, ld_residual, es, m, k) ||
+                        overlap(x_out, ld_x_out, es, x, ldx, es, m, k) ||
+                        overlap(x_out, ld_x_out, es, residual, ld_residual, es, m, k);
   if (k > 0 && epilogue <= W8A8_EPI_SILU_MUL && !in_place &&
       fused_norm_supported(x, x_dtype, ldx, residual, ld_residual, residual_out,
                            ld_residual_out, norm_weight, x_out, ld_x_out, m, n, k)) {
@@ -557,6 +579,16 @@ int w8a8_prologue_quant(const void* x, int x_dtype, int64_t ldx, const void* res
       !aligned(smooth, xs) || !aligned(norm_weight, w32 ? 4 : xs) || !aligned(static_scale, 4) ||
       !aligned(scales_out, 4) || !aligned(x_out, w32 ? 4 : xs))
     return W8A8_ERR_ALIGN;
+  // Each row is read before it is written: an output may be the very rows of
+  // an input, and must not overlap one otherwise, nor the other output.
+  const int64_t es = static_cast<int64_t>(xs), eo = w32 ? 4 : es;
+  const void* r_out = residual != nullptr ? residual_out : nullptr;  // written only with a residual
+  if (!rows_alias_ok(r_out, ld_residual_out, es, x, ldx, es, m, k) ||
+      !rows_alias_ok(r_out, ld_residual_out, es, residual, ld_residual, es, m, k) ||
+      !rows_alias_ok(x_out, ld_x_out, eo, x, ldx, es, m, k) ||
+      !rows_alias_ok(x_out, ld_x_out, eo, residual, ld_residual, es, m, k) ||
+      overlap(r_out, ld_residual_out, es, x_out, ld_x_out, eo, m, k))
+    return W8A8_ERR_OVERLAP;
   return status_of(launch_prologue_quant(x, x_dtype, ldx, residual, ld_residual, residual_out,
                                          ld_residual_out, norm_weight, norm_weight_dtype, eps,
                                          smooth, static_scale, m, k, q, ldq, scales_out, x_out,

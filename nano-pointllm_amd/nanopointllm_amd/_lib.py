@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libw8a8_gfx950.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 F32, F16, BF16, I32, I8 = 0, 1, 2, 3, 4
 EPI_I32, EPI_DEQUANT, EPI_SILU_MUL, EPI_SILU_MUL_Q8 = 0, 1, 2, 3
@@ -23,6 +23,7 @@ ROWS_AS_IS, ROWS_INTERLEAVE_HALVES = 0, 1
 OK = 0
 ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ALIGN, ERR_WORKSPACE, ERR_HIP = -1, -2, -3, -4, -5, -6
 ERR_TOO_LARGE = -7
+ERR_OVERLAP = -8
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _TORCH_TO_CODE = {

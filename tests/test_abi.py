@@ -150,6 +150,46 @@ def test_rmsnorm_linear_arguments_rejected_without_launch():
     assert call(x=None, norm=None, m=0) == _lib.OK
 
 
+def test_row_outputs_overlapping_inputs_are_rejected_without_launch():
+    """residual_out and x_out may be the very rows of an input (in place);
+    any other overlap, or the two outputs overlapping, is refused before any
+    launch (a row-wise kernel would write rows another workgroup still reads)."""
+    lib = _lib.load()
+    fake = ctypes.c_void_p(0x1000)
+    m, k = 2, 64
+    row = k * 2                          # bytes of one binary16 row
+    x, res = 0x100000, 0x200000
+
+    def rl(residual=None, residual_out=None, x_out=None, ld_x_out=k):
+        return lib.w8a8_rmsnorm_linear(ctypes.c_void_p(x), _lib.F16, k, _p(residual), k,
+                                       _p(residual_out), k, fake, 1e-6, fake, fake, None,
+                                       _lib.EPI_DEQUANT, fake, _lib.F16, 16, 0.0, _lib.F16,
+                                       m, 16, k, None, _p(x_out), ld_x_out, None, 0, None)
+
+    assert rl(x_out=x + row) == _lib.ERR_OVERLAP                # shifted by one row
+    assert rl(x_out=x, ld_x_out=2 * k) == _lib.ERR_OVERLAP      # same base, other rows
+    assert rl(residual=res, residual_out=res + 64) == _lib.ERR_OVERLAP
+    assert rl(residual=res, residual_out=x + 2) == _lib.ERR_OVERLAP
+    assert rl(residual=res, residual_out=0x300000, x_out=0x300000 + 2) == _lib.ERR_OVERLAP
+
+    def pq(residual=None, residual_out=None, x_out=None, w_dtype=_lib.F16):
+        return lib.w8a8_prologue_quant(ctypes.c_void_p(x), _lib.F16, k, _p(residual), k,
+                                       _p(residual_out), k, fake, w_dtype, 1e-6, None, None,
+                                       m, k, fake, k, fake, _p(x_out), k, None)
+
+    assert pq(x_out=x + row) == _lib.ERR_OVERLAP
+    assert pq(residual=res, residual_out=res + row) == _lib.ERR_OVERLAP
+    # binary32 normalized rows written over the binary16 input rows: twice the
+    # bytes per row, so not row for row.
+    assert pq(x_out=x, w_dtype=_lib.F32) == _lib.ERR_OVERLAP
+    assert lib.w8a8_status_string(_lib.ERR_OVERLAP) == (
+        b"an output overlaps an input other than row for row")
+
+
+def _p(addr):
+    return None if addr is None else ctypes.c_void_p(addr)
+
+
 def test_status_errors_map_to_python_exceptions():
     with pytest.raises(ValueError, match="workspace"):
         _lib.check(_lib.ERR_WORKSPACE, "w8a8_linear")
