@@ -362,10 +362,7 @@ hipError_t launch_cfg(GemmParams p, hipStream_t st) {
 //     of 32x32, a 2-stage ring of four k-blocks, 2 per CU) when those tiles
 //     fit in one round, else 128x128 with a 4-stage ring of two k-blocks,
 //     one per CU (8-14% faster on O and down at M = 560..1024, 15-20% at
-//     M = 384, with weights streamed from HBM), or 96x112 tiles (14 waves of
-//     48x16) when those still fit in one workgroup per CU and put at least a
-//     quarter more CUs to work (O and down at M = 560: 222 tiles against 160,
-//     1-3% faster).  With at most one 64x64 tile
+//     M = 384, with weights streamed from HBM).  With at most one 64x64 tile
 //     per CU, 32x32 tiles of one wave (a 3-stage ring of four k-blocks, 3 per
 //     CU by LDS) spread the work over more CUs when they fit in one round:
 //     9-13% faster on QKV at M = 64 and on O and down at M = 128;
@@ -398,8 +395,6 @@ hipError_t launch_t(const GemmParams& p, hipStream_t st) {
       return launch_cfg<4, 2, 2, 7, 3, 2, 1, EPI, TY, TH>(p, st);
     case kGemmW256Sq:
       return launch_cfg<4, 4, 4, 4, 2, 1, 2, EPI, TY, TH>(p, st);
-    case kGemm96x112:
-      return launch_cfg<2, 7, 3, 1, 4, 1, 2, EPI, TY, TH>(p, st);
     default:
       return launch_cfg<2, 4, 4, 4, 3, 2, 1, EPI, TY, TH>(p, st);
   }
@@ -416,8 +411,6 @@ int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus) {
     const int64_t small_tiles = ceil_div(MB, 4) * ceil_div(NB, 4);
     if (small_tiles <= cus && ceil_div(MB, 2) * ceil_div(NB, 2) <= 3 * cus) return kGemmTinyDeep;
     if (small_tiles <= slots) return kGemmSmallDeep;
-    const int64_t t96_tiles = ceil_div(MB, 6) * ceil_div(NB, 7);
-    if (t96_tiles <= cus && t96_tiles * 4 >= big_tiles * 5) return kGemm96x112;
     return kGemmBigDeep;
   }
   if (tiles_m * ceil_div(NB, 12) <= slots) return kGemmW192;

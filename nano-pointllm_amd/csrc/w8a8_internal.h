@@ -108,7 +108,6 @@ enum GemmTile : int {
   kGemmW224 = 5,       // 128x224, 8 waves
   kGemmW256 = 6,       // 128x256, 8 waves
   kGemmW256Sq = 7,     // 256x256, 16 waves, 2-stage ring of two k-blocks, 1 per CU
-  kGemm96x112 = 8,     // 96x112, 14 waves, 4-stage ring of two k-blocks, 1 per CU
 };
 int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus);
 

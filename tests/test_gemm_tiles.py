@@ -14,8 +14,7 @@ QKV, O, GATEUP, DOWN = 12288, 4096, 22016, 4096
 
 @pytest.mark.parametrize("m,n,cfg", [
     (560, QKV, "big"), (768, QKV, "w192"), (1024, QKV, "w192"), (2048, QKV, "w256"),
-    (560, O, "t96x112"), (768, O, "big-deep"), (1024, O, "big-deep"),
-    (520, O, "t96x112"), (600, O, "big-deep"), (480, O, "small-deep"),
+    (560, O, "big-deep"), (768, O, "big-deep"), (1024, O, "big-deep"),
     (560, GATEUP, "w224"), (768, GATEUP, "big"), (1024, GATEUP, "w256"),
     (64, QKV, "tiny-deep"), (128, O, "tiny-deep"), (256, O, "small-deep"),
     (256, QKV, "big-deep"), (384, GATEUP, "w192"), (8192, 8192, "w256sq"),
@@ -28,10 +27,8 @@ def test_llama7b_prefill_tiles(m, n, cfg):
 
 def test_every_config_fits_one_round_or_is_the_widest():
     """Within one round of 512 workgroup slots the rule never leaves a config
-    that would also fit with more tiles; one workgroup per CU takes 96x112
-    only where its tiles still fit one per CU and outnumber the 128x128 ones
-    by a quarter; past one round, only 128x256, 128x128, or 256x256 from two
-    full rounds of those with no extra row padding."""
+    that would also fit with more tiles; past it, only 128x256, 128x128, or
+    256x256 from two full rounds of those with no extra row padding."""
     for m in range(65, 4097, 37):
         for n in (4096, 11008, 12288, 22016, 32000):
             cfg = gemm_config(m, n)
@@ -43,12 +40,6 @@ def test_every_config_fits_one_round_or_is_the_widest():
                 assert tiles[cfg] <= 512 and tiles["big"] > 512
             if cfg == "w224":
                 assert tiles["w192"] > 512
-            if cfg == "t96x112":
-                t96 = -(-mb // 6) * -(-nb // 7)
-                assert tiles["big"] <= 256 and t96 <= 256 and 4 * t96 >= 5 * tiles["big"]
-            if cfg == "big-deep":
-                t96 = -(-mb // 6) * -(-nb // 7)
-                assert t96 > 256 or 4 * t96 < 5 * tiles["big"]
             if cfg == "w256sq":
                 assert tiles["w256"] > 512 and -(-mb // 16) * -(-nb // 16) >= 512
                 assert 2 * -(-mb // 16) == tm

@@ -2,9 +2,7 @@
 stages of several k-blocks: one-wave 32x32 tiles with stages of four k-blocks
 (256 K) when there is at most one 64x64 tile per CU, else the 64x64 tile with
 stages of four k-blocks when its tiles fit in two per CU, else the 128x128
-tile, or the 96x112 tile where its tiles still fit one per CU and put a
-quarter more CUs to work, with stages of two k-blocks (128 K) and one
-workgroup per CU.
+tile with stages of two k-blocks (128 K) and one workgroup per CU.
 
 Bars as for every GEMM path: int32 accumulators bit-exact against the
 oracle's integer product; binary16 / bfloat16 dequant outputs bit-equal to the
@@ -56,9 +54,9 @@ def _case(m, n, k, seed):
 # 3100 -> 49 (a last 128-K stage of one k-block), 4250 -> 67 (a last 256-K
 # stage of three), 11008 -> 172, and 70 (one 256-K stage of two).
 SHAPES = [
-    (560, 4000, 4197, "t96x112"),
-    (520, 4100, 3100, "t96x112"),
-    (560, 4096, 70, "t96x112"),
+    (560, 4000, 4197, "big-deep"),
+    (520, 4100, 3100, "big-deep"),
+    (560, 4096, 70, "big-deep"),
     (1000, 4096, 1000, "big-deep"),
     (700, 4100, 70, "big-deep"),
     (130, 12288, 3100, "big-deep"),
@@ -95,7 +93,7 @@ def test_deep_stage_silu_mul_and_int8_chain(cuda, m, inter, k):
     from nanopointllm_amd import _lib, w8a8
 
     cfg = _config(m, 2 * inter)
-    assert cfg in ("big-deep", "small-deep", "tiny-deep", "t96x112")
+    assert cfg in ("big-deep", "small-deep", "tiny-deep")
     xq, wq, sx, sw, _ = _case(m, 2 * inter, k, seed=7 + k)
     note(f"gemm {cfg} silu m={m} inter={inter} k={k}")
     wp = w8a8.pack_rows(wq.to(cuda), _lib.ROWS_INTERLEAVE_HALVES)
@@ -120,7 +118,7 @@ def test_deep_stage_silu_mul_and_int8_chain(cuda, m, inter, k):
 def test_deep_stage_requant1_epilogue(cuda, m, n, k):
     from nanopointllm_amd import integer_epilogues as E, w8a8
 
-    assert _config(m, n) in ("big-deep", "small-deep", "tiny-deep", "t96x112")
+    assert _config(m, n) in ("big-deep", "small-deep", "tiny-deep")
     xq, wq, _, sw, _ = _case(m, n, k, seed=5 + k)
     comp = [O.compile_fp16_requant_scale(0.02, float(w), 0.5) for w in sw]
     mult = np.array([c[0] for c in comp], np.uint32)
