@@ -154,8 +154,8 @@ def dequantize_int32_to_bf16(acc: torch.Tensor, activation_scale: torch.Tensor,
 
 
 def linear_i8in_requant(xq: torch.Tensor, w_packed: torch.Tensor, multiplier: torch.Tensor,
-                        right_shift: torch.Tensor, bias: torch.Tensor | None, n: int
-                        ) -> torch.Tensor:
+                        right_shift: torch.Tensor, bias: torch.Tensor | None, n: int, *,
+                        in_features: int | None = None) -> torch.Tensor:
     """Static-A8 linear with the integer requantization fused into the
     product's epilogue: int8 ``requantize_int32(xq @ wq^T, bias, multiplier,
     right_shift)``."""
@@ -164,6 +164,7 @@ def linear_i8in_requant(xq: torch.Tensor, w_packed: torch.Tensor, multiplier: to
         raise ValueError("activations must be int8")
     x2, ldq = w8a8._rows_view(xq)
     m, k = x2.shape
+    w8a8._check_operands(k, w_packed, None, None, n, in_features)
     mult = _as_i32(multiplier, n, "multiplier")
     shift = _as_i32(right_shift, n, "right_shift")
     b = _as_i32(bias, n, "bias")
@@ -207,4 +208,5 @@ class StaticA8RequantLinear(nn.Module):
 
     def forward(self, xq: torch.Tensor) -> torch.Tensor:
         return linear_i8in_requant(xq, self.packed, self.multiplier, self.right_shift,
-                                   self.bias_i32, self.out_features)
+                                   self.bias_i32, self.out_features,
+                                   in_features=self.in_features)

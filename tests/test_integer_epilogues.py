@@ -187,6 +187,13 @@ def test_linear_i8in_requant_fused(cuda, m):
     np.testing.assert_array_equal(ym, _requant_ref(acc, np.zeros(n, np.int32),
                                                    mm.cpu().numpy().view(np.uint32),
                                                    ss.cpu().numpy()))
+    # An activation of another K is refused before any launch.
+    with pytest.raises(ValueError, match="shapes do not match"):
+        mod(xq[:, : k - 64].contiguous().to(cuda))
+    with pytest.raises(ValueError, match="shapes do not match"):
+        E.linear_i8in_requant(torch.zeros(m, k + 64, dtype=torch.int8, device=cuda), wp,
+                              _u32_as_i32(mult).to(cuda), torch.from_numpy(shift).to(cuda),
+                              None, n)
 
 
 @pytest.mark.gpu
