@@ -3,8 +3,8 @@
 TEST INFRASTRUCTURE ONLY.  Only ``tests/`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this module: it is the CPU path that the benchmark
 times next to the GPU (the reference's own golden runs these torch calls on
-the CPU), and a second checker.  The product path under ``nano-pointllm_amd/``
-never imports it.
+the CPU), and a second oracle to compare results with.  The product path
+under ``nano-pointllm_amd/`` never imports it.
 
 It follows the reference's torch code step by step, on CPU tensors:
 

@@ -1,10 +1,10 @@
 """CPU oracle for the W8A8 quantized linear path (numpy restatement).
 
 TEST INFRASTRUCTURE ONLY.  Only ``tests/``, ``__graft_entry__.smoke()`` and
-the ``cpu_baseline`` leg of ``bench.py`` may import this module, and only as
-the checker (or, for ``cpu_baseline``, as the timed CPU restatement).  The
-product path under ``nano-pointllm_amd/`` never imports it and never falls
-back to it.
+the ``cpu_baseline`` leg of ``bench.py`` may import this module, and only to
+check results against (or, for ``cpu_baseline``, as the timed CPU
+restatement).  The product path under ``nano-pointllm_amd/`` never imports
+it and never falls back to it.
 
 Every function restates the reference algorithm it cites (paths relative to
 the reference repository root).  Arithmetic follows the reference exactly:
