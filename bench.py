@@ -459,6 +459,44 @@ def stack_with_lm_head(layers, m: int, device) -> dict:
     return {"ms": round(ms, 4), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes}
 
 
+def runner_decode_step(m: int, device, steps: int = 20, warmup: int = 5) -> dict:
+    """A whole decode step of a 32-layer LLaMA-7B-shaped model through
+    ``W8A8LlamaRunner`` (lightweight_runner.py:421-737) at M = m rows: per
+    layer the fused RMSNorm + packed QKV launch, o_proj, the fused residual
+    add + RMSNorm + gate/up SiLU*mul launch, down and the residual add; then
+    the final norm and the fp16 LM head.  Random weights (~N(0, 0.02)); the
+    attention core is ``query_passthrough_core`` (no kernel).  Captured with
+    ``DecodeGraphBucket`` (engine/cuda_graph.py:17-52) and replayed; the
+    first replay is checked against the eager step."""
+    import torch
+
+    from nanopointllm_amd import workloads as W
+    from nanopointllm_amd.runner import DecodeGraphBucket, W8A8LlamaRunner
+
+    model = W.llama_model(device, layers=W.LAYERS, seed=7)
+    runner = W8A8LlamaRunner(model, W.query_passthrough_core)
+    ids = torch.randint(0, W.VOCAB, (m,), generator=torch.Generator().manual_seed(8)).to(device)
+    eager = runner(ids).clone()
+    bucket = DecodeGraphBucket(device)
+    bucket.capture(lambda: runner(ids))
+    same = bool(torch.equal(bucket.replay(), eager))
+    for _ in range(warmup):
+        bucket.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        bucket.replay()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    nbytes = (step_bytes(m, W.LAYERS) + W.VOCAB * W.HIDDEN * 2 + 2 * m * W.HIDDEN
+              + 2 * m * W.VOCAB)
+    del bucket, runner, model
+    torch.cuda.empty_cache()
+    return {"ms": round(ms, 4), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes,
+            "m": m, "layers": W.LAYERS, "replay_equals_eager": same,
+            "attention_core": "query pass-through (no kernel)"}
+
+
 def _median_s(fn, reps: int = 5) -> float:
     """Median wall time of fn over reps runs, after one untimed run."""
     fn()
@@ -656,6 +694,8 @@ def main() -> int:
         extra["stack_with_fp16_lm_head"] = stack_with_lm_head(layers, m, device)
         log("decode step with the int8 MLP chain")
         extra["decode_step_int8_mlp_chain"] = decode_step_int8_mlp(layers, m, device)
+        log("runner decode step (32 layers, fused norms, LM head)")
+        extra["runner_decode_step"] = runner_decode_step(m, device)
 
     cpu = parity = None
     if not args.no_cpu:

@@ -376,6 +376,23 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
     // row is held here by thread c % TPR as its chunk c / TPR, and TPR is a
     // multiple of 64, so lane l of a wavefront holds chunk 64 g + l of some
     // group g and the butterfly is the same.
+    // Every CU normalizes all M rows, so at M = 8 this arithmetic is a large
+    // part of the prologue.  For binary16 rows three steps take one packed or
+    // mixed-precision instruction and give the same bits as the binary32
+    // sequence of the reference:
+    //   dtype(x + residual): binary32 carries 24 >= 2 * 11 + 2 bits, so
+    //     rounding the binary32 sum of two binary16 values to binary16 is one
+    //     correct rounding, which v_pk_add_f16 computes;
+    //   the sum of squares: lo * lo is exact in binary32 for a binary16 lo
+    //     (22 significant bits, within the normal range), so
+    //     fma(lo, lo, ss) == fl(fl(lo * lo) + ss) (v_fma_mix_f32);
+    //   dtype(w * h): the product of two binary16 values is exact in
+    //     binary32, so rounding it once is v_pk_mul_f16.
+    constexpr bool kHalf = std::is_same<TX, __half>::value;
+    using h2 = _Float16 __attribute__((ext_vector_type(2)));
+    // By value: __builtin_bit_cast of a vector element lvalue (raw[i][q])
+    // reads element 0 whatever the index, so elements go through a scalar.
+    auto as_h2 = [](uint32_t u) { return __builtin_bit_cast(h2, u); };
     float sq[NCH];
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
@@ -385,8 +402,12 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
         // summed = dtype(x + residual)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          raw[i][q] = pack2(bits_to_f32<TX>(raw[i][q] & 0xffffu) + bits_to_f32<TX>(rraw[i][q] & 0xffffu),
-                            bits_to_f32<TX>(raw[i][q] >> 16) + bits_to_f32<TX>(rraw[i][q] >> 16));
+          if constexpr (kHalf) {
+            raw[i][q] = __builtin_bit_cast(uint32_t, as_h2(raw[i][q]) + as_h2(rraw[i][q]));
+          } else {
+            raw[i][q] = pack2(bits_to_f32<TX>(raw[i][q] & 0xffffu) + bits_to_f32<TX>(rraw[i][q] & 0xffffu),
+                              bits_to_f32<TX>(raw[i][q] >> 16) + bits_to_f32<TX>(rraw[i][q] >> 16));
+          }
         }
         if (ok && writer) {
           *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.residual_out) +
@@ -399,12 +420,15 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       for (int q = 0; q < 4; ++q) {
         const float lo = bits_to_f32<TX>(raw[i][q] & 0xffffu);
         const float hi = bits_to_f32<TX>(raw[i][q] >> 16);
-        ss = __fadd_rn(ss, __fmul_rn(lo, lo));
-        ss = __fadd_rn(ss, __fmul_rn(hi, hi));
+        if constexpr (kHalf) {
+          ss = __builtin_fmaf(lo, lo, ss);
+          ss = __builtin_fmaf(hi, hi, ss);
+        } else {
+          ss = __fadd_rn(ss, __fmul_rn(lo, lo));
+          ss = __fadd_rn(ss, __fmul_rn(hi, hi));
+        }
       }
-#pragma unroll
-      for (int off = 32; off > 0; off >>= 1) ss = __fadd_rn(ss, __shfl_xor(ss, off));
-      sq[i] = ss;
+      sq[i] = wave_sum_xor(ss);
     }
     if (lane == 0 && row_live) {
 #pragma unroll
@@ -428,10 +452,16 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         // mul_keep_sign: a -0 element stays -0, as in the prologue kernel.
-        const float lo = to_f32(from_f32<TX>(mul_keep_sign(bits_to_f32<TX>(raw[i][q] & 0xffffu), rstd)));
-        const float hi = to_f32(from_f32<TX>(mul_keep_sign(bits_to_f32<TX>(raw[i][q] >> 16), rstd)));
-        raw[i][q] = pack2(mul_keep_sign(bits_to_f32<TX>(wraw[i][q] & 0xffffu), lo),
-                          mul_keep_sign(bits_to_f32<TX>(wraw[i][q] >> 16), hi));
+        if constexpr (kHalf) {
+          const h2 h = {static_cast<_Float16>(mul_keep_sign(bits_to_f32<TX>(raw[i][q] & 0xffffu), rstd)),
+                        static_cast<_Float16>(mul_keep_sign(bits_to_f32<TX>(raw[i][q] >> 16), rstd))};
+          raw[i][q] = __builtin_bit_cast(uint32_t, as_h2(wraw[i][q]) * h);
+        } else {
+          const float lo = to_f32(from_f32<TX>(mul_keep_sign(bits_to_f32<TX>(raw[i][q] & 0xffffu), rstd)));
+          const float hi = to_f32(from_f32<TX>(mul_keep_sign(bits_to_f32<TX>(raw[i][q] >> 16), rstd)));
+          raw[i][q] = pack2(mul_keep_sign(bits_to_f32<TX>(wraw[i][q] & 0xffffu), lo),
+                            mul_keep_sign(bits_to_f32<TX>(wraw[i][q] >> 16), hi));
+        }
       }
       if (ok && writer && p.x_out != nullptr) {
         *reinterpret_cast<u32x4*>(static_cast<uint16_t*>(p.x_out) +
@@ -449,8 +479,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       am2 = __builtin_elementwise_max(am2, __builtin_bit_cast(u16x2, raw[i][q] & 0x7fff7fffu));
   }
   uint32_t am = max(static_cast<uint32_t>(am2[0]), static_cast<uint32_t>(am2[1]));
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) am = max(am, static_cast<uint32_t>(__shfl_xor(static_cast<int>(am), off)));
+  am = wave_max_u32(am);
   // The first weight loads go out once x has arrived (the absmax above waits
   // for it) and stream while x is quantized.  Only kFusedPreSteps steps go out
   // before the quantization: a wave that issues more loads than the CU's

@@ -62,14 +62,12 @@ __device__ inline float round_to(float v) {
   return to_f32(from_f32<T>(v));
 }
 
-// Sum over the workgroup of one float per thread (every thread gets it).
+// Sum (or max of |x|) over the workgroup of one float per thread, every
+// thread getting it: the xor butterfly within each wavefront, then the
+// wavefront results in order.
 template <bool MAX>
 __device__ inline float block_reduce(float v, float* red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) {
-    const float o = __shfl_xor(v, off);
-    v = MAX ? fmaxf(v, o) : v + o;
-  }
+  v = MAX ? wave_max_abs(v) : wave_sum_xor(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   __syncthreads();  // red[] may still be read from a previous reduction
   if (lane == 0) red[wave] = v;

@@ -100,8 +100,7 @@ __global__ __launch_bounds__(NT) void quant_rows_kernel(
         for (int j = 0; j < 8; ++j) amax = fmaxf(amax, fabsf(t[j]));
       }
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    amax = wave_max_abs(amax);
     if ((tid & 63) == 0) red[tid >> 6] = amax;
     __syncthreads();
     amax = red[0];
@@ -181,8 +180,7 @@ __global__ __launch_bounds__(NT) void quant_rows_parts_kernel(
   const float* pr = parts + row * nparts;
   float amax = 0.0f;
   for (int64_t i = tid; i < nparts; i += NT) amax = fmaxf(amax, pr[i]);
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  amax = wave_max_abs(amax);
   if ((tid & 63) == 0) red[tid >> 6] = amax;
   __syncthreads();
   amax = red[0];

@@ -288,6 +288,50 @@ __device__ inline uint16_t f16_bits(float v) {
   return __builtin_bit_cast(uint16_t, __float2half_rn(v));
 }
 
+// ------------------------------------------------------ wavefront butterfly
+// op over the 64 lanes of a wavefront in the order of the xor butterfly
+// v = op(v, shfl_xor(v, d)) for d = 32, 16, 8, 4, 2, 1, every lane ending
+// with the result, without LDS round trips.  Partners at distance 32 and 16
+// come from v_permlane32_swap / v_permlane16_swap of the value with itself
+// (one half of the pair holds the lane's value, the other its partner's), at
+// 8 from a DPP rotation by 8 within a row of 16 (lane j reads j ^ 8), at 2
+// and 1 from quad permutations.  At 4 a rotation by 4 reads lane j ^ 4 or
+// (j ^ 4) ^ 8, which hold the same bits after the level at distance 8: each
+// level leaves a lane and its partner with op of the same two values, and op
+// must be commutative bit for bit (binary32 +; max of non-negative values).
+// Every lane of the wavefront must be active.
+template <typename Op>
+__device__ inline uint32_t wave_butterfly(uint32_t v, Op op) {
+  constexpr int kRowRor8 = 0x128, kRowRor4 = 0x124, kQuadXor2 = 0x4e, kQuadXor1 = 0xb1;
+  const auto a = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+  v = op(a[0], a[1]);
+  const auto b = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+  v = op(b[0], b[1]);
+  v = op(v, __builtin_amdgcn_update_dpp(0u, v, kRowRor8, 0xf, 0xf, false));
+  v = op(v, __builtin_amdgcn_update_dpp(0u, v, kRowRor4, 0xf, 0xf, false));
+  v = op(v, __builtin_amdgcn_update_dpp(0u, v, kQuadXor2, 0xf, 0xf, false));
+  v = op(v, __builtin_amdgcn_update_dpp(0u, v, kQuadXor1, 0xf, 0xf, false));
+  return v;
+}
+
+// Binary32 sum with the bits of the __shfl_xor butterfly.
+__device__ inline float wave_sum_xor(float v) {
+  return __uint_as_float(wave_butterfly(__float_as_uint(v), [](uint32_t x, uint32_t y) {
+    return __float_as_uint(__fadd_rn(__uint_as_float(x), __uint_as_float(y)));
+  }));
+}
+
+// fmaxf over non-negative values (|x|): the same bits in any order.
+__device__ inline float wave_max_abs(float v) {
+  return __uint_as_float(wave_butterfly(__float_as_uint(v), [](uint32_t x, uint32_t y) {
+    return __float_as_uint(fmaxf(__uint_as_float(x), __uint_as_float(y)));
+  }));
+}
+
+__device__ inline uint32_t wave_max_u32(uint32_t v) {
+  return wave_butterfly(v, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
+}
+
 // Packed-tile byte offset of element (r, k) of a [rows, K] operand.
 __host__ __device__ inline int64_t packed_offset(int64_t r, int64_t k, int64_t KB) {
   int64_t tile = (r >> 4) * KB + (k >> 6);

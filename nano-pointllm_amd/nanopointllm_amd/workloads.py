@@ -14,6 +14,7 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 import torch
+import torch.nn as nn
 
 HIDDEN = 4096
 INTERMEDIATE = 11008
@@ -106,3 +107,100 @@ def config1(seed: int = 0) -> tuple[torch.Tensor, torch.Tensor]:
     x[:, idx] *= 20.0
     w = torch.randn(HIDDEN, HIDDEN, generator=g) * 0.02
     return x.to(torch.float16), w.to(torch.float16)
+
+
+class RMSNorm(nn.Module):
+    """``LightweightRMSNorm`` (lightweight_runner.py:239-245): binary32 mean of
+    squares, ``rsqrt(var + eps)``, cast back, times the weight."""
+
+    def __init__(self, hidden: int, eps: float = 1e-6, *, device=None, dtype=None) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden, device=device, dtype=dtype))
+        self.variance_epsilon = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        dtype = x.dtype
+        h = x.float()
+        var = h.pow(2).mean(-1, keepdim=True)
+        h = h * torch.rsqrt(var + self.variance_epsilon)
+        return self.weight * h.to(dtype)
+
+
+class _Attention(nn.Module):
+    def __init__(self, hidden: int, heads: int, kv_heads: int, **kw) -> None:
+        super().__init__()
+        self.num_heads, self.num_key_value_heads = heads, kv_heads
+        self.head_dim = hidden // heads
+        kv = kv_heads * self.head_dim
+        self.q_proj = nn.Linear(hidden, hidden, bias=False, **kw)
+        self.k_proj = nn.Linear(hidden, kv, bias=False, **kw)
+        self.v_proj = nn.Linear(hidden, kv, bias=False, **kw)
+        self.o_proj = nn.Linear(hidden, hidden, bias=False, **kw)
+
+
+class _MLP(nn.Module):
+    def __init__(self, hidden: int, intermediate: int, **kw) -> None:
+        super().__init__()
+        self.gate_proj = nn.Linear(hidden, intermediate, bias=False, **kw)
+        self.up_proj = nn.Linear(hidden, intermediate, bias=False, **kw)
+        self.down_proj = nn.Linear(intermediate, hidden, bias=False, **kw)
+
+
+class _DecoderLayer(nn.Module):
+    def __init__(self, hidden: int, heads: int, kv_heads: int, intermediate: int, **kw) -> None:
+        super().__init__()
+        self.input_layernorm = RMSNorm(hidden, **kw)
+        self.self_attn = _Attention(hidden, heads, kv_heads, **kw)
+        self.post_attention_layernorm = RMSNorm(hidden, **kw)
+        self.mlp = _MLP(hidden, intermediate, **kw)
+
+
+class LlamaShaped(nn.Module):
+    """The module tree of a Hugging Face ``LlamaForCausalLM`` that the
+    reference's runners read (``model.embed_tokens``, ``model.layers[i]``
+    with ``input_layernorm`` / ``self_attn.{q,k,v,o}_proj`` /
+    ``post_attention_layernorm`` / ``mlp.{gate,up,down}_proj``,
+    ``model.norm``, ``lm_head``; lightweight_runner.py:421-737), with no
+    forward of its own: the W8A8 runner supplies it."""
+
+    def __init__(self, *, hidden: int = HIDDEN, heads: int = HEADS, kv_heads: int = KV_HEADS,
+                 intermediate: int = INTERMEDIATE, vocab: int = VOCAB, layers: int = LAYERS,
+                 device=None, dtype=None) -> None:
+        super().__init__()
+        kw = {"device": device, "dtype": dtype}
+        self.model = nn.Module()
+        self.model.embed_tokens = nn.Embedding(vocab, hidden, **kw)
+        self.model.layers = nn.ModuleList([_DecoderLayer(hidden, heads, kv_heads, intermediate,
+                                                         **kw) for _ in range(layers)])
+        self.model.norm = RMSNorm(hidden, **kw)
+        self.lm_head = nn.Linear(hidden, vocab, bias=False, **kw)
+
+
+def llama_model(device: str | torch.device, *, layers: int = LAYERS, seed: int = 0,
+                dtype: torch.dtype = torch.float16, **shape) -> LlamaShaped:
+    """A LLaMA-7B-shaped model (``shape`` overrides hidden / heads / kv_heads /
+    intermediate / vocab) with random weights drawn on ``device``: linear
+    weights ~N(0, 0.02), norm weights 1 + N(0, 0.1), embeddings ~N(0, 1).
+    The parameters are created without initialisation and filled once."""
+    with torch.device("meta"):
+        model = LlamaShaped(layers=layers, dtype=dtype, **shape)
+    model = model.to_empty(device=device)
+    g = _gen(seed, device)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if "norm" in name:
+                p.normal_(1.0, 0.1, generator=g)
+            elif "embed" in name:
+                p.normal_(0.0, 1.0, generator=g)
+            else:
+                p.normal_(0.0, 0.02, generator=g)
+    return model
+
+
+def query_passthrough_core(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, layer_index: int,
+                           state) -> torch.Tensor:
+    """A stand-in for the attention core that returns the query rows as the
+    context ``[T, H * D]`` (a view, no kernel): the step around it is the
+    W8A8 path alone.  Rotary, the KV cache and the attention kernel are not
+    part of that path."""
+    return q.reshape(q.shape[0], -1)

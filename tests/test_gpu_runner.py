@@ -23,8 +23,9 @@ import sys
 
 import pytest
 import torch
-import torch.nn as nn
 import torch.nn.functional as F
+
+from nanopointllm_amd.workloads import LlamaShaped
 
 pytestmark = pytest.mark.gpu
 
@@ -34,64 +35,10 @@ def note(msg):
     sys.__stderr__.flush()
 
 
-class _RMSNorm(nn.Module):
-    """LightweightRMSNorm's formula (lightweight_runner.py:239-245)."""
-
-    def __init__(self, hidden, eps=1e-6):
-        super().__init__()
-        self.weight = nn.Parameter(torch.ones(hidden))
-        self.variance_epsilon = eps
-
-    def forward(self, x):
-        dtype = x.dtype
-        h = x.float()
-        var = h.pow(2).mean(-1, keepdim=True)
-        h = h * torch.rsqrt(var + self.variance_epsilon)
-        return self.weight * h.to(dtype)
-
-
-class _Attn(nn.Module):
-    def __init__(self, hidden, heads, kv_heads):
-        super().__init__()
-        self.num_heads, self.num_key_value_heads = heads, kv_heads
-        self.head_dim = hidden // heads
-        self.q_proj = nn.Linear(hidden, hidden, bias=False)
-        self.k_proj = nn.Linear(hidden, kv_heads * self.head_dim, bias=False)
-        self.v_proj = nn.Linear(hidden, kv_heads * self.head_dim, bias=False)
-        self.o_proj = nn.Linear(hidden, hidden, bias=False)
-
-
-class _MLP(nn.Module):
-    def __init__(self, hidden, inter):
-        super().__init__()
-        self.gate_proj = nn.Linear(hidden, inter, bias=False)
-        self.up_proj = nn.Linear(hidden, inter, bias=False)
-        self.down_proj = nn.Linear(inter, hidden, bias=False)
-
-
-class _Layer(nn.Module):
-    def __init__(self, hidden, heads, kv_heads, inter):
-        super().__init__()
-        self.input_layernorm = _RMSNorm(hidden)
-        self.self_attn = _Attn(hidden, heads, kv_heads)
-        self.post_attention_layernorm = _RMSNorm(hidden)
-        self.mlp = _MLP(hidden, inter)
-
-
-class _FakeLlama(nn.Module):
-    def __init__(self, hidden, heads, kv_heads, inter, vocab, layers):
-        super().__init__()
-        self.model = nn.Module()
-        self.model.embed_tokens = nn.Embedding(vocab, hidden)
-        self.model.layers = nn.ModuleList([_Layer(hidden, heads, kv_heads, inter)
-                                           for _ in range(layers)])
-        self.model.norm = _RMSNorm(hidden)
-        self.lm_head = nn.Linear(hidden, vocab, bias=False)
-
-
 def _model(cuda, *, hidden=256, heads=4, kv_heads=2, inter=384, vocab=512, layers=2, seed=0):
     g = torch.Generator().manual_seed(seed)
-    m = _FakeLlama(hidden, heads, kv_heads, inter, vocab, layers)
+    m = LlamaShaped(hidden=hidden, heads=heads, kv_heads=kv_heads, intermediate=inter,
+                    vocab=vocab, layers=layers)
     with torch.no_grad():
         for name, p in m.named_parameters():
             if name.endswith("norm.weight") or "layernorm" in name:
