@@ -96,6 +96,11 @@ def _norm_eps(norm: nn.Module) -> float:
     return float(getattr(norm, "variance_epsilon", getattr(norm, "eps", 1.0e-6)))
 
 
+def _rows2(hidden_states: torch.Tensor) -> torch.Tensor:
+    """``[1, T, hidden]`` (the reference's staged decode layout) -> ``[T, hidden]``."""
+    return hidden_states[0] if hidden_states.dim() == 3 else hidden_states
+
+
 def _linear_parts(module: nn.Module) -> tuple[torch.Tensor, torch.Tensor | None]:
     return module.weight, getattr(module, "bias", None)
 
@@ -207,6 +212,19 @@ class W8A8PackedQKV(nn.Module):
         out = _w.rmsnorm_linear(staged, norm.weight, _norm_eps(norm), lin.packed, lin.scale,
                                 lin.bias, lin.out_features, in_features=lin.in_features)
         return self._split(out.y)
+
+    def project_rmsnorm_residual(self, hidden_states: torch.Tensor, residual: torch.Tensor,
+                                 norm: nn.Module
+                                 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor]:
+        """As :meth:`project_rmsnorm` on ``dtype(hidden_states + residual)``
+        (``residual_norm``, lightweight_runner.py:247-257): the add runs in the
+        same launch.  Returns ``(q, k, v, hidden_states + residual)``."""
+        lin = self.linear.weight_q
+        out = _w.rmsnorm_linear(_rows2(hidden_states), norm.weight, _norm_eps(norm), lin.packed,
+                                lin.scale, lin.bias, lin.out_features,
+                                residual=_rows2(residual), in_features=lin.in_features)
+        q, k, v = self._split(out.y)
+        return q, k, v, out.residual
 
     def _split(self, qkv: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         q_size = self.num_heads * self.head_dim

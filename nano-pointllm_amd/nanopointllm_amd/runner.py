@@ -95,6 +95,30 @@ class W8A8LlamaLayer(nn.Module):
         out = residual + mlp_out
         return out.unsqueeze(0) if hidden_states.dim() == 3 else out
 
+    @torch.no_grad()
+    def forward_carry(self, hidden_states: torch.Tensor, residual: torch.Tensor | None,
+                      attention_state: Any = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """The layer with its final residual add left to the caller: returns
+        ``(mlp_out, residual)``, whose binary16 / bfloat16 sum is what
+        :meth:`forward` returns.  With ``residual`` given, the layer's input
+        is ``dtype(hidden_states + residual)``, formed in the RMSNorm + packed
+        QKV launch; a rounded add of two 16-bit values is the same single
+        rounding wherever it runs, so a stack of ``forward_carry`` calls gives
+        the bits of a stack of ``forward`` calls with one launch fewer per
+        layer."""
+        rows = _rows(hidden_states)
+        if residual is None:
+            q, k, v = self.qkv.project_rmsnorm(rows, self.input_layernorm)
+            layer_in = rows
+        else:
+            q, k, v, layer_in = self.qkv.project_rmsnorm_residual(rows, _rows(residual),
+                                                                  self.input_layernorm)
+        context = self.attention_core(q, k, v, self.layer_index, attention_state)
+        attn_out = self.o_proj(context)
+        residual, mlp_out = self.mlp.forward_residual_rmsnorm(attn_out, layer_in,
+                                                              self.post_attention_layernorm)
+        return mlp_out, residual
+
 
 class W8A8LlamaRunner(nn.Module):
     """``LightweightLlamaRunner`` (lightweight_runner.py:563-737) with W8A8
@@ -129,9 +153,15 @@ class W8A8LlamaRunner(nn.Module):
             hidden_states = self.embed_tokens(input_ids)
         else:
             hidden_states = inputs_embeds
+        # Each layer's final residual add (lightweight_runner.py:552) runs in
+        # the next layer's RMSNorm + QKV launch; the last one here.
+        shape = hidden_states.shape
+        hidden, residual = _rows(hidden_states), None
         for layer in self.layers:
-            hidden_states = layer(hidden_states, attention_state)
-        return self.lm_head(self.norm(hidden_states))
+            hidden, residual = layer.forward_carry(hidden, residual, attention_state)
+        if residual is not None:
+            hidden = residual + hidden
+        return self.lm_head(self.norm(hidden.view(shape)))
 
 
 class DecodeGraphBucket:

@@ -181,6 +181,25 @@ def test_rows_give_the_same_bits_on_every_kernel_path(cuda, llama7b_layer):
     assert torch.equal(whole[:, :12], singles)
 
 
+@pytest.mark.parametrize("rows", [1, 8, 40])
+def test_carried_residual_equals_the_per_layer_add(cuda, rows):
+    """The runner leaves each layer's final residual add to the next layer's
+    RMSNorm + QKV launch (forward_carry); two LLaMA-7B-size layers, so the
+    second QKV takes the carried residual, on the fused decode kernel (rows 1
+    and 8) and the prologue + GEMM route (40 rows).  Bits equal to a stack of
+    the reference-form layer.forward calls (lightweight_runner.py:552)."""
+    model = _model(cuda, hidden=4096, heads=32, kv_heads=32, inter=11008, vocab=256, layers=2,
+                   seed=11)
+    runner = _runner(model, rowlocal_core)
+    x = torch.randn(1, rows, 4096, generator=torch.Generator().manual_seed(rows)).half().to(cuda)
+    note(f"carried residual vs per-layer add, rows={rows}")
+    got = runner(inputs_embeds=x)
+    h = x
+    for layer in runner.layers:
+        h = layer(h)
+    assert torch.equal(got, runner.lm_head(runner.norm(h)))
+
+
 @pytest.mark.parametrize("rows", [1, 8])
 def test_decode_graph_replays_match_eager(cuda, llama7b_layer, rows):
     from nanopointllm_amd.runner import DecodeGraphBucket
