@@ -329,35 +329,43 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   const int j0 = tid - row * tpr;
   const int nchunk = KB * 8;  // 8-element chunks per padded row
   const bool row_live = row < M;
-  const uint16_t* xr =
-      static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(row_live ? row : 0) * p.ldx;
+  // Branch-free raw buffer loads of x (and of the RMSNorm operands): each
+  // descriptor's range ends with row M-1's K elements (M * ld * 2 < 2^30),
+  // and a chunk outside the rows (of a row >= M, or past K) gets an offset
+  // beyond every range, so it reads zeros without a memory access.  Loads
+  // under a branch would each wait for the one before.
+  constexpr int kOutside = 0x7ffffff0;
+  const int K = p.K;
+  auto rows_rsrc = [&](const void* base, int64_t ld) {
+    const int nrec = __builtin_amdgcn_readfirstlane(
+        base == nullptr ? 0 : static_cast<int>((M - 1) * ld * 2) + K * 2);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, nrec, kBufferWord3);
+  };
+  auto chunk_off = [&](int c, int64_t ld) {
+    return row_live && c * 8 < K ? static_cast<int>(row * ld * 2) + c * 16 : kOutside;
+  };
+  const __amdgpu_buffer_rsrc_t xrsrc = rows_rsrc(p.x, p.ldx);
   u32x4 raw[NCH];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
-    const int c = j0 + i * tpr;
-    if (row_live && c < nchunk && c * 8 < p.K) {
-      raw[i] = *reinterpret_cast<const u32x4*>(xr + static_cast<int64_t>(c) * 8);
-    } else {
-      raw[i] = u32x4{0u, 0u, 0u, 0u};
-    }
+    raw[i] = __builtin_bit_cast(
+        u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, chunk_off(j0 + i * tpr, p.ldx), 0, 0));
   }
-  // RMSNorm operands, loaded with x (before any weight load is queued).
+  // RMSNorm operands, loaded with x (before any weight load is queued); a
+  // null residual has an empty range.
   [[maybe_unused]] u32x4 rraw[NORM ? NCH : 1];
   [[maybe_unused]] u32x4 wraw[NORM ? NCH : 1];
   if constexpr (NORM) {
-    const uint16_t* rr =
-        p.residual == nullptr
-            ? nullptr
-            : static_cast<const uint16_t*>(p.residual) + static_cast<int64_t>(row_live ? row : 0) * p.ld_res;
-    const uint16_t* wr = static_cast<const uint16_t*>(p.norm_w);
+    const __amdgpu_buffer_rsrc_t rrsrc = rows_rsrc(p.residual, p.ld_res);
+    const __amdgpu_buffer_rsrc_t wrsrc = rows_rsrc(p.norm_w, 0);
 #pragma unroll
     for (int i = 0; i < NCH; ++i) {
       const int c = j0 + i * tpr;
-      const bool ok = row_live && c < nchunk && c * 8 < p.K;
-      rraw[i] = (ok && rr != nullptr) ? *reinterpret_cast<const u32x4*>(rr + static_cast<int64_t>(c) * 8)
-                                      : u32x4{0u, 0u, 0u, 0u};
-      wraw[i] = ok ? *reinterpret_cast<const u32x4*>(wr + static_cast<int64_t>(c) * 8)
-                   : u32x4{0u, 0u, 0u, 0u};
+      rraw[i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rrsrc, chunk_off(c, p.ld_res), 0, 0));
+      wraw[i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     wrsrc, row_live && c * 8 < K ? c * 16 : kOutside, 0, 0));
     }
   }
   load_ops();
@@ -693,7 +701,8 @@ bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, in
   if (!((x_dtype == kF16 || x_dtype == kBF16) && M >= 1 && M <= kFusedMaxRows16 && K >= 8 &&
         K % 8 == 0 &&
         ceil_div(K, kTileK) <= (M <= kFusedMaxRows ? kFusedMaxKB : kFusedMaxKB16) &&
-        ldx % 8 == 0 && (reinterpret_cast<uintptr_t>(x) & 15u) == 0))
+        ldx % 8 == 0 && M * ldx * 2 < (int64_t{1} << 30) &&
+        (reinterpret_cast<uintptr_t>(x) & 15u) == 0))
     return false;
   const int64_t nb = ceil_div(N, kTileRows);
   const int64_t g = nb < cu_count() ? nb : cu_count();
@@ -758,7 +767,8 @@ bool fused_norm_supported(const void* x, int x_dtype, int64_t ldx, const void* r
   if (norm_w == nullptr || !a16(norm_w)) return false;
   if (x_out != nullptr && (!a16(x_out) || ld_xout % 8 != 0)) return false;
   if (residual != nullptr) {
-    if (!a16(residual) || !a16(residual_out) || ld_res % 8 != 0 || ld_res_out % 8 != 0)
+    if (!a16(residual) || !a16(residual_out) || ld_res % 8 != 0 || ld_res_out % 8 != 0 ||
+        M * ld_res * 2 >= (int64_t{1} << 30))
       return false;
     const int64_t nb = ceil_div(N, kTileRows);
     const int64_t g = nb < cu_count() ? nb : cu_count();
