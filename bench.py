@@ -71,6 +71,10 @@ def parse_args():
                          "x 5 repetitions, after the counter-calibration copy (the region "
                          "rocprofv3 runs of that projection measure)")
     ap.add_argument("--profile-m", type=int, default=8)
+    ap.add_argument("--profile-runner", action="store_true",
+                    help="only the whole-model decode step through W8A8LlamaRunner at --m rows "
+                         "(32 LLaMA-7B-shaped layers, LM head), captured and replayed (the "
+                         "region rocprofv3 runs of the runner measure)")
     return ap.parse_args()
 
 
@@ -652,6 +656,9 @@ def main() -> int:
                                                         args.profile_m)}))
         return 0
     m = args.m
+    if args.profile_runner:
+        print(json.dumps({"profile_runner": runner_decode_step(m, device)}))
+        return 0
     log(f"building {args.layers} layers of packed W8A8 weights (M={m})")
     layers = [Layer(i, m, device) for i in range(args.layers)]
     if args.profile_gateup:
