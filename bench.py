@@ -466,38 +466,70 @@ def stack_with_lm_head(layers, m: int, device) -> dict:
 def runner_decode_step(m: int, device, steps: int = 20, warmup: int = 5) -> dict:
     """A whole decode step of a 32-layer LLaMA-7B-shaped model through
     ``W8A8LlamaRunner`` (lightweight_runner.py:421-737) at M = m rows: per
-    layer the fused RMSNorm + packed QKV launch, o_proj, the fused residual
-    add + RMSNorm + gate/up SiLU*mul launch, down and the residual add; then
-    the final norm and the fp16 LM head.  Random weights (~N(0, 0.02)); the
-    attention core is ``query_passthrough_core`` (no kernel).  Captured with
-    ``DecodeGraphBucket`` (engine/cuda_graph.py:17-52) and replayed; the
-    first replay is checked against the eager step."""
+    layer the fused RMSNorm + packed QKV launch (with the previous layer's
+    residual add), o_proj, the fused residual add + RMSNorm + gate/up SiLU*mul
+    launch and down; then the final norm and the fp16 LM head.  Random weights
+    (~N(0, 0.02)); the attention core is ``query_passthrough_core`` (no
+    kernel).  Captured with ``DecodeGraphBucket`` (engine/cuda_graph.py:17-52)
+    and replayed; the first replay is checked against the eager step.  Timed
+    twice on the same model: with per-token dynamic quantization of h, and
+    with the static int8 MLP chain (a calibrated h scale per layer, the
+    maximum |h| of one eager step, lightweight_runner.py:362-379)."""
     import torch
 
     from nanopointllm_amd import workloads as W
     from nanopointllm_amd.runner import DecodeGraphBucket, W8A8LlamaRunner
+    from nanopointllm_amd.w8a8 import static_activation_scale
 
     model = W.llama_model(device, layers=W.LAYERS, seed=7)
     runner = W8A8LlamaRunner(model, W.query_passthrough_core)
     ids = torch.randint(0, W.VOCAB, (m,), generator=torch.Generator().manual_seed(8)).to(device)
-    eager = runner(ids).clone()
-    bucket = DecodeGraphBucket(device)
-    bucket.capture(lambda: runner(ids))
-    same = bool(torch.equal(bucket.replay(), eager))
-    for _ in range(warmup):
-        bucket.replay()
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        bucket.replay()
-    torch.cuda.synchronize()
-    ms = (time.perf_counter() - t0) * 1e3 / steps
     nbytes = (step_bytes(m, W.LAYERS) + W.VOCAB * W.HIDDEN * 2 + 2 * m * W.HIDDEN
               + 2 * m * W.VOCAB)
-    del bucket, runner, model
+
+    def timed() -> tuple[float, bool]:
+        eager = runner(ids).clone()
+        bucket = DecodeGraphBucket(device)
+        bucket.capture(lambda: runner(ids))
+        same = bool(torch.equal(bucket.replay(), eager))
+        for _ in range(warmup):
+            bucket.replay()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            bucket.replay()
+        torch.cuda.synchronize()
+        ms = (time.perf_counter() - t0) * 1e3 / steps
+        del bucket
+        return ms, same
+
+    ms, same = timed()
+    # Calibrate: each layer's max |h| (the down projection's input) over one
+    # eager step, then every MLP switches to the static int8 chain.
+    h_max: dict[int, torch.Tensor] = {}
+    hooks = [layer.mlp.down.register_forward_hook(
+        lambda mod, args, out, i=i: h_max.__setitem__(i, args[0].detach().abs().max()))
+        for i, layer in enumerate(runner.layers)]
+    runner(ids)
+    for h in hooks:
+        h.remove()
+    for i, layer in enumerate(runner.layers):
+        layer.mlp.h_scale = float(static_activation_scale(h_max[i], device=device))
+    ms_q8, same_q8 = timed()
+    spec = {p.name: p for p in W.PROJECTIONS}
+    h_bytes = (W.algorithmic_bytes(m, spec["gateup"].n, spec["gateup"].k, silu=True)
+               + W.algorithmic_bytes(m, spec["down"].n, spec["down"].k))
+    h_bytes_q8 = (W.algorithmic_bytes(m, spec["gateup"].n, spec["gateup"].k, silu=True,
+                                      int8_out=True)
+                  + W.algorithmic_bytes(m, spec["down"].n, spec["down"].k, int8_in=True))
+    nbytes_q8 = nbytes - W.LAYERS * (h_bytes - h_bytes_q8)
+    del runner, model
     torch.cuda.empty_cache()
     return {"ms": round(ms, 4), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes,
             "m": m, "layers": W.LAYERS, "replay_equals_eager": same,
+            "int8_mlp_chain": {"ms": round(ms_q8, 4),
+                               "GBps": round(nbytes_q8 / (ms_q8 * 1e-3) / 1e9, 1),
+                               "bytes": nbytes_q8, "replay_equals_eager": same_q8},
             "attention_core": "query pass-through (no kernel)"}
 
 

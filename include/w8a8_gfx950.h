@@ -221,7 +221,8 @@ int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w
  *   DEQUANT_BF16_EXACT), x_scale_out (nullable) its per-row scales.
  * Any m, k <= 32768.  Decode shapes of the fused decode route with m <= 8
  * and k <= 4096 (and enough weight per CU to cover reading x and the
- * residual on every CU) run as one kernel and need no workspace; the others
+ * residual on every CU) run as one kernel and need no workspace, with the
+ * epilogues I32 / DEQUANT / SILU_MUL / SILU_MUL_Q8; the others
  * run the activation prologue (w8a8_prologue_quant), which writes the int8
  * rows straight into the layout the product reads (row-major for the GEMV,
  * the packed tiles for the GEMM: no packing pass), then the product, and

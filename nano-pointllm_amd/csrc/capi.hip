@@ -502,7 +502,8 @@ int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* res
                         overlap(r_out, ld_residual_out, es, residual, ld_residual, es, m, k) ||
                         overlap(x_out, ld_x_out, es, x, ldx, es, m, k) ||
                         overlap(x_out, ld_x_out, es, residual, ld_residual, es, m, k);
-  if (k > 0 && epilogue <= W8A8_EPI_SILU_MUL && !in_place &&
+  const bool fused_epilogue = epilogue <= W8A8_EPI_SILU_MUL || epilogue == W8A8_EPI_SILU_MUL_Q8;
+  if (k > 0 && fused_epilogue && !in_place &&
       fused_norm_supported(x, x_dtype, ldx, residual, ld_residual, residual_out,
                            ld_residual_out, norm_weight, x_out, ld_x_out, m, n, k)) {
     // One kernel: residual add, RMSNorm, per-token quantization, GEMV, epilogue.

@@ -624,7 +624,8 @@ hipError_t launch_norm_f(const FusedParams& p, hipStream_t st) {
 }
 
 template <typename TX>
-hipError_t dispatch_norm_f(const FusedParams& p, int epi, int y_dtype, hipStream_t st) {
+hipError_t dispatch_norm_f(const FusedParams& p, int epi, int y_dtype, int h_dtype,
+                           hipStream_t st) {
   switch (epi) {
     case kEpiI32:
       return launch_norm_f<kEpiI32, TX, int32_t, float>(p, st);
@@ -636,6 +637,10 @@ hipError_t dispatch_norm_f(const FusedParams& p, int epi, int y_dtype, hipStream
     case kEpiSilu:
       if (y_dtype == kF16) return launch_norm_f<kEpiSilu, TX, __half, __half>(p, st);
       if (y_dtype == kBF16) return launch_norm_f<kEpiSilu, TX, __hip_bfloat16, __hip_bfloat16>(p, st);
+      return hipErrorInvalidValue;
+    case kEpiSiluQ8:
+      if (h_dtype == kF16) return launch_norm_f<kEpiSiluQ8, TX, int8_t, __half>(p, st);
+      if (h_dtype == kBF16) return launch_norm_f<kEpiSiluQ8, TX, int8_t, __hip_bfloat16>(p, st);
       return hipErrorInvalidValue;
     default:
       return hipErrorInvalidValue;
@@ -809,8 +814,9 @@ hipError_t launch_gemv_fused_norm(const void* x, int x_dtype, int64_t ldx, const
   p.NB = static_cast<int>(ceil_div(op.N, kTileRows));
   p.G = static_cast<int>(p.NB < cu_count() ? p.NB : cu_count());
   if (p.NB == 0 || p.M == 0) return hipSuccess;
-  if (x_dtype == kF16) return dispatch_norm_f<__half>(p, op.epi, op.y_dtype, st);
-  if (x_dtype == kBF16) return dispatch_norm_f<__hip_bfloat16>(p, op.epi, op.y_dtype, st);
+  if (x_dtype == kF16) return dispatch_norm_f<__half>(p, op.epi, op.y_dtype, op.h_dtype, st);
+  if (x_dtype == kBF16)
+    return dispatch_norm_f<__hip_bfloat16>(p, op.epi, op.y_dtype, op.h_dtype, st);
   return hipErrorInvalidValue;
 }
 

@@ -334,6 +334,18 @@ class W8A8MLP(nn.Module):
                                            verify_source=verify_source)
         self.h_scale = h_scale
         self.two_phase = two_phase
+        self._h_rows_cache: dict[tuple[int, torch.device, float], torch.Tensor] = {}
+
+    def _h_rows(self, hq: torch.Tensor) -> torch.Tensor:
+        """The static h scale once per row of ``hq``, made once per row count
+        and device (a fill per call would add kernels to every decode step;
+        a captured step finds it made by its warm-up calls)."""
+        key = (hq.numel() // hq.shape[-1] if hq.numel() else 0, hq.device, float(self.h_scale))
+        t = self._h_rows_cache.get(key)
+        if t is None:
+            t = torch.full((key[0],), self.h_scale, dtype=torch.float32, device=hq.device)
+            self._h_rows_cache[key] = t
+        return t
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.h_scale is None:
@@ -342,8 +354,7 @@ class W8A8MLP(nn.Module):
                 return self.down.forward_i8(out.hq, out.scale.reshape(-1), out_dtype=x.dtype)
             return self.down(self.gate_up(x))
         hq = self.gate_up.forward_q8(x, self.h_scale)
-        s = torch.full((1,), self.h_scale, dtype=torch.float32, device=x.device)
-        return self.down.forward_i8(hq, s, out_dtype=x.dtype)
+        return self.down.forward_i8(hq, self._h_rows(hq), out_dtype=x.dtype)
 
     def forward_residual_rmsnorm(self, hidden_states: torch.Tensor, residual: torch.Tensor,
                                  norm: nn.Module) -> tuple[torch.Tensor, torch.Tensor]:
@@ -359,8 +370,8 @@ class W8A8MLP(nn.Module):
                                   in_features=p.in_features)
         if self.h_scale is None:
             return first.residual, self.down(first.y)
-        s = torch.full((1,), self.h_scale, dtype=torch.float32, device=hidden_states.device)
-        return first.residual, self.down.forward_i8(first.y, s, out_dtype=hidden_states.dtype)
+        return first.residual, self.down.forward_i8(first.y, self._h_rows(first.y),
+                                                    out_dtype=hidden_states.dtype)
 
     def forward_i8(self, xq: torch.Tensor, x_scale: torch.Tensor, *,
                    out_dtype: torch.dtype = torch.float16) -> torch.Tensor:
@@ -372,8 +383,7 @@ class W8A8MLP(nn.Module):
                 return self.down.forward_i8(out.hq, out.scale.reshape(-1), out_dtype=out_dtype)
             return self.down(self.gate_up.forward_i8(xq, x_scale, out_dtype=out_dtype))
         hq = self.gate_up.forward_i8(xq, x_scale, out_dtype=out_dtype, h_scale=self.h_scale)
-        s = torch.full((1,), self.h_scale, dtype=torch.float32, device=xq.device)
-        return self.down.forward_i8(hq, s, out_dtype=out_dtype)
+        return self.down.forward_i8(hq, self._h_rows(hq), out_dtype=out_dtype)
 
 
 class W8A8RMSNormQuant(nn.Module):

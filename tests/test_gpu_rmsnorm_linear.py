@@ -209,6 +209,51 @@ def test_rmsnorm_linear_against_two_launches_and_oracle(cuda, label, proj, m, dt
                                       O.dequant_epilogue(acc, es, s, b).astype(np.float16))
 
 
+@pytest.mark.parametrize("m,dtype", [(1, "f16"), (8, "f16"), (8, "bf16")])
+def test_residual_rmsnorm_gateup_int8_h_in_one_launch(cuda, m, dtype):
+    """The static int8 MLP chain's gate/up (lightweight_runner.py:362-379 with
+    a calibrated h scale): residual add + RMSNorm + quantization + packed
+    gate/up + SiLU*mul + int8 requant of h, the one fused kernel at decode
+    shapes (no workspace).  The same bits as the activation prologue + the
+    int8-in linear; int8 h equal to quantize_symmetric (w8a8.py:33-43) of the
+    oracle's SiLU*mul (binary16) from the kernel's own normalized rows."""
+    from nanopointllm_amd import _lib, w8a8
+
+    q, s, b = _weights("gateup")
+    wp, sw, bias = _device("gateup", cuda)
+    n, k, tdt = q.shape[0], HIDDEN, TDT[dtype]
+    x = _rows(m, k, dtype, seed=500 + m).to(cuda)
+    res = _rows(m, k, dtype, seed=600 + m, scale=0.3).to(cuda)
+    nw = _norm_weight(k, dtype, seed=700 + m).to(cuda)
+    h_scale = float(O.scale_from_absmax(np.float32(2.5)))
+    hq = torch.empty(m, n // 2, dtype=torch.int8, device=cuda)
+    rows = torch.empty(m, k, dtype=tdt, device=cuda)
+    res_out = torch.empty(m, k, dtype=tdt, device=cuda)
+    sx = torch.empty(m, dtype=torch.float32, device=cuda)
+    lib = _lib.load()
+    note(f"rmsnorm_linear gate/up SiLU*mul + int8 h, m={m} {dtype}")
+    rc = lib.w8a8_rmsnorm_linear(
+        x.data_ptr(), _lib.dtype_code(tdt), k, res.data_ptr(), k, res_out.data_ptr(), k,
+        nw.data_ptr(), ctypes.c_float(1e-6), wp.data_ptr(), sw.data_ptr(), bias.data_ptr(),
+        _lib.EPI_SILU_MUL_Q8, hq.data_ptr(), _lib.I8, n // 2, ctypes.c_float(h_scale),
+        _lib.dtype_code(tdt), m, n, k, sx.data_ptr(), rows.data_ptr(), k, None, 0,
+        _lib.stream_handle(cuda))
+    assert rc == _lib.OK                      # no workspace: the one fused kernel
+    pro = w8a8.prologue_quant(x, norm_weight=nw, eps=1e-6, residual=res, return_rows=True)
+    hq2 = w8a8.linear_i8in(pro.q, pro.scale.reshape(-1), wp, sw, bias, n,
+                           epilogue=_lib.EPI_SILU_MUL_Q8, out_dtype=torch.int8,
+                           y_scale=h_scale, inter_dtype=tdt)
+    bits = lambda t: t.view(torch.int16)
+    assert torch.equal(hq, hq2)
+    assert torch.equal(bits(rows), bits(pro.rows))
+    assert torch.equal(bits(res_out), bits(pro.residual))
+    assert torch.equal(sx, pro.scale.reshape(-1))
+    if dtype == "f16":
+        xq, es = O.dynamic_per_token_quant(rows.float().cpu().numpy())
+        eh = O.gateup_silu_mul_from_acc(O.int32_matmul_f64(xq, q), es, s, b, layout="interleave")
+        np.testing.assert_array_equal(hq.cpu().numpy(), O.quantize_symmetric(eh, h_scale))
+
+
 @pytest.mark.parametrize("dtype", ["f16", "bf16"])
 @pytest.mark.parametrize("m", [1, 8])
 def test_fused_accumulators_exact_where_the_sum_is_exact(cuda, dtype, m):
