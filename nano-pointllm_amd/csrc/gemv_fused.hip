@@ -97,11 +97,6 @@ __device__ inline i32x4 mfma_16x16x64(i32x4 a, i32x4 b, i32x4 c) {
 // values, so the integer max is the absmax.
 typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
-template <typename TX>
-__device__ inline float bits_to_f32(uint32_t b16) {
-  return to_f32(__builtin_bit_cast(TX, static_cast<uint16_t>(b16)));
-}
-
 // Sums the per-wave partials of output block nb and writes its outputs.
 // `ops` holds the block's 16 weight scales followed by its 16 biases.
 template <int EPI, typename TY, typename TH>

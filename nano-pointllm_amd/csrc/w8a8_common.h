@@ -64,6 +64,19 @@ template <> __device__ inline __hip_bfloat16 from_f32<__hip_bfloat16>(float v) {
   return __builtin_bit_cast(__hip_bfloat16, b);
 }
 
+// A 16-bit pattern of type TX as binary32.
+template <typename TX>
+__device__ inline float bits_to_f32(uint32_t b16) {
+  return to_f32(__builtin_bit_cast(TX, static_cast<uint16_t>(b16)));
+}
+
+// Two binary32 values rounded to the 16-bit type T, packed low then high.
+template <typename T>
+__device__ inline uint32_t pack2_bits(float lo, float hi) {
+  return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(lo))) |
+         (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<T>(hi))) << 16);
+}
+
 // Loads 8 consecutive elements as binary32.  `vec` selects one (fp16/bf16)
 // or two (f32) 16-byte loads; callers guarantee 16-byte alignment then.
 template <typename T>
@@ -286,6 +299,20 @@ __host__ __device__ inline uint16_t dequant_bf16_exact(int32_t acc, uint16_t sa_
 // representable scales of the W8A8 contract).
 __device__ inline uint16_t f16_bits(float v) {
   return __builtin_bit_cast(uint16_t, __float2half_rn(v));
+}
+
+// ------------------------------------------------------------ raw buffers
+// A raw buffer descriptor over [base, base + bytes) (gfx9 word 3: 32-bit
+// data format): loads at offsets outside the range return zeros without a
+// memory access, so they need no branch.  A null base gets an empty range.
+__device__ inline __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<void*>(base), 0, __builtin_amdgcn_readfirstlane(base == nullptr ? 0 : bytes),
+      0x00020000);
+}
+
+__device__ inline u32x4 load16(__amdgpu_buffer_rsrc_t r, int offset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, offset, 0, 0));
 }
 
 // ------------------------------------------------------ wavefront butterfly
