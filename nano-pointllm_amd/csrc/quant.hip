@@ -49,6 +49,35 @@ __device__ inline void store8(int8_t* __restrict__ q, int64_t row, int64_t k0, i
   }
 }
 
+// Loads the REG 8-element chunks (tid + c * NT) of a row whose elements are
+// 16-byte aligned, K % 8 == 0: range-checked raw buffer loads, all issued
+// before any is used (zeros past K, and for a null row).  A load under a
+// branch per chunk would wait for each before issuing the next.
+template <typename TX, int REG, int NT>
+__device__ inline void load_row_chunks(const TX* row, int64_t K, int tid, float (&v)[REG][8]) {
+  constexpr int kWords = sizeof(TX) == 4 ? 2 : 1;
+  const __amdgpu_buffer_rsrc_t d = raw_rsrc(row, static_cast<int>(K * sizeof(TX)));
+  u32x4 raw[REG][kWords];
+#pragma unroll
+  for (int c = 0; c < REG; ++c) {
+    const int off = (tid + c * NT) * 8 * static_cast<int>(sizeof(TX));
+#pragma unroll
+    for (int w = 0; w < kWords; ++w) raw[c][w] = load16(d, off + 16 * w);
+  }
+#pragma unroll
+  for (int c = 0; c < REG; ++c) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if constexpr (sizeof(TX) == 4) {
+        v[c][j] = __uint_as_float(raw[c][j >> 2][j & 3]);
+      } else {
+        const uint32_t w = raw[c][0][j >> 1];
+        v[c][j] = bits_to_f32<TX>(j & 1 ? w >> 16 : w & 0xffffu);
+      }
+    }
+  }
+}
+
 // One workgroup per row.  The row (8 elements per thread-chunk) is read once
 // into registers when it fits (REG), reduced to |x|max for a dynamic scale
 // (or the caller's scale is read), then quantized and written either as a
@@ -70,15 +99,19 @@ __global__ __launch_bounds__(NT) void quant_rows_kernel(
 
   float v[REG > 0 ? REG : 1][8];
   if constexpr (REG > 0) {
+    if (vec_in) {
+      load_row_chunks<TX, REG, NT>(live ? xr : nullptr, K, tid, v);
+    } else {
 #pragma unroll
-    for (int c = 0; c < REG; ++c) {
-      const int64_t k0 = (tid + static_cast<int64_t>(c) * NT) * 8;
-      const int64_t rem = K - k0;
-      if (live && rem > 0) {
-        load8(xr + k0, v[c], vec_in != 0, static_cast<int>(rem < 8 ? rem : 8));
-      } else {
+      for (int c = 0; c < REG; ++c) {
+        const int64_t k0 = (tid + static_cast<int64_t>(c) * NT) * 8;
+        const int64_t rem = K - k0;
+        if (live && rem > 0) {
+          load8(xr + k0, v[c], false, static_cast<int>(rem < 8 ? rem : 8));
+        } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[c][j] = 0.0f;
+          for (int j = 0; j < 8; ++j) v[c][j] = 0.0f;
+        }
       }
     }
   }
@@ -165,15 +198,19 @@ __global__ __launch_bounds__(NT) void quant_rows_parts_kernel(
   const int64_t nchunk = (K + 7) / 8;
   float v[REG > 0 ? REG : 1][8];
   if constexpr (REG > 0) {
+    if (vec_in) {
+      load_row_chunks<TX, REG, NT>(xr, K, tid, v);
+    } else {
 #pragma unroll
-    for (int c = 0; c < REG; ++c) {
-      const int64_t k0 = (tid + static_cast<int64_t>(c) * NT) * 8;
-      const int64_t rem = K - k0;
-      if (rem > 0) {
-        load8(xr + k0, v[c], vec_in != 0, static_cast<int>(rem < 8 ? rem : 8));
-      } else {
+      for (int c = 0; c < REG; ++c) {
+        const int64_t k0 = (tid + static_cast<int64_t>(c) * NT) * 8;
+        const int64_t rem = K - k0;
+        if (rem > 0) {
+          load8(xr + k0, v[c], false, static_cast<int>(rem < 8 ? rem : 8));
+        } else {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) v[c][j] = 0.0f;
+          for (int j = 0; j < 8; ++j) v[c][j] = 0.0f;
+        }
       }
     }
   }
