@@ -472,9 +472,10 @@ def runner_decode_step(m: int, device, steps: int = 20, warmup: int = 5) -> dict
     (~N(0, 0.02)); the attention core is ``query_passthrough_core`` (no
     kernel).  Captured with ``DecodeGraphBucket`` (engine/cuda_graph.py:17-52)
     and replayed; the first replay is checked against the eager step.  Timed
-    twice on the same model: with per-token dynamic quantization of h, and
-    with the static int8 MLP chain (a calibrated h scale per layer, the
-    maximum |h| of one eager step, lightweight_runner.py:362-379)."""
+    on the same model with per-token dynamic quantization of h, then as a
+    560-row prefill step, then with the static int8 MLP chain (a calibrated h
+    scale per layer, the maximum |h| of one eager step,
+    lightweight_runner.py:362-379)."""
     import torch
 
     from nanopointllm_amd import workloads as W
@@ -487,7 +488,7 @@ def runner_decode_step(m: int, device, steps: int = 20, warmup: int = 5) -> dict
     nbytes = (step_bytes(m, W.LAYERS) + W.VOCAB * W.HIDDEN * 2 + 2 * m * W.HIDDEN
               + 2 * m * W.VOCAB)
 
-    def timed() -> tuple[float, bool]:
+    def timed(ids=ids) -> tuple[float, bool]:
         eager = runner(ids).clone()
         bucket = DecodeGraphBucket(device)
         bucket.capture(lambda: runner(ids))
@@ -504,6 +505,14 @@ def runner_decode_step(m: int, device, steps: int = 20, warmup: int = 5) -> dict
         return ms, same
 
     ms, same = timed()
+    # A prefill step of 560 rows (the size of 513 point tokens plus a prompt)
+    # on the same model: every projection on the MFMA GEMM, the RMSNorm
+    # prologue writing the GEMM's packed tiles.
+    pm = 560
+    pids = torch.randint(0, W.VOCAB, (pm,), generator=torch.Generator().manual_seed(9)).to(device)
+    ms_pf, same_pf = timed(pids)
+    ops_pf = W.LAYERS * sum(W.algorithmic_ops(pm, p.n, p.k) for p in W.PROJECTIONS)
+    ops_pf += 2 * pm * W.VOCAB * W.HIDDEN
     # Calibrate: each layer's max |h| (the down projection's input) over one
     # eager step, then every MLP switches to the static int8 chain.
     h_max: dict[int, torch.Tensor] = {}
@@ -530,6 +539,9 @@ def runner_decode_step(m: int, device, steps: int = 20, warmup: int = 5) -> dict
             "int8_mlp_chain": {"ms": round(ms_q8, 4),
                                "GBps": round(nbytes_q8 / (ms_q8 * 1e-3) / 1e9, 1),
                                "bytes": nbytes_q8, "replay_equals_eager": same_q8},
+            "prefill": {"m": pm, "ms": round(ms_pf, 4),
+                        "TOPS": round(ops_pf / (ms_pf * 1e-3) / 1e12, 1),
+                        "replay_equals_eager": same_pf},
             "attention_core": "query pass-through (no kernel)"}
 
 
