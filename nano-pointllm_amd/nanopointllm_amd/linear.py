@@ -334,18 +334,24 @@ class W8A8MLP(nn.Module):
                                            verify_source=verify_source)
         self.h_scale = h_scale
         self.two_phase = two_phase
-        self._h_rows_cache: dict[tuple[int, torch.device, float], torch.Tensor] = {}
+        self._h_rows_buf: dict[tuple[torch.device, float], torch.Tensor] = {}
+        self._h_rows_keep: list[torch.Tensor] = []
 
     def _h_rows(self, hq: torch.Tensor) -> torch.Tensor:
-        """The static h scale once per row of ``hq``, made once per row count
-        and device (a fill per call would add kernels to every decode step;
-        a captured step finds it made by its warm-up calls)."""
-        key = (hq.numel() // hq.shape[-1] if hq.numel() else 0, hq.device, float(self.h_scale))
-        t = self._h_rows_cache.get(key)
-        if t is None:
-            t = torch.full((key[0],), self.h_scale, dtype=torch.float32, device=hq.device)
-            self._h_rows_cache[key] = t
-        return t
+        """The static h scale once per row of ``hq``: a prefix of one filled
+        buffer per device and scale (a fill per call would add kernels to
+        every decode step; a captured step finds the buffer made by its
+        warm-up calls).  The buffer grows geometrically and the outgrown ones
+        are kept, since a captured graph may still read them."""
+        m = hq.numel() // hq.shape[-1] if hq.numel() else 0
+        key = (hq.device, float(self.h_scale))
+        buf = self._h_rows_buf.get(key)
+        if buf is None or buf.numel() < m:
+            size = max(m, 16, 2 * (0 if buf is None else buf.numel()))
+            buf = torch.full((size,), self.h_scale, dtype=torch.float32, device=hq.device)
+            self._h_rows_keep.append(buf)
+            self._h_rows_buf[key] = buf
+        return buf[:m]
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if self.h_scale is None:
