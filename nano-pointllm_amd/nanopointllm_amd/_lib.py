@@ -100,6 +100,8 @@ _SIGNATURES = {
 def load(path: str | Path | None = None) -> ctypes.CDLL:
     """Load (once) and return the library; raise if it is absent or stale."""
     global _lib
+    if _lib is not None and path is None:
+        return _lib
     with _lock:
         if _lib is not None and path is None:
             return _lib
@@ -138,7 +140,11 @@ def check(status: int, what: str) -> None:
 
 
 def stream_handle(device: torch.device) -> int:
-    return torch.cuda.current_stream(device).cuda_stream
+    """The raw ``hipStream_t`` of torch's current stream on ``device`` (the
+    direct query: building a ``torch.cuda.Stream`` object per launch costs
+    more host time than the launch itself at decode shapes)."""
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(index)
 
 
 def require_cuda(*tensors: torch.Tensor) -> torch.device:

@@ -9,6 +9,7 @@ and the trivial elementwise QDQ reconstruction (``q * s``).
 from __future__ import annotations
 
 from dataclasses import asdict, dataclass
+from functools import lru_cache
 from typing import Any, NamedTuple
 
 import torch
@@ -40,10 +41,12 @@ CONTRACT = W8A8Contract()
 
 
 # ---------------------------------------------------------------- low level
+@lru_cache(maxsize=1024)
 def packed_bytes(rows: int, k: int) -> int:
     return int(_lib.load().w8a8_packed_bytes(rows, k))
 
 
+@lru_cache(maxsize=1024)
 def workspace_bytes(m: int, k: int) -> int:
     return int(_lib.load().w8a8_workspace_bytes(m, k))
 
