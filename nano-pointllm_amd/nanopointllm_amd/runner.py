@@ -27,6 +27,11 @@ with the quantization of its output:
    (lightweight_runner.py:320-383);
 7. the final residual add in the activation dtype, as the reference does.
 
+After the last layer, its residual add and the final ``norm``
+(``LightweightRMSNorm``, lightweight_runner.py:609, 675) run as one launch of
+the activation prologue, the same kernel and formula as the in-layer norms,
+in front of the LM head.
+
 The stack is inference-only (no autograd).  Nothing on it synchronizes with
 the host or allocates outside torch's allocator, so a decode step can be
 captured into a HIP graph;
@@ -40,8 +45,9 @@ from typing import Any, Callable
 import torch
 import torch.nn as nn
 
+from . import w8a8 as _w
 from .inject import inject_w8a8
-from .linear import W8A8Linear, W8A8MLP, W8A8PackedQKV
+from .linear import W8A8Linear, W8A8MLP, W8A8PackedQKV, _norm_eps
 
 AttentionCore = Callable[[torch.Tensor, torch.Tensor, torch.Tensor, int, Any], torch.Tensor]
 
@@ -124,8 +130,10 @@ class W8A8LlamaRunner(nn.Module):
     """``LightweightLlamaRunner`` (lightweight_runner.py:563-737) with W8A8
     decoder layers: ``embed_tokens`` -> layers -> ``norm`` -> ``lm_head``.
 
-    The final norm and the LM head stay in the model's dtype (the LM head is
-    not a W8A8 linear in the reference either).  ``inject`` installs the W8A8
+    The final norm (residual add included) runs on the activation prologue
+    kernel when its weight has the activations' dtype, else as the model's
+    own module; the LM head stays a linear in the model's dtype (it is not a
+    W8A8 linear in the reference either).  ``inject`` installs the W8A8
     modules first (``h_scales`` and ``weight_cache`` as in :func:`inject_w8a8`).
     """
 
@@ -154,14 +162,24 @@ class W8A8LlamaRunner(nn.Module):
         else:
             hidden_states = inputs_embeds
         # Each layer's final residual add (lightweight_runner.py:552) runs in
-        # the next layer's RMSNorm + QKV launch; the last one here.
+        # the next layer's RMSNorm + QKV launch; the last one in the final norm's.
         shape = hidden_states.shape
         hidden, residual = _rows(hidden_states), None
         for layer in self.layers:
             hidden, residual = layer.forward_carry(hidden, residual, attention_state)
-        if residual is not None:
-            hidden = residual + hidden
-        return self.lm_head(self.norm(hidden.view(shape)))
+        return self.lm_head(self.final_norm(hidden, residual).view(shape))
+
+    def final_norm(self, hidden: torch.Tensor, residual: torch.Tensor | None) -> torch.Tensor:
+        """``norm(dtype(hidden + residual))`` for ``[T, hidden]`` rows
+        (lightweight_runner.py:247-257, 675): one launch of the activation
+        prologue, whose normalized rows are the output (its int8 rows are not
+        used).  Rows that are not binary16 / bfloat16, or a norm weight of
+        another dtype than the rows', run the model's own module."""
+        w = self.norm.weight
+        if hidden.dtype not in (torch.float16, torch.bfloat16) or w.dtype != hidden.dtype:
+            return self.norm(hidden if residual is None else residual + hidden)
+        return _w.prologue_quant(hidden, norm_weight=w, eps=_norm_eps(self.norm),
+                                 residual=residual, return_rows=True).rows
 
 
 class DecodeGraphBucket:

@@ -11,6 +11,8 @@ Bars:
   attention core is row-local;
 * every replay of a captured decode step equals the eager step for the same
   input, with eager work and synchronizations between the replays;
+* the final residual add + norm (one prologue launch) gives the oracle's
+  rounded sum and its LightweightRMSNorm within 2 ulps, almost all bit-equal;
 * end to end, the logits stay within the int8 quantization error of a dense
   binary32 model with the same weights and attention (relative Frobenius
   error below 5%, cosine above 0.998); a wiring mistake (missing residual,
@@ -135,7 +137,9 @@ def test_runner_is_the_chain_of_its_primitives(cuda, tokens):
         a = layer.self_attn.o_proj(causal_core(q, k, v, i, None))
         r, xq, sx = w8a8.rmsnorm_quant(a, layer.post_attention_layernorm.weight, 1e-6, residual=x)
         x = r + layer.mlp.w8a8_mlp.forward_i8(xq, sx, out_dtype=torch.float16)
-    expect = model.lm_head(model.model.norm(x))
+    norm = model.model.norm
+    expect = model.lm_head(w8a8.prologue_quant(x, norm_weight=norm.weight,
+                                               eps=norm.variance_epsilon, return_rows=True).rows)
     assert logits.shape == (1, tokens, 512)
     assert torch.equal(logits[0], expect)
 
@@ -197,7 +201,47 @@ def test_carried_residual_equals_the_per_layer_add(cuda, rows):
     h = x
     for layer in runner.layers:
         h = layer(h)
-    assert torch.equal(got, runner.lm_head(runner.norm(h)))
+    assert torch.equal(got, runner.lm_head(runner.final_norm(h[0], None).view(h.shape)))
+
+
+@pytest.mark.parametrize("rows,dtype", [(1, torch.float16), (8, torch.float16),
+                                        (8, torch.bfloat16), (560, torch.float16)])
+def test_final_norm_is_lightweight_rmsnorm(cuda, rows, dtype):
+    """The runner's final residual add + norm (one prologue launch) against
+    the oracle's ``LightweightRMSNorm`` (lightweight_runner.py:239-257) of the
+    rounded sum: the sum bit-exact, the normalized rows within 2 ulps and
+    almost all bit-equal (binary32 sums of squares in another order); and
+    within 2 ulps of the model's own torch module."""
+    import numpy as np
+    from oracle import w8a8_oracle as O
+
+    model = _model(cuda, hidden=4096, heads=32, kv_heads=32, inter=256, vocab=64, layers=1,
+                   seed=13)
+    runner = _runner(model, rowlocal_core)
+    norm = runner.norm
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.1 * torch.randn(4096, generator=torch.Generator().manual_seed(5)))
+        norm.weight.data = norm.weight.data.to(dtype)
+    g = torch.Generator().manual_seed(rows)
+    hid = (torch.randn(rows, 4096, generator=g) * 2).to(dtype)
+    res = (torch.randn(rows, 4096, generator=g) * 0.5).to(dtype)
+    note(f"final norm vs LightweightRMSNorm, rows={rows}, {dtype}")
+    got = runner.final_norm(hid.to(cuda), res.to(cuda))
+    assert got.dtype == dtype and got.shape == (rows, 4096)
+    name = "f16" if dtype == torch.float16 else "bf16"
+    summed = O.residual_add(hid.float().numpy(), res.float().numpy(), name)
+    want = O.rmsnorm(summed, norm.weight.detach().float().cpu().numpy(), norm.variance_epsilon,
+                     name)
+    ulps = _ulps16(got.cpu(), torch.from_numpy(want).to(dtype))
+    assert ulps.max() <= 2 and np.count_nonzero(ulps) <= max(2, ulps.size // 1000)
+    with torch.no_grad():
+        ref = norm((hid + res).to(cuda)).cpu()
+    assert _ulps16(got.cpu(), ref).max() <= 2
+
+
+def _ulps16(a: torch.Tensor, b: torch.Tensor):
+    key = lambda t: (lambda i: torch.where(i < 0, -(i & 0x7FFF), i))(t.view(torch.int16).int())
+    return (key(a) - key(b)).abs().numpy()
 
 
 @pytest.mark.parametrize("rows", [1, 8])
