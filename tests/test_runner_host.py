@@ -42,3 +42,31 @@ def test_graph_bucket_state_checks():
         bucket.replay()
     with pytest.raises(RuntimeError, match="needs a GPU"):
         bucket.capture(lambda: torch.zeros(1))
+
+
+def _bare_runner(norm):
+    from nanopointllm_amd.runner import W8A8LlamaRunner
+
+    runner = W8A8LlamaRunner.__new__(W8A8LlamaRunner)
+    nn.Module.__init__(runner)
+    runner.norm = norm
+    return runner
+
+
+def test_final_norm_routing():
+    """Binary32 rows (or a norm weight of another dtype) run the model's own
+    norm module on dtype(hidden + residual); 16-bit rows with a matching
+    weight go to the activation prologue kernel, which has no host path."""
+    from nanopointllm_amd.workloads import RMSNorm
+
+    norm = RMSNorm(8)
+    with torch.no_grad():
+        norm.weight.copy_(torch.linspace(0.5, 1.5, 8))
+    runner = _bare_runner(norm)
+    h, r = torch.randn(3, 8), torch.randn(3, 8)
+    with torch.no_grad():
+        assert torch.equal(runner.final_norm(h, r), norm(r + h))
+        assert torch.equal(runner.final_norm(h, None), norm(h))
+    half = _bare_runner(RMSNorm(8, dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="only on the GPU"):
+        half.final_norm(h.half(), r.half())
