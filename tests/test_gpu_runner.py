@@ -8,7 +8,8 @@ Bars:
 * the runner equals the chain of its primitives bit for bit, and the same
   rows give the same bits whether they run as one prefill batch (MFMA GEMM),
   in decode chunks of 8 (GEMV) or one by one (fused decode kernel) when the
-  attention core is row-local;
+  attention core is row-local, for binary16 and bfloat16 models; the
+  carried residual gives the bits of the per-layer add in both dtypes;
 * every replay of a captured decode step equals the eager step for the same
   input, with eager work and synchronizations between the replays;
 * the final residual add + norm (one prologue launch) gives the oracle's
@@ -37,7 +38,8 @@ def note(msg):
     sys.__stderr__.flush()
 
 
-def _model(cuda, *, hidden=256, heads=4, kv_heads=2, inter=384, vocab=512, layers=2, seed=0):
+def _model(cuda, *, hidden=256, heads=4, kv_heads=2, inter=384, vocab=512, layers=2, seed=0,
+           dtype=torch.float16):
     g = torch.Generator().manual_seed(seed)
     m = LlamaShaped(hidden=hidden, heads=heads, kv_heads=kv_heads, intermediate=inter,
                     vocab=vocab, layers=layers)
@@ -49,7 +51,7 @@ def _model(cuda, *, hidden=256, heads=4, kv_heads=2, inter=384, vocab=512, layer
                 p.copy_(torch.randn(p.shape, generator=g))
             else:
                 p.copy_(torch.randn(p.shape, generator=g) / p.shape[-1] ** 0.5)
-    return m.to(device=cuda, dtype=torch.float16)
+    return m.to(device=cuda, dtype=dtype)
 
 
 def _expand_kv(t, heads):
@@ -184,19 +186,36 @@ def test_rows_give_the_same_bits_on_every_kernel_path(cuda, llama7b_layer):
     singles = torch.cat([runner(inputs_embeds=x[:, i:i + 1]) for i in range(0, 12)], dim=1)
     assert torch.equal(whole[:, :12], singles)
 
+def test_bf16_rows_give_the_same_bits_on_every_kernel_path(cuda):
+    """As above for a bfloat16 model: one prefill batch (MFMA GEMM), decode
+    chunks of 8 and single rows (fused decode kernels) give the same bits."""
+    model = _model(cuda, hidden=4096, heads=32, kv_heads=32, inter=11008, vocab=256, layers=1,
+                   seed=17, dtype=torch.bfloat16)
+    runner = _runner(model, rowlocal_core)
+    x = torch.randn(1, 80, 4096, generator=torch.Generator().manual_seed(4)).bfloat16().to(cuda)
+    note("bf16 runner rows: prefill GEMM vs decode chunks of 8 vs single rows")
+    whole = runner(inputs_embeds=x)
+    assert whole.dtype == torch.bfloat16
+    chunks = torch.cat([runner(inputs_embeds=x[:, i:i + 8]) for i in range(0, 80, 8)], dim=1)
+    assert torch.equal(whole, chunks)
+    singles = torch.cat([runner(inputs_embeds=x[:, i:i + 1]) for i in range(0, 6)], dim=1)
+    assert torch.equal(whole[:, :6], singles)
 
-@pytest.mark.parametrize("rows", [1, 8, 40])
-def test_carried_residual_equals_the_per_layer_add(cuda, rows):
+
+@pytest.mark.parametrize("rows,dtype", [(1, torch.float16), (8, torch.float16),
+                                        (40, torch.float16), (8, torch.bfloat16),
+                                        (40, torch.bfloat16)])
+def test_carried_residual_equals_the_per_layer_add(cuda, rows, dtype):
     """The runner leaves each layer's final residual add to the next layer's
     RMSNorm + QKV launch (forward_carry); two LLaMA-7B-size layers, so the
     second QKV takes the carried residual, on the fused decode kernel (rows 1
     and 8) and the prologue + GEMM route (40 rows).  Bits equal to a stack of
     the reference-form layer.forward calls (lightweight_runner.py:552)."""
     model = _model(cuda, hidden=4096, heads=32, kv_heads=32, inter=11008, vocab=256, layers=2,
-                   seed=11)
+                   seed=11, dtype=dtype)
     runner = _runner(model, rowlocal_core)
-    x = torch.randn(1, rows, 4096, generator=torch.Generator().manual_seed(rows)).half().to(cuda)
-    note(f"carried residual vs per-layer add, rows={rows}")
+    x = torch.randn(1, rows, 4096, generator=torch.Generator().manual_seed(rows)).to(dtype).to(cuda)
+    note(f"carried residual vs per-layer add, rows={rows}, {dtype}")
     got = runner(inputs_embeds=x)
     h = x
     for layer in runner.layers:
