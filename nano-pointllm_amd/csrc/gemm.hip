@@ -16,7 +16,9 @@
 //     workgroup tile is a WM x WN grid of wavefronts: 128x256 (8 wavefronts
 //     of 64x64) when there are enough such tiles to fill every CU twice, else
 //     128x128 (16 wavefronts of 32x32), else 64x64 (4 wavefronts of 32x32,
-//     4 workgroups per CU) when 128x128 tiles would not cover every CU.
+//     4 workgroups per CU) when 128x128 tiles would not cover every CU; past
+//     64 rows, 64x32 (4 wavefronts of 32x16) when those fill one round.  The
+//     full rule is at launch_t.
 //   * Both operands are in the packed 16x64 tile layout, so a k-step (64) of
 //     the workgroup tile is (BM + BN)/16 fragments of 1 KiB.  Each wavefront
 //     copies its share with global_load_lds_dwordx4 straight into a 3- or
@@ -354,6 +356,11 @@ hipError_t launch_cfg(GemmParams p, hipStream_t st) {
 // cold weights, LLaMA-7B projections at M = 256..2048).  A launch is fastest
 // when its tiles fill one round of workgroup slots (2 per CU) as closely as
 // possible, and when several rounds are needed, with the widest tile:
+//   * past 64 rows (M > 64), 64x32 tiles (4 waves of 32x16, a 3-stage ring of
+//     four k-blocks, 2 workgroups per CU) when they fit in one round and
+//     number at least half the CUs: O and down at M = 65..128 13-16% faster
+//     than the tiles below, 4-10% at M = 160..256, N = 2048 14%; beyond one
+//     round (N = 8192 past M = 128) they lose;
 //   * 128x128 tiles, when they fit in one round: 16 waves of 32x32, a
 //     4-stage ring of one k-block (64 K), 2 workgroups per CU, when there
 //     are more of them than CUs; else (one tile per CU or less, where every
@@ -365,7 +372,7 @@ hipError_t launch_cfg(GemmParams p, hipStream_t st) {
 //     M = 384, with weights streamed from HBM).  With at most one 64x64 tile
 //     per CU, 32x32 tiles of one wave (a 3-stage ring of four k-blocks, 3 per
 //     CU by LDS) spread the work over more CUs when they fit in one round:
-//     9-13% faster on QKV at M = 64 and on O and down at M = 128;
+//     9-13% faster on QKV at M = 64;
 //   * else the widest of 128x192, 128x224 and 128x256 whose tiles still fit
 //     in one round, trying the narrowest first (8 waves of 32x96, 32x112 or
 //     64x64, 3-stage ring): 128x224 takes gate/up at M = 560 in 495 tiles,
@@ -395,6 +402,8 @@ hipError_t launch_t(const GemmParams& p, hipStream_t st) {
       return launch_cfg<4, 2, 2, 7, 3, 2, 1, EPI, TY, TH>(p, st);
     case kGemmW256Sq:
       return launch_cfg<4, 4, 4, 4, 2, 1, 2, EPI, TY, TH>(p, st);
+    case kGemmMid:
+      return launch_cfg<2, 2, 2, 1, 3, 2, 4, EPI, TY, TH>(p, st);
     default:
       return launch_cfg<2, 4, 4, 4, 3, 2, 1, EPI, TY, TH>(p, st);
   }
@@ -407,6 +416,8 @@ int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus) {
   const int64_t tiles_m = ceil_div(MB, 8);  // 128-row tiles
   const int64_t big_tiles = tiles_m * ceil_div(NB, 8);
   if (big_tiles <= slots) {
+    const int64_t mid_tiles = ceil_div(MB, 4) * ceil_div(NB, 2);
+    if (MB > 4 && 2 * mid_tiles >= cus && mid_tiles <= slots) return kGemmMid;
     if (big_tiles > cus) return kGemmBig;
     const int64_t small_tiles = ceil_div(MB, 4) * ceil_div(NB, 4);
     if (small_tiles <= cus && ceil_div(MB, 2) * ceil_div(NB, 2) <= 3 * cus) return kGemmTinyDeep;

@@ -108,6 +108,7 @@ enum GemmTile : int {
   kGemmW224 = 5,       // 128x224, 8 waves
   kGemmW256 = 6,       // 128x256, 8 waves
   kGemmW256Sq = 7,     // 256x256, 16 waves, 2-stage ring of two k-blocks, 1 per CU
+  kGemmMid = 8,        // 64x32, 4 waves, 3-stage ring of four k-blocks, 2 per CU
 };
 int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus);
 

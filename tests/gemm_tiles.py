@@ -6,7 +6,7 @@ machine without a GPU."""
 from __future__ import annotations
 
 CONFIG_NAMES = ("tiny-deep", "small-deep", "big-deep", "big", "w192", "w224", "w256",
-                "w256sq")
+                "w256sq", "mid")
 
 
 def gemm_config(m: int, n: int, cus: int = 256) -> str:

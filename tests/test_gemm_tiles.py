@@ -16,7 +16,8 @@ QKV, O, GATEUP, DOWN = 12288, 4096, 22016, 4096
     (560, QKV, "big"), (768, QKV, "w192"), (1024, QKV, "w192"), (2048, QKV, "w256"),
     (560, O, "big-deep"), (768, O, "big-deep"), (1024, O, "big-deep"),
     (560, GATEUP, "w224"), (768, GATEUP, "big"), (1024, GATEUP, "w256"),
-    (64, QKV, "tiny-deep"), (128, O, "tiny-deep"), (256, O, "small-deep"),
+    (64, QKV, "tiny-deep"), (128, O, "mid"), (256, O, "mid"), (65, DOWN, "mid"),
+    (100, 1000, "tiny-deep"), (160, 8192, "small-deep"), (128, 8192, "mid"),
     (256, QKV, "big-deep"), (384, GATEUP, "w192"), (8192, 8192, "w256sq"),
     (2048, GATEUP, "w256sq"), (2040, GATEUP, "w256sq"),
     (2050, GATEUP, "w256"), (4096, O, "w256"), (4096, QKV, "w256sq"),
@@ -43,6 +44,13 @@ def test_every_config_fits_one_round_or_is_the_widest():
             if cfg == "w256sq":
                 assert tiles["w256"] > 512 and -(-mb // 16) * -(-nb // 16) >= 512
                 assert 2 * -(-mb // 16) == tm
+    # 64x32 tiles only past 64 rows, within one round and on at least half the CUs.
+    for m in range(17, 1025, 13):
+        for n in (1000, 2048, 4096, 8192, 12288, 22016):
+            mb, nb = -(-m // 16), -(-n // 16)
+            mid = -(-mb // 4) * -(-nb // 2)
+            fits = mb > 4 and 128 <= mid <= 512 and -(-mb // 8) * -(-nb // 8) <= 512
+            assert (gemm_config(m, n) == "mid") == fits, (m, n)
 
 
 def test_query_rejects_empty_or_oversized_problems():

@@ -1,8 +1,10 @@
 """Prefill GEMM shapes with at most one round of tiles, which select ring
-stages of several k-blocks: one-wave 32x32 tiles with stages of four k-blocks
-(256 K) when there is at most one 64x64 tile per CU, else the 64x64 tile with
-stages of four k-blocks when its tiles fit in two per CU, else the 128x128
-tile with stages of two k-blocks (128 K) and one workgroup per CU.
+stages of several k-blocks: past 64 rows, 64x32 tiles (stages of four
+k-blocks, two workgroups per CU) when they fill one round on at least half
+the CUs; else one-wave 32x32 tiles with stages of four k-blocks (256 K) when
+there is at most one 64x64 tile per CU, else the 64x64 tile with stages of
+four k-blocks when its tiles fit in two per CU, else the 128x128 tile with
+stages of two k-blocks (128 K) and one workgroup per CU.
 
 Bars as for every GEMM path: int32 accumulators bit-exact against the
 oracle's integer product; binary16 / bfloat16 dequant outputs bit-equal to the
@@ -63,8 +65,13 @@ SHAPES = [
     (300, 6000, 11008, "small-deep"),
     (300, 6000, 4250, "small-deep"),
     (100, 1000, 4250, "tiny-deep"),
-    (65, 8000, 70, "tiny-deep"),
-    (128, 4096, 11008, "tiny-deep"),
+    (64, 12288, 4250, "tiny-deep"),
+    (48, 9000, 70, "tiny-deep"),
+    (65, 8000, 70, "mid"),
+    (128, 4096, 11008, "mid"),
+    (96, 4100, 4197, "mid"),
+    (200, 2048, 3100, "mid"),
+    (256, 4096, 4250, "mid"),
 ]
 
 
@@ -88,12 +95,13 @@ def test_deep_stage_int32_and_dequant(cuda, m, n, k, cfg):
                                           err_msg=f"{dt} bias={b is not None}")
 
 
-@pytest.mark.parametrize("m,inter,k", [(560, 2000, 4197), (300, 3000, 4250), (100, 500, 4250)])
+@pytest.mark.parametrize("m,inter,k", [(560, 2000, 4197), (300, 3000, 4250), (100, 500, 4250),
+                                      (96, 2048, 4197)])
 def test_deep_stage_silu_mul_and_int8_chain(cuda, m, inter, k):
     from nanopointllm_amd import _lib, w8a8
 
     cfg = _config(m, 2 * inter)
-    assert cfg in ("big-deep", "small-deep", "tiny-deep")
+    assert cfg in ("big-deep", "small-deep", "tiny-deep", "mid")
     xq, wq, sx, sw, _ = _case(m, 2 * inter, k, seed=7 + k)
     note(f"gemm {cfg} silu m={m} inter={inter} k={k}")
     wp = w8a8.pack_rows(wq.to(cuda), _lib.ROWS_INTERLEAVE_HALVES)
@@ -114,11 +122,12 @@ def test_deep_stage_silu_mul_and_int8_chain(cuda, m, inter, k):
     np.testing.assert_array_equal(hq.cpu().numpy(), eq)
 
 
-@pytest.mark.parametrize("m,n,k", [(560, 4000, 4197), (300, 6000, 4250), (100, 1000, 4250)])
+@pytest.mark.parametrize("m,n,k", [(560, 4000, 4197), (300, 6000, 4250), (100, 1000, 4250),
+                                   (128, 4096, 3100)])
 def test_deep_stage_requant1_epilogue(cuda, m, n, k):
     from nanopointllm_amd import integer_epilogues as E, w8a8
 
-    assert _config(m, n) in ("big-deep", "small-deep", "tiny-deep")
+    assert _config(m, n) in ("big-deep", "small-deep", "tiny-deep", "mid")
     xq, wq, _, sw, _ = _case(m, n, k, seed=5 + k)
     comp = [O.compile_fp16_requant_scale(0.02, float(w), 0.5) for w in sw]
     mult = np.array([c[0] for c in comp], np.uint32)
