@@ -41,7 +41,9 @@ constexpr int kFusedCH = 4;
 // Weight ring steps issued before x is quantized (the others follow it).
 constexpr int kFusedPreSteps = 1;
 // Raw buffer loads: descriptor word 3 of gfx9 (32-bit data format), the
-// nontemporal cache policy and the bytes of one 16 x 64 packed k-block.
+// nontemporal cache policy (each weight byte is read once: 6% faster than the
+// default policy on gate/up at M = 8) and the bytes of one 16 x 64 packed
+// k-block.
 constexpr int kBufferWord3 = 0x00020000;
 constexpr int kCacheNT = 2;
 constexpr int kBlockBytes = 1024;
