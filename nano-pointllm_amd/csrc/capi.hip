@@ -520,15 +520,13 @@ int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* res
   int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
   const int64_t kp = round_up(k, kTileK);
   const bool gemv = use_gemv(m, n);
+  // The GEMV reads whole 64-column blocks: the prologue writes zeros in the
+  // pad columns K..kp of its row-major rows.
   hipError_t e = launch_prologue_quant(x, x_dtype, ldx, residual, ld_residual, residual_out,
                                        ld_residual_out, norm_weight, x_dtype, eps, nullptr,
-                                       nullptr, m, k, act, kp, sx, x_out, ld_x_out, stream, !gemv);
+                                       nullptr, m, k, act, kp, sx, x_out, ld_x_out, stream, !gemv,
+                                       kp);
   if (e != hipSuccess) return status_of(e);
-  if (gemv && kp > k) {
-    // The GEMV reads whole 64-column blocks: zero the pad columns.
-    e = launch_pad_rows(act, m, k, kp, act, kp, stream);
-    if (e != hipSuccess) return status_of(e);
-  }
   op.a = act;
   op.lda = kp;
   op.sx = sx;

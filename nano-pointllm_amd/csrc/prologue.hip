@@ -53,6 +53,9 @@ struct PrologueParams {
   // the GEMM with KB k-blocks; the grid then covers ceil(M/16)*16 rows and
   // every row writes all KB*64 columns (zeros past K and in the pad rows).
   int64_t KB;
+  // Row-major q: columns written per row, K <= q_cols <= ldq, zeros past K
+  // (the GEMV reads whole 64-column blocks).
+  int64_t q_cols;
 };
 
 __device__ inline bool aligned16(const void* p) {
@@ -227,8 +230,9 @@ __device__ inline void prologue_vec(const PrologueParams& p, float* red) {
     }
     if (p.KB > 0) {
       if (k0 < p.KB * kTileK) *reinterpret_cast<u32x2*>(p.q + packed_offset(row, k0, p.KB)) = qw;
-    } else if (k0 < K) {
-      *reinterpret_cast<u32x2*>(p.q + row * p.ldq + k0) = qw;
+    } else if (k0 < p.q_cols) {
+      // K % 8 == 0 here: a chunk lies wholly before K or wholly past it.
+      *reinterpret_cast<u32x2*>(p.q + row * p.ldq + k0) = k0 < K ? qw : u32x2{0u, 0u};
     }
     if (p.x_out != nullptr && k0 < K) {
       TY* xo = static_cast<TY*>(p.x_out) + row * p.ld_xout + k0;
@@ -370,7 +374,7 @@ __global__ __launch_bounds__(kProThreads) void prologue_quant_kernel(ProloguePar
 #pragma unroll
   for (int c = 0; c < REG; ++c) {
     const int64_t k0 = (tid + static_cast<int64_t>(c) * kProThreads) * 8;
-    if (k0 >= K) continue;
+    if (k0 >= p.q_cols) continue;
     int8_t* qr = p.q + row * p.ldq + k0;
     TY* xo = p.x_out != nullptr ? static_cast<TY*>(p.x_out) + row * p.ld_xout + k0 : nullptr;
 #pragma unroll
@@ -378,6 +382,8 @@ __global__ __launch_bounds__(kProThreads) void prologue_quant_kernel(ProloguePar
       if (k0 + j < K) {
         qr[j] = static_cast<int8_t>(fast ? quant1_h(v[c][j], s, r) : quant1(v[c][j], s));
         if (xo != nullptr) xo[j] = from_f32<TY>(v[c][j]);
+      } else if (k0 + j < p.q_cols) {
+        qr[j] = 0;
       }
     }
   }
@@ -431,11 +437,16 @@ hipError_t launch_prologue_quant(const void* x, int x_dtype, int64_t ldx, const 
                                  const void* norm_weight, int w_dtype, float eps,
                                  const void* smooth, const float* static_scale, int64_t M,
                                  int64_t K, int8_t* q, int64_t ldq, float* scales_out,
-                                 void* x_out, int64_t ld_xout, hipStream_t st, bool packed) {
+                                 void* x_out, int64_t ld_xout, hipStream_t st, bool packed,
+                                 int64_t q_cols) {
+  if (q_cols < K) q_cols = K;
   PrologueParams p{x,          ldx, residual, ld_res, residual_out, ld_res_out, norm_weight,
                    eps,        smooth, static_scale, M, K, q, ldq, scales_out, x_out,
-                   ld_xout,    packed ? ceil_div(K, kTileK) : 0};
+                   ld_xout,    packed ? ceil_div(K, kTileK) : 0, q_cols};
   if (M == 0 || K == 0) return hipSuccess;
+  // Every chunk a row writes lies inside the launch's coverage: q_cols is at
+  // most round_up(K, 64), and the per-thread passes cover multiples of 4096.
+  if (!packed && (q_cols > ldq || q_cols > ceil_div(K, kTileK) * kTileK)) return hipErrorInvalidValue;
   const bool w32 = norm_weight != nullptr && w_dtype == kF32;
   if (x_dtype == kF16)
     return w32 ? launch_tw<__half, float>(p, st) : launch_tw<__half, __half>(p, st);

@@ -51,8 +51,9 @@ struct LinearOperands {
 // q [M, ldq] (K columns), or with `packed` the GEMM's 16x64 tiles
 // (ceil(M/16)*16 rows x ceil(K/64)*64 columns, zero padded; ldq unused),
 // scales_out [M] (nullable), x_out [M, ld_xout] (nullable) receives the rows
-// before quantization (x's dtype, or F32 with an F32 RMSNorm weight).
-// K <= prologue_max_k().
+// before quantization (x's dtype, or F32 with an F32 RMSNorm weight).  The
+// row-major q gets q_cols columns per row (at least K, at most
+// min(ldq, round_up(K, 64))), zeros past K.  K <= prologue_max_k().
 int64_t prologue_max_k();
 hipError_t launch_prologue_quant(const void* x, int x_dtype, int64_t ldx, const void* residual,
                                  int64_t ld_res, void* residual_out, int64_t ld_res_out,
@@ -60,7 +61,7 @@ hipError_t launch_prologue_quant(const void* x, int x_dtype, int64_t ldx, const 
                                  const void* smooth, const float* static_scale, int64_t M,
                                  int64_t K, int8_t* q, int64_t ldq, float* scales_out,
                                  void* x_out, int64_t ld_xout, hipStream_t st,
-                                 bool packed = false);
+                                 bool packed = false, int64_t q_cols = 0);
 
 // Elementwise epilogues over caller int32 accumulators acc[m, ld_acc]:
 // requant1 per element with per-column multiplier / shift / bias (nullable)
@@ -109,6 +110,8 @@ enum GemmTile : int {
   kGemmW256 = 6,       // 128x256, 8 waves
   kGemmW256Sq = 7,     // 256x256, 16 waves, 2-stage ring of two k-blocks, 1 per CU
   kGemmMid = 8,        // 64x32, 4 waves, 3-stage ring of four k-blocks, 2 per CU
+  kGemmWd7x2 = 9,      // 112x256 weights-direct, 8 waves of 112x32, 4 k-blocks ahead, 1 per CU
+  kGemmWd9x1 = 10,     // 144x64 weights-direct, 4 waves of 144x16, 6 k-blocks ahead, 1 per CU
 };
 int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus);
 

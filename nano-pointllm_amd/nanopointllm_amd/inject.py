@@ -24,7 +24,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from .linear import W8A8GateUpSiluMul, W8A8Linear, W8A8MLP, W8A8PackedQKV
+from .linear import W8A8GateUpSiluMul, W8A8Linear, W8A8MLP, W8A8PackedQKV, _rows2
 
 _ATTN_LINEARS = ("q_proj", "k_proj", "v_proj", "o_proj")
 _MLP_LINEARS = ("gate_proj", "up_proj", "down_proj")
@@ -137,7 +137,7 @@ def rmsnorm_packed_qkv_decode(hidden_states: torch.Tensor, norm: nn.Module, qkv:
     QKV product, one kernel at decode shapes (``w8a8_rmsnorm_linear``, the W8A8
     form of ``_rmsnorm_packed_qkv_kernel``, :163-234).  Returns q, k, v views
     like the reference."""
-    rows = hidden_states[0] if hidden_states.dim() == 3 else hidden_states
+    rows = _rows2(hidden_states)
     if not rows.is_contiguous():
         rows = rows.contiguous()
     return qkv.project_rmsnorm(rows, norm)
@@ -151,8 +151,8 @@ def residual_rmsnorm_mlp_decode(hidden_states: torch.Tensor, residual: torch.Ten
     and per-token quantization are one kernel; returns ``(residual, mlp_out)``
     with the reference's ``[1, B, H]`` staging for 3-D inputs."""
     three_d = hidden_states.dim() == 3
-    rows = hidden_states[0] if three_d else hidden_states
-    res = residual[0] if three_d else residual
+    rows = _rows2(hidden_states)
+    res = _rows2(residual)
     summed, out = mlp.forward_residual_rmsnorm(rows.contiguous(), res.contiguous(), norm)
     if three_d:
         return summed.unsqueeze(0), out.unsqueeze(0)

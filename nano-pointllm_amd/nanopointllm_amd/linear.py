@@ -93,12 +93,25 @@ def _interleave_halves(v: torch.Tensor) -> torch.Tensor:
 
 
 def _norm_eps(norm: nn.Module) -> float:
-    return float(getattr(norm, "variance_epsilon", getattr(norm, "eps", 1.0e-6)))
+    """The epsilon of a LightweightRMSNorm (``variance_epsilon``,
+    lightweight_runner.py:229-236) or of a norm that names it ``eps``."""
+    for name in ("variance_epsilon", "eps"):
+        eps = getattr(norm, name, None)
+        if eps is not None:
+            return float(eps)
+    raise ValueError("the norm module has no epsilon (variance_epsilon or eps)")
 
 
 def _rows2(hidden_states: torch.Tensor) -> torch.Tensor:
-    """``[1, T, hidden]`` (the reference's staged decode layout) -> ``[T, hidden]``."""
-    return hidden_states[0] if hidden_states.dim() == 3 else hidden_states
+    """``[1, T, hidden]`` (the reference's staged decode layout) or
+    ``[T, hidden]`` -> ``[T, hidden]``."""
+    if hidden_states.dim() == 3:
+        if hidden_states.shape[0] != 1:
+            raise ValueError("hidden states must be [1, tokens, hidden] or [tokens, hidden]")
+        return hidden_states[0]
+    if hidden_states.dim() != 2:
+        raise ValueError("hidden states must be [1, tokens, hidden] or [tokens, hidden]")
+    return hidden_states
 
 
 def _linear_parts(module: nn.Module) -> tuple[torch.Tensor, torch.Tensor | None]:
@@ -192,8 +205,7 @@ class W8A8PackedQKV(nn.Module):
     def project(self, hidden_states: torch.Tensor
                 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         """``_project_qkv_decode_packed`` (paged_attention.py:97-115) semantics."""
-        staged = hidden_states[0] if hidden_states.dim() == 3 else hidden_states
-        return self._split(self.linear(staged))
+        return self._split(self.linear(_rows2(hidden_states)))
 
     def project_i8(self, xq: torch.Tensor, x_scale: torch.Tensor, *,
                    out_dtype: torch.dtype = torch.float16
@@ -207,7 +219,7 @@ class W8A8PackedQKV(nn.Module):
         """``_rmsnorm_staged_packed_qkv_decode`` (paged_attention.py:283-305):
         ``norm`` (a LightweightRMSNorm / LlamaRMSNorm) applied to the rows,
         then the packed QKV projection, one kernel at decode shapes."""
-        staged = hidden_states[0] if hidden_states.dim() == 3 else hidden_states
+        staged = _rows2(hidden_states)
         lin = self.linear.weight_q
         out = _w.rmsnorm_linear(staged, norm.weight, _norm_eps(norm), lin.packed, lin.scale,
                                 lin.bias, lin.out_features, in_features=lin.in_features)
@@ -367,7 +379,14 @@ class W8A8MLP(nn.Module):
         """``post_attention_layernorm.residual_norm`` then the MLP
         (lightweight_runner.py:247-257, 320-383), with the residual add and
         RMSNorm inside the gate/up launch at decode shapes.  Returns
-        ``(hidden_states + residual, mlp output)``."""
+        ``(hidden_states + residual, mlp output)``.
+
+        ``two_phase`` has no effect here: this route always hands the 16-bit
+        ``h`` to the down projection, which quantizes it per token in its own
+        launch.  The two-phase route gives the same bits (it quantizes the
+        same ``h`` with the same per-token scales) and would add a launch to
+        this one, since the fused norm kernel does not write the partial
+        row maxima."""
         p = self.gate_up.weight_q
         epi = _lib.EPI_SILU_MUL if self.h_scale is None else _lib.EPI_SILU_MUL_Q8
         first = _w.rmsnorm_linear(hidden_states, norm.weight, _norm_eps(norm), p.packed, p.scale,
@@ -406,8 +425,7 @@ class W8A8RMSNormQuant(nn.Module):
     def __init__(self, norm: nn.Module) -> None:
         super().__init__()
         self.weight = norm.weight
-        self.variance_epsilon = float(getattr(norm, "variance_epsilon",
-                                              getattr(norm, "eps", 1.0e-6)))
+        self.variance_epsilon = _norm_eps(norm)
 
     def forward(self, hidden_states: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         return _w.rmsnorm_quant(hidden_states, self.weight, self.variance_epsilon)

@@ -107,7 +107,9 @@ def test_rmsnorm_linear_random_case(cuda, case):
     res_out = torch.empty(m, k, dtype=tdt, device=cuda)
     sx = torch.empty(m, dtype=torch.float32, device=cuda)
     lib = _lib.load()
-    ws = torch.empty(lib.w8a8_workspace_bytes(m, k), dtype=torch.uint8, device=cuda)
+    # Poisoned: the int8 rows' pad columns (K up to the next multiple of 64)
+    # must be written as zeros by the call itself.
+    ws = torch.full((lib.w8a8_workspace_bytes(m, k),), 0x5A, dtype=torch.uint8, device=cuda)
     ptr = lambda t: None if t is None else t.data_ptr()
     note(f"rmsnorm_linear sweep {_ids(case)}")
     rc = lib.w8a8_rmsnorm_linear(

@@ -49,6 +49,9 @@ CASES = [
     ("gemv", 40, 2752, 1024, False),
     ("gemm", 567, 2752, 1024, False),
     ("gemm-i8", 200, 520, 704, True),
+    # int8 rows with K > 8192: the fused kernel's stream on int8 x.
+    ("fused-i8-deep", 8, 1376, 11008, True),
+    ("fused-i8-deep", 3, 1376, 9216, True),
 ]
 
 
@@ -147,3 +150,58 @@ def test_two_phase_argument_checks(cuda):
                                        p.out_features)
     with pytest.raises(ValueError, match="even"):
         w8a8.gateup_silu_mul_two_phase(x, p.packed, p.scale, None, p.out_features - 1)
+
+
+# Full-size LLaMA-7B packed gate/up (22016 x 4096): the GEMM tiles the
+# library picks at these row counts, each run with the per-block maxima of h.
+FULL_M = [560, 567, 768, 1024, 2048]
+
+
+@pytest.fixture(scope="module")
+def gateup_full(cuda):
+    return _gateup(11008, 4096, seed=77, cuda=cuda)
+
+
+@pytest.fixture(scope="module")
+def down_full(cuda):
+    from nanopointllm_amd.linear import PackedW8A8Weight
+
+    g = torch.Generator().manual_seed(78)
+    w = (torch.randn(4096, 11008, generator=g) * 0.02).to(torch.float16)
+    _, qd, sd = O.per_output_weight_qdq(w.float().numpy())
+    return PackedW8A8Weight.from_float(w.to(cuda)), qd, sd
+
+
+def test_full_size_tiles_are_covered():
+    from gemm_tiles import gemm_config
+
+    tiles = {gemm_config(m, 22016) for m in FULL_M}
+    assert len(tiles) >= 4, tiles
+
+
+@pytest.mark.parametrize("m", FULL_M)
+def test_two_phase_full_size_gateup(cuda, gateup_full, down_full, m):
+    """h equals the plain SiLU*mul linear, hq and its scales are bit-exact
+    against the oracle's per-token quantization of that h, and the down
+    projection on hq is exact against the oracle (on a sample of rows)."""
+    from gemm_tiles import gemm_config
+    from nanopointllm_amd import _lib, w8a8, workloads as W
+
+    p = gateup_full
+    x = W.prefill_activations(m, 4096, seed=m, point_tokens=min(513, m - 7)).to(cuda)
+    note(f"two-phase full size m={m} tile={gemm_config(m, 22016)}")
+    plain = w8a8.linear_dynamic(x, p.packed, p.scale, p.bias, p.out_features,
+                                epilogue=_lib.EPI_SILU_MUL)
+    out = w8a8.gateup_silu_mul_two_phase(x, p.packed, p.scale, p.bias, p.out_features)
+    h = plain.cpu().numpy()
+    np.testing.assert_array_equal(out.h.cpu().numpy(), h)
+    eq, es = O.dynamic_per_token_quant(h.astype(np.float32))
+    hq = out.hq.cpu().numpy()
+    np.testing.assert_array_equal(hq, eq)
+    np.testing.assert_array_equal(out.scale.cpu().numpy(), es[:, 0])
+    dp, qd, sd = down_full
+    y = w8a8.linear_i8in(out.hq, out.scale.reshape(-1), dp.packed, dp.scale, None,
+                         dp.out_features, out_dtype=torch.float16).cpu().numpy()
+    rows = np.unique(np.linspace(0, m - 1, 48).astype(int))
+    exp, _ = O.linear_from_quantized(hq[rows], es[rows], qd, sd)
+    np.testing.assert_array_equal(y[rows], exp.astype(np.float16))

@@ -70,3 +70,56 @@ def test_final_norm_routing():
     half = _bare_runner(RMSNorm(8, dtype=torch.float16))
     with pytest.raises(RuntimeError, match="only on the GPU"):
         half.final_norm(h.half(), r.half())
+
+
+def test_rows2_and_norm_eps_refuse_what_they_cannot_serve():
+    """The staged-decode helpers take ``[1, T, H]`` or ``[T, H]`` only (a
+    batch other than 1 would silently drop rows), and a norm without an
+    epsilon attribute is refused rather than given a default."""
+    from types import SimpleNamespace
+
+    from nanopointllm_amd.linear import _norm_eps, _rows2
+
+    assert _rows2(torch.zeros(1, 5, 8)).shape == (5, 8)
+    assert _rows2(torch.zeros(5, 8)).shape == (5, 8)
+    with pytest.raises(ValueError, match="tokens, hidden"):
+        _rows2(torch.zeros(2, 5, 8))
+    with pytest.raises(ValueError, match="tokens, hidden"):
+        _rows2(torch.zeros(8))
+    assert _norm_eps(SimpleNamespace(variance_epsilon=1e-5)) == 1e-5
+    assert _norm_eps(SimpleNamespace(eps=3e-6)) == 3e-6
+    with pytest.raises(ValueError, match="no epsilon"):
+        _norm_eps(SimpleNamespace(weight=None))
+
+
+def test_fused_norm_mlp_keeps_the_plain_chain_with_two_phase(monkeypatch):
+    """``W8A8MLP.forward_residual_rmsnorm`` hands the fused norm + gate/up
+    launch's 16-bit h to down's own per-token quantization whether or not
+    ``two_phase`` is set (same bits either way); the two-phase gate/up is
+    not called."""
+    from types import SimpleNamespace
+
+    from nanopointllm_amd import _lib, linear
+
+    calls = []
+
+    def fake_rmsnorm_linear(x, w, eps, packed, scale, bias, n, **kw):
+        calls.append(("rmsnorm_linear", kw.get("epilogue"), kw.get("residual") is not None))
+        return SimpleNamespace(y="h", residual="summed")
+
+    monkeypatch.setattr(linear._w, "rmsnorm_linear", fake_rmsnorm_linear)
+    for two_phase in (False, True):
+        calls.clear()
+        mlp = linear.W8A8MLP.__new__(linear.W8A8MLP)
+        nn.Module.__init__(mlp)
+        mlp.gate_up = SimpleNamespace(
+            weight_q=SimpleNamespace(packed=None, scale=None, bias=None, out_features=16,
+                                     in_features=8),
+            forward_two_phase=lambda *a, **k: calls.append("two_phase"))
+        mlp.down = lambda h: calls.append(("down", h)) or "y"
+        mlp.h_scale = None
+        mlp.two_phase = two_phase
+        norm = SimpleNamespace(weight=None, variance_epsilon=1e-6)
+        out = mlp.forward_residual_rmsnorm("x", "r", norm)
+        assert out == ("summed", "y")
+        assert calls == [("rmsnorm_linear", _lib.EPI_SILU_MUL, True), ("down", "h")]

@@ -93,3 +93,41 @@ def test_noalloc_refuses_more_than_its_scratch(cuda):
     sx = torch.empty(m, device=cuda)
     note("noalloc refuses an oversized problem")
     assert _call("w8a8_linear_noalloc", x, wp, sw, None, n, 1, y, sx) == _lib.ERR_TOO_LARGE
+
+
+def test_noalloc_graph_replays_equal_eager(cuda):
+    """Captured in a HIP graph (GEMM regime, so the scratch holds the packed
+    activations) and replayed with eager work between replays: every replay
+    equals the eager call bit for bit.  The eager call comes first, so the
+    scratch address is resolved outside the capture."""
+    m, n, k = 560, 4096, 4096
+    x, wp, sw, bias = _case(m, n, k, 5, cuda)
+    y_eager = torch.empty(m, n, dtype=torch.float16, device=cuda)
+    sx_eager = torch.empty(m, dtype=torch.float32, device=cuda)
+    note("noalloc graph capture m=560")
+    assert _call("w8a8_linear_noalloc", x, wp, sw, bias, n, 1, y_eager, sx_eager) == 0
+    torch.cuda.synchronize()
+    y = torch.full((m, n), 3, dtype=torch.float16, device=cuda)
+    sx = torch.empty(m, dtype=torch.float32, device=cuda)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        assert _call("w8a8_linear_noalloc", x, wp, sw, bias, n, 1, y, sx) == 0
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = _call("w8a8_linear_noalloc", x, wp, sw, bias, n, 1, y, sx)
+    assert rc == 0
+    for rep in range(3):
+        y.fill_(7)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y, y_eager), rep
+        assert torch.equal(sx, sx_eager), rep
+        # Eager work on the same scratch between replays: a smaller GEMV-regime call.
+        x2, wp2, sw2, _ = _case(40, 1024, 1000, 6 + rep, cuda)
+        y2 = torch.empty(40, 1024, dtype=torch.int32, device=cuda)
+        sx2 = torch.empty(40, dtype=torch.float32, device=cuda)
+        assert _call("w8a8_linear_noalloc", x2, wp2, sw2, None, 1024, 0, y2, sx2) == 0
+        torch.cuda.synchronize()
