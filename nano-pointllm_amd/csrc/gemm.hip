@@ -29,6 +29,8 @@
 //     column block land on the same XCD and share its L2.
 #include "w8a8_internal.h"
 
+#include <utility>
+
 namespace w8a8 {
 
 namespace {
@@ -80,125 +82,24 @@ __device__ inline void wait_vmcnt() {
 // overtake them; unlike __syncthreads it does not drain outstanding loads.
 __device__ inline void ring_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// WM x WN wavefronts, each owning BR x BC blocks of 16x16 (BM = 16 WM BR,
-// BN = 16 WN BC), with an STG-deep LDS ring whose stages hold KT k-blocks
-// (64 K each) of both operands.
-// The second launch bound is waves per SIMD: OCC workgroups of WM x WN
-// wavefronts over the CU's 4 SIMDs, so the register budget admits OCC
-// workgroups per CU.
-template <int WM, int WN, int BR, int BC, int STG, int OCC, int KT, int EPI, typename TY,
-          typename TH>
-__global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(GemmParams p) {
-  constexpr int NW = WM * WN;
-  constexpr int BMF = WM * BR;  // 16-row activation tiles per k-block
-  constexpr int BNF = WN * BC;  // 16-row weight tiles per k-block
-  constexpr int F = BMF + BNF;
-  constexpr int FS = F * KT;    // fragments per stage
-  // Fragment copies per wave per stage: LPW for the first FS - (LPW-1) NW
-  // waves, LPW - 1 for the rest.
-  constexpr int LPW = (FS + NW - 1) / NW;
-  __shared__ i32x4 lds[STG][FS][64];
-
-  // XCD-major tile mapping: workgroup b runs on XCD b % 8.
-  const int b = blockIdx.x;
-  const int tile = (b % kXcds) * p.per_xcd + b / kXcds;
-  if (tile >= p.tiles) return;
-  const int mb0 = (tile % p.tiles_m) * BMF;
-  const int nb0 = (tile / p.tiles_m) * BNF;
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave / WN;
-  const int wn = wave % WN;
-  const int KB = p.KB;
-  const int NS = static_cast<int>(ceil_div(KB, KT));  // ring stages over K
-
-  // Fragment f = q*NW + wave of a stage is k-block f / F of the stage; of
-  // that k-block, g = f % F < BMF are activation blocks mb0 + g, the rest
-  // weight blocks nb0 + g - BMF.  Blocks past the operand are clamped to its
-  // last block: their products only reach accumulator rows or columns that
-  // the epilogue never stores.  K-blocks past KB (the last stage of a K that
-  // is not a multiple of 64 KT) reload block KB - 1 and are not multiplied.
-  const bool full = (LPW - 1) * NW + wave < FS;  // wave-uniform
-  const i32x4* src[LPW];
-  int kk_of[LPW];
-#pragma unroll
-  for (int q = 0; q < LPW; ++q) {
-    const int f = min(q * NW + wave, FS - 1);
-    const int g = f % F;
-    kk_of[q] = f / F;
-    if (g < BMF) {
-      src[q] = p.a + static_cast<int64_t>(min(mb0 + g, p.MB - 1)) * KB * 64 + lane;
-    } else {
-      src[q] = p.w + static_cast<int64_t>(min(nb0 + g - BMF, p.NB - 1)) * KB * 64 + lane;
-    }
-  }
-  auto issue = [&](int stage, int slot) {
-#pragma unroll
-    for (int q = 0; q < LPW; ++q)
-      if (q < LPW - 1 || full) {
-        const int kb = min(stage * KT + kk_of[q], KB - 1);
-        __builtin_amdgcn_global_load_lds(
-            static_cast<const void*>(src[q] + static_cast<int64_t>(kb) * 64),
-            (lds_void*)(&lds[slot][q * NW + wave][0]), 16, 0, 0);
-      }
-  };
-
-  i32x4 acc[BR][BC];
-#pragma unroll
-  for (int i = 0; i < BR; ++i)
-#pragma unroll
-    for (int j = 0; j < BC; ++j)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0;
-
-#pragma unroll
-  for (int s = 0; s < STG - 1; ++s)
-    if (s < NS) issue(s, s);
-
-  for (int st = 0; st < NS; ++st) {
-    // Stage st has landed once only the later stages' loads may remain.
-    if (st + STG - 2 < NS) {
-      if (full) {
-        wait_vmcnt<LPW * (STG - 2)>();
-      } else {
-        wait_vmcnt<(LPW - 1) * (STG - 2)>();
-      }
-    } else {
-      wait_vmcnt<0>();
-    }
-    ring_barrier();
-    // Every wave has finished reading the slot of stage st-1: refill it.
-    if (st + STG - 1 < NS) issue(st + STG - 1, (st + STG - 1) % STG);
-    const int slot = st % STG;
-#pragma unroll
-    for (int kk = 0; kk < KT; ++kk) {
-      if (KT == 1 || st * KT + kk < KB) {
-        i32x4 af[BR], bf[BC];
-#pragma unroll
-        for (int i = 0; i < BR; ++i) af[i] = lds[slot][kk * F + wm * BR + i][lane];
-#pragma unroll
-        for (int j = 0; j < BC; ++j) bf[j] = lds[slot][kk * F + BMF + wn * BC + j][lane];
-#pragma unroll
-        for (int i = 0; i < BR; ++i)
-#pragma unroll
-          for (int j = 0; j < BC; ++j) acc[i][j] = mfma_16x16x64(af[i], bf[j], acc[i][j]);
-      }
-    }
-  }
-
-  // Epilogue.  Register r of block (i, j) in lane l holds tile row
-  // 16(wm BR + i) + 4(l/16) + r and tile column 16(wn BC + j) + l%16.
-  // When the output tile fits in the LDS ring, the values go to LDS first and
-  // leave as 16-byte row chunks (stored directly, 16 lanes cover only 16
-  // columns of a row: short partial-line writes).
+// Stores a workgroup's output tile through the epilogue EPI: a WM x WN grid
+// of wavefronts, each holding BR x BC 16x16 blocks of int32 accumulators.
+// Register r of block (i, j) in lane l holds tile row 16(wm BR + i) +
+// 4(l/16) + r and tile column 16(wn BC + j) + l%16.  When the output tile
+// fits in the STAGE_BYTES of LDS at `stage` (whose operand reads every wave
+// has finished once the first barrier below passes), the values go to LDS
+// first and leave as 16-byte row chunks (stored directly, 16 lanes cover only
+// 16 columns of a row: short partial-line writes).
+template <int WM, int WN, int BR, int BC, int STAGE_BYTES, int EPI, typename TY, typename TH>
+__device__ inline void store_tile(const GemmParams& p, i32x4 (&acc)[BR][BC], int wm, int wn,
+                                  int mb0, int nb0, int lane, void* stage) {
   constexpr int BM = 16 * WM * BR;
   constexpr int BN = 16 * WN * BC;
   constexpr bool kHalfCols = EPI == kEpiSilu || EPI == kEpiSiluQ8;  // one output per gate/up pair
   constexpr int BNO = kHalfCols ? BN / 2 : BN;
   constexpr int kOutBytes = static_cast<int>(sizeof(TY));
-  constexpr bool kStage = BM * BNO * kOutBytes <= STG * FS * 1024 && (BNO * kOutBytes) % 16 == 0;
-  [[maybe_unused]] TY* const stile = reinterpret_cast<TY*>(&lds[0][0][0]);
+  constexpr bool kStage = BM * BNO * kOutBytes <= STAGE_BYTES && (BNO * kOutBytes) % 16 == 0;
+  [[maybe_unused]] TY* const stile = static_cast<TY*>(stage);
   if constexpr (kStage) ring_barrier();  // every wave is done reading the ring
   // Writes output (m, n_out) of tile-local row ml and column nlo.
   auto put = [&](int ml, int nlo, bool ok, int64_t m, int64_t n_out, TY v) {
@@ -308,7 +209,7 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
     __syncthreads();
     constexpr int EV = 16 / kOutBytes;  // outputs per 16-byte chunk
     constexpr int CPR = BNO / EV;       // chunks per tile row
-    constexpr int NT = NW * 64;
+    constexpr int NT = WM * WN * 64;
     constexpr int RPP = NT / CPR;       // tile rows per pass; threads past RPP * CPR idle
     static_assert(RPP >= 1, "a pass covers at least one tile row");
     const int64_t n_out_total = kHalfCols ? p.N / 2 : p.N;
@@ -333,6 +234,294 @@ __global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(G
       }
     }
   }
+}
+
+// WM x WN wavefronts, each owning BR x BC blocks of 16x16 (BM = 16 WM BR,
+// BN = 16 WN BC), with an STG-deep LDS ring whose stages hold KT k-blocks
+// (64 K each) of both operands.
+// The second launch bound is waves per SIMD: OCC workgroups of WM x WN
+// wavefronts over the CU's 4 SIMDs, so the register budget admits OCC
+// workgroups per CU.
+template <int WM, int WN, int BR, int BC, int STG, int OCC, int KT, int EPI, typename TY,
+          typename TH>
+__global__ __launch_bounds__(WM * WN * 64, OCC * WM * WN / 4) void gemm_kernel(GemmParams p) {
+  constexpr int NW = WM * WN;
+  constexpr int BMF = WM * BR;  // 16-row activation tiles per k-block
+  constexpr int BNF = WN * BC;  // 16-row weight tiles per k-block
+  constexpr int F = BMF + BNF;
+  constexpr int FS = F * KT;    // fragments per stage
+  // Fragment copies per wave per stage: LPW for the first FS - (LPW-1) NW
+  // waves, LPW - 1 for the rest.
+  constexpr int LPW = (FS + NW - 1) / NW;
+  __shared__ i32x4 lds[STG][FS][64];
+
+  // XCD-major tile mapping: workgroup b runs on XCD b % 8.
+  const int b = blockIdx.x;
+  const int tile = (b % kXcds) * p.per_xcd + b / kXcds;
+  if (tile >= p.tiles) return;
+  const int mb0 = (tile % p.tiles_m) * BMF;
+  const int nb0 = (tile / p.tiles_m) * BNF;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / WN;
+  const int wn = wave % WN;
+  const int KB = p.KB;
+  const int NS = static_cast<int>(ceil_div(KB, KT));  // ring stages over K
+
+  // Fragment f = q*NW + wave of a stage is k-block f / F of the stage; of
+  // that k-block, g = f % F < BMF are activation blocks mb0 + g, the rest
+  // weight blocks nb0 + g - BMF.  Blocks past the operand are clamped to its
+  // last block: their products only reach accumulator rows or columns that
+  // the epilogue never stores.  K-blocks past KB (the last stage of a K that
+  // is not a multiple of 64 KT) reload block KB - 1 and are not multiplied.
+  const bool full = (LPW - 1) * NW + wave < FS;  // wave-uniform
+  const i32x4* src[LPW];
+  int kk_of[LPW];
+#pragma unroll
+  for (int q = 0; q < LPW; ++q) {
+    const int f = min(q * NW + wave, FS - 1);
+    const int g = f % F;
+    kk_of[q] = f / F;
+    if (g < BMF) {
+      src[q] = p.a + static_cast<int64_t>(min(mb0 + g, p.MB - 1)) * KB * 64 + lane;
+    } else {
+      src[q] = p.w + static_cast<int64_t>(min(nb0 + g - BMF, p.NB - 1)) * KB * 64 + lane;
+    }
+  }
+  auto issue = [&](int stage, int slot) {
+#pragma unroll
+    for (int q = 0; q < LPW; ++q)
+      if (q < LPW - 1 || full) {
+        const int kb = min(stage * KT + kk_of[q], KB - 1);
+        __builtin_amdgcn_global_load_lds(
+            static_cast<const void*>(src[q] + static_cast<int64_t>(kb) * 64),
+            (lds_void*)(&lds[slot][q * NW + wave][0]), 16, 0, 0);
+      }
+  };
+
+  i32x4 acc[BR][BC];
+#pragma unroll
+  for (int i = 0; i < BR; ++i)
+#pragma unroll
+    for (int j = 0; j < BC; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][j][r] = 0;
+
+#pragma unroll
+  for (int s = 0; s < STG - 1; ++s)
+    if (s < NS) issue(s, s);
+
+  for (int st = 0; st < NS; ++st) {
+    // Stage st has landed once only the later stages' loads may remain.
+    if (st + STG - 2 < NS) {
+      if (full) {
+        wait_vmcnt<LPW * (STG - 2)>();
+      } else {
+        wait_vmcnt<(LPW - 1) * (STG - 2)>();
+      }
+    } else {
+      wait_vmcnt<0>();
+    }
+    ring_barrier();
+    // Every wave has finished reading the slot of stage st-1: refill it.
+    if (st + STG - 1 < NS) issue(st + STG - 1, (st + STG - 1) % STG);
+    const int slot = st % STG;
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      if (KT == 1 || st * KT + kk < KB) {
+        i32x4 af[BR], bf[BC];
+#pragma unroll
+        for (int i = 0; i < BR; ++i) af[i] = lds[slot][kk * F + wm * BR + i][lane];
+#pragma unroll
+        for (int j = 0; j < BC; ++j) bf[j] = lds[slot][kk * F + BMF + wn * BC + j][lane];
+#pragma unroll
+        for (int i = 0; i < BR; ++i)
+#pragma unroll
+          for (int j = 0; j < BC; ++j) acc[i][j] = mfma_16x16x64(af[i], bf[j], acc[i][j]);
+      }
+    }
+  }
+
+  store_tile<WM, WN, BR, BC, STG * FS * 1024, EPI, TY, TH>(p, acc, wm, wn, mb0, nb0, lane,
+                                                           &lds[0][0][0]);
+}
+
+// Workgroup barrier with the wave's LDS reads complete, through the builtin
+// s_waitcnt, so the compiler's own wait insertion knows they are (an inline
+// asm wait is opaque to it, and it would then wait for the newer reads of
+// the next k-block too).  The empty asm statements keep LDS accesses on
+// their side of the barrier.
+__device__ inline void ring_barrier_tracked() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0); vmcnt and expcnt at their maxima
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, unrolled at compile time.
+template <typename F, int... I>
+__device__ inline void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ inline void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+__device__ inline __amdgpu_buffer_rsrc_t dma_rsrc(const void* base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, 0x7fffffff, 0x00020000);
+}
+
+// 16 bytes per lane from the buffer at voffset into LDS at lds + 16 * lane
+// (buffer_load_dwordx4 ... lds).
+__device__ inline void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void*)lds, 16, voffset, 0, 0, 0);
+}
+
+// Weights-direct GEMM: NW wavefronts, each owning all A 16-row activation
+// blocks of the tile and B 16-row weight blocks of its own (tile 16A x
+// 16 NW B).  A weight fragment is used by exactly one wavefront, so it goes
+// from global memory straight into registers (the packed fragment is the
+// MFMA operand image) through a ring of D + 1 register sets, D k-blocks ahead;
+// only the activation fragments, which every wavefront reads, pass through
+// LDS: buffer_load ... lds copies into an S-slot ring, and each wavefront
+// reads k-block t+1 into registers during k-block t's MFMAs.  Per k-block a
+// wavefront reads A KiB from LDS for A x B MFMAs, against (BR + BC) KiB for
+// BR x BC in gemm_kernel.  One barrier per k-block.
+template <int NW, int A, int B, int D, int EPI, typename TY, typename TH>
+__global__ __launch_bounds__(NW * 64, NW / 4) void gemm_wd_kernel(GemmParams p) {
+  static_assert(D >= 2 && NW % 4 == 0, "prefetch depth and wavefront count");
+  constexpr int S = D <= 2 ? 2 : (D <= 4 ? 4 : 8);  // ring slots: a power of two >= D
+  constexpr int BS = D + 1;                          // weight register sets
+  constexpr int LPW = (A + NW - 1) / NW;             // activation copies per wavefront
+  constexpr int BM = 16 * A;
+  constexpr int BN = 16 * NW * B;
+  constexpr bool kHalfCols = EPI == kEpiSilu || EPI == kEpiSiluQ8;
+  constexpr int kRing = S * A * 1024;
+  constexpr int kOut = BM * (kHalfCols ? BN / 2 : BN) * static_cast<int>(sizeof(TY));
+  constexpr int kLds = kRing > kOut ? kRing : kOut;
+  __shared__ i32x4 lds[kLds / 16];
+  auto ring = reinterpret_cast<i32x4 (*)[A][64]>(lds);
+
+  const int b = blockIdx.x;
+  const int tile = (b % kXcds) * p.per_xcd + b / kXcds;
+  if (tile >= p.tiles) return;
+  const int mb0 = (tile % p.tiles_m) * A;
+  const int nb0 = (tile / p.tiles_m) * (NW * B);
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int KB = p.KB;
+
+  // Activation block q * NW + wave of the tile (clamped to the last block:
+  // its products reach only rows the epilogue never stores).
+  const bool full = (LPW - 1) * NW + wave < A;
+  const __amdgpu_buffer_rsrc_t arsrc = dma_rsrc(p.a + static_cast<int64_t>(mb0) * KB * 64);
+  uint32_t aoff[LPW];
+#pragma unroll
+  for (int q = 0; q < LPW; ++q) {
+    const int f = min(q * NW + wave, A - 1);
+    aoff[q] = static_cast<uint32_t>((min(mb0 + f, p.MB - 1) - mb0) * KB * 1024 + lane * 16);
+  }
+  const i32x4* bsrc[B];
+#pragma unroll
+  for (int j = 0; j < B; ++j)
+    bsrc[j] = p.w + static_cast<int64_t>(min(nb0 + wave * B + j, p.NB - 1)) * KB * 64 + lane;
+
+  i32x4 breg[BS][B];
+  i32x4 af[2][A];
+  i32x4 acc[A][B];
+#pragma unroll
+  for (int i = 0; i < A; ++i)
+#pragma unroll
+    for (int j = 0; j < B; ++j) acc[i][j] = i32x4{0, 0, 0, 0};
+
+  auto issue = [&](int kb, auto set_c) __attribute__((always_inline)) {
+    constexpr int set = decltype(set_c)::value;
+#pragma unroll
+    for (int q = 0; q < LPW; ++q)
+      if (q < LPW - 1 || full)
+        dma16(arsrc, &ring[kb & (S - 1)][q * NW + wave][0], aoff[q] + static_cast<uint32_t>(kb) * 1024);
+#pragma unroll
+    for (int j = 0; j < B; ++j) breg[set][j] = bsrc[j][static_cast<int64_t>(kb) * 64];
+  };
+  // Loads per wavefront per k-block.
+  constexpr int kLoadsFull = LPW + B;
+  constexpr int kLoadsPart = LPW - 1 + B;
+
+  static_for<D>([&](auto i) __attribute__((always_inline)) {
+    if (decltype(i)::value < KB) issue(decltype(i)::value, i);
+  });
+  // k-block 0 has landed once only k-blocks 1 .. D-1 may be in flight.
+  if (D - 1 < KB) {
+    if (full) wait_vmcnt<kLoadsFull * (D - 1)>(); else wait_vmcnt<kLoadsPart * (D - 1)>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  ring_barrier_tracked();
+#pragma unroll
+  for (int i = 0; i < A; ++i) af[0][i] = ring[0][i][lane];
+
+  // k-block kb: make kb+1's activations visible and read them, refill the
+  // slot and register set kb+1 leaves behind with k-block kb+D, then kb's
+  // MFMAs.  STEADY: kb + 1 < KB is known.
+  auto step = [&](int kb, auto set_c, auto cur_c, auto steady_c) __attribute__((always_inline)) {
+    constexpr int set = decltype(set_c)::value;
+    constexpr int nset = (set + D) % BS;
+    constexpr int cur = decltype(cur_c)::value;
+    constexpr bool steady = decltype(steady_c)::value;
+    if (steady || kb + 1 < KB) {
+      // k-block kb+1 has landed once only kb+2 .. kb+D-1 may be in flight.
+      if (kb + D - 1 < KB) {
+        if (full) wait_vmcnt<kLoadsFull * (D - 2)>(); else wait_vmcnt<kLoadsPart * (D - 2)>();
+      } else {
+        wait_vmcnt<0>();
+      }
+      ring_barrier_tracked();
+      // Slot (kb+D) & (S-1) held k-block kb+D-S <= kb-1, read before the barrier.
+      if (kb + D < KB) issue(kb + D, std::integral_constant<int, nset>{});
+#pragma unroll
+      for (int i = 0; i < A; ++i) af[cur ^ 1][i] = ring[(kb + 1) & (S - 1)][i][lane];
+    }
+#pragma unroll
+    for (int i = 0; i < A; ++i)
+#pragma unroll
+      for (int j = 0; j < B; ++j) acc[i][j] = mfma_16x16x64(af[cur][i], breg[set][j], acc[i][j]);
+  };
+  // Unrolled by U, a multiple of the register-set count and of 2, so every
+  // set and buffer index is static.
+  constexpr int U = (BS % 2 == 0) ? BS : 2 * BS;
+  int kb = 0;
+  for (; kb + U < KB; kb += U) {
+    static_for<U>([&](auto i) __attribute__((always_inline)) {
+      constexpr int I = decltype(i)::value;
+      step(kb + I, std::integral_constant<int, I % BS>{}, std::integral_constant<int, I % 2>{},
+           std::true_type{});
+    });
+  }
+  static_for<U>([&](auto i) __attribute__((always_inline)) {
+    constexpr int I = decltype(i)::value;
+    if (kb + I < KB)
+      step(kb + I, std::integral_constant<int, I % BS>{}, std::integral_constant<int, I % 2>{},
+           std::false_type{});
+  });
+
+  store_tile<1, NW, A, B, kLds, EPI, TY, TH>(p, acc, 0, wave, mb0, nb0, lane, lds);
+}
+
+// Launches the weights-direct kernel for the problem in p.
+template <int NW, int A, int B, int D, int EPI, typename TY, typename TH>
+hipError_t launch_wd(GemmParams p, hipStream_t st) {
+  const int64_t tiles_m = ceil_div(p.MB, A);
+  const int64_t tiles = tiles_m * ceil_div(p.NB, NW * B);
+  if (tiles == 0) return hipSuccess;
+  if (ceil_div(tiles, kXcds) * kXcds > INT32_MAX) return hipErrorInvalidConfiguration;
+  p.tiles_m = static_cast<int>(tiles_m);
+  p.tiles = static_cast<int>(tiles);
+  p.per_xcd = static_cast<int>(ceil_div(tiles, kXcds));
+  hipLaunchKernelGGL((gemm_wd_kernel<NW, A, B, D, EPI, TY, TH>), dim3(p.per_xcd * kXcds),
+                     dim3(NW * 64), 0, st, p);
+  return hipGetLastError();
 }
 
 // Launches one tile configuration for the problem in p (tile counts are
@@ -404,6 +593,10 @@ hipError_t launch_t(const GemmParams& p, hipStream_t st) {
       return launch_cfg<4, 4, 4, 4, 2, 1, 2, EPI, TY, TH>(p, st);
     case kGemmMid:
       return launch_cfg<2, 2, 2, 1, 3, 2, 4, EPI, TY, TH>(p, st);
+    case kGemmWd7x2:
+      return launch_wd<8, 7, 2, 4, EPI, TY, TH>(p, st);
+    case kGemmWd9x1:
+      return launch_wd<4, 9, 1, 6, EPI, TY, TH>(p, st);
     default:
       return launch_cfg<2, 4, 4, 4, 3, 2, 1, EPI, TY, TH>(p, st);
   }
@@ -412,6 +605,19 @@ hipError_t launch_t(const GemmParams& p, hipStream_t st) {
 }  // namespace
 
 int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus) {
+  // Weights-direct tiles when one round of them (one workgroup per CU) fills
+  // at least 85% of the CUs with at least 85% of the tile rows in use:
+  // 112 x 256 (packed QKV at M = 449..560), then 144 x 64 (O and down at
+  // M = 433..576).
+  if (MB > 4) {
+    auto fits = [&](int64_t a, int64_t cols) {
+      const int64_t tm = ceil_div(MB, a);
+      const int64_t tiles = tm * ceil_div(NB, cols);
+      return tiles <= cus && 100 * tiles >= 85 * cus && 100 * MB >= 85 * tm * a;
+    };
+    if (fits(7, 16)) return kGemmWd7x2;
+    if (fits(9, 4)) return kGemmWd9x1;
+  }
   const int64_t slots = cus * 2;
   const int64_t tiles_m = ceil_div(MB, 8);  // 128-row tiles
   const int64_t big_tiles = tiles_m * ceil_div(NB, 8);
