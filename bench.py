@@ -2,23 +2,28 @@
 """W8A8 linear-path benchmark on one MI355X.
 
 Workload (one "step"): the W8A8 linear stack of one LLaMA-7B decode step at
-M decode rows (default 8): 32 layers x {packed QKV [12288x4096], O
-[4096x4096], packed gate/up [22016x4096] with fused SiLU*mul -> [M, 11008],
-down [4096x11008]}.  Every layer has its own random-init weights (~N(0, 0.02),
-per-output int8, 6.48 GB packed in HBM) so nothing is served from the 256 MB
-Infinity Cache; RMSNorm and attention are stubbed by seeded fp16 activations,
-and the down projection consumes the gate/up output.  The step is captured
-once in a HIP graph and replayed.  Inputs are resident in HBM before timing.
+M decode rows (default 8) plus the fp16 LM head, as the full-stack config
+names it: 32 layers x {packed QKV [12288x4096], O [4096x4096], packed gate/up
+[22016x4096] with fused SiLU*mul -> [M, 11008], down [4096x11008]}, then the
+fp16 LM head [32003x4096] (torch F.linear: it is not a W8A8 linear).  Every
+layer has its own random-init weights (~N(0, 0.02), per-output int8, 6.48 GB
+packed in HBM) so nothing is served from the 256 MB Infinity Cache; RMSNorm
+and attention are stubbed by seeded fp16 activations, and the down projection
+consumes the gate/up output.  The step is captured once in a HIP graph and
+replayed.  Inputs are resident in HBM before timing.
 
 `value` = algorithmic HBM bytes of the step / step time (GB/s), with bytes =
-N*K + 2N + 2MK + 2M*N_out per linear.  The `roofline` object is for the
-dominant kernel (the packed gate/up linear: per-token quantization, int8 GEMV and
-SiLU*mul in one kernel at M <= 8), timed with HIP
-events on the stream it is launched on.  `cpu_baseline` times the torch-CPU
-restatement of the reference's integer path on all host cores (rank 0, N=1
-only), and `parity` reports the GPU outputs' max-abs / max-relative error
-against it.  `extra` carries per-projection decode GB/s at M=1,4,8, the
-prefill GEMM TOPS at M=560/768/1024 and the stack with the fp16 LM head.
+N*K + 2N + 2MK + 2M*N_out per W8A8 linear and 2*V*H + 2MH + 2MV for the LM
+head.  The `roofline` object is for the dominant kernel (the packed gate/up
+linear: per-token quantization, int8 GEMV and SiLU*mul in one kernel at
+M <= 8), timed with HIP events on the stream it is launched on.
+`cpu_baseline` times the torch-CPU restatement of the reference's integer
+path on all host cores (rank 0, N=1 only), and `parity` reports the GPU
+outputs' max-abs / max-relative error against it.  `extra` carries
+per-projection decode GB/s at M=1,4,8, the prefill TOPS at M=560/768/1024
+(the quantize + GEMM call, the int8-in call with its packing pass, and the
+GEMM kernel alone), the stack without the LM head, and the whole-model step
+through the runner.
 
     python bench.py [--steps K] [--warmup W] [--m 8] [--no-extra] [--no-cpu]
 """
@@ -294,15 +299,25 @@ def projection_sweep(layers, device, ms_list=(1, 4, 8)) -> dict:
 
 
 def prefill_sweep(layers, device, m: int = 560) -> dict:
-    """Prefill TOPS per projection: fused linear (quant + GEMM) and GEMM kernel alone."""
+    """Prefill TOPS per projection, graphs over 8 layers' cold weights:
+    * ``linear``: binary16 x in (per-token quantization launch + GEMM);
+    * ``i8in_pack_gemm``: row-major int8 x in (``w8a8_linear_i8in``: the pass
+      that packs the rows into 16x64 tiles, then the GEMM);
+    * ``gemm_kernel``: the GEMM kernel alone on x already packed
+      (``w8a8_linear_packed``), with the tile the library picks."""
     import torch
 
     from nanopointllm_amd import _lib, w8a8, workloads as W
 
+    lib = _lib.load()
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    names = ("tiny-deep", "small-deep", "big-deep", "big", "w192", "w224", "w256", "w256sq",
+             "mid", "wd7x2")
     out = {}
     for spec in W.PROJECTIONS:
         x16 = W.prefill_activations(m, spec.k, seed=11).to(device)
         xq, sx = w8a8.quant_rows(x16)
+        xp = w8a8.pack_rows(xq)
         fn_args = dict(epilogue=_lib.EPI_SILU_MUL) if spec.silu else {}
         sub = layers[:8]
 
@@ -311,25 +326,33 @@ def prefill_sweep(layers, device, m: int = 560) -> dict:
                 p = layer.weights[spec.name]
                 w8a8.linear_dynamic(x16, p.packed, p.scale, None, p.out_features, **fn_args)
 
-        def run_gemm(spec=spec, xq=xq, sx=sx, fn_args=fn_args):
+        def run_i8in(spec=spec, xq=xq, sx=sx, fn_args=fn_args):
             for layer in sub:
                 p = layer.weights[spec.name]
                 w8a8.linear_i8in(xq, sx, p.packed, p.scale, None, p.out_features,
                                  out_dtype=torch.float16, **fn_args)
 
-        ms_lin, g1 = time_graph(run_linear, steps=10, warmup=3)
-        ms_gemm, g2 = time_graph(run_gemm, steps=10, warmup=3)
-        del g1, g2
+        def run_kernel(spec=spec, xp=xp, sx=sx, fn_args=fn_args):
+            for layer in sub:
+                p = layer.weights[spec.name]
+                w8a8.linear_packed(xp, sx, m, spec.k, p.packed, p.scale, None, p.out_features,
+                                   out_dtype=torch.float16, **fn_args)
+
+        timed = {}
+        for key, fn in (("linear", run_linear), ("i8in_pack_gemm", run_i8in),
+                        ("gemm_kernel", run_kernel)):
+            ms, g = time_graph(fn, steps=10, warmup=3)
+            del g
+            timed[key] = ms / len(sub)
         ops = W.algorithmic_ops(m, spec.n, spec.k)
-        lin = ms_lin / len(sub)
-        gemm = ms_gemm / len(sub)
-        out[spec.name] = {
-            "linear_us": round(lin * 1e3, 2),
-            "linear_TOPS": round(ops / (lin * 1e-3) / 1e12, 1),
-            "gemm_us": round(gemm * 1e3, 2),
-            "gemm_TOPS": round(ops / (gemm * 1e-3) / 1e12, 1),
-            "gemm_frac_int8_peak": round(ops / (gemm * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
-        }
+        row = {}
+        for key, per in timed.items():
+            row[f"{key}_us"] = round(per * 1e3, 2)
+            row[f"{key}_TOPS"] = round(ops / (per * 1e-3) / 1e12, 1)
+        row["gemm_kernel_frac_int8_peak"] = round(
+            ops / (timed["gemm_kernel"] * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)
+        row["tile"] = names[lib.w8a8_gemm_tile_config(m, spec.n, cus)]
+        out[spec.name] = row
     torch.cuda.synchronize()
     return out
 
@@ -440,9 +463,9 @@ def decode_step_int8_mlp(layers, m: int, device) -> dict:
             "h_scale": h_scale}
 
 
-def stack_with_lm_head(layers, m: int, device) -> dict:
-    """The 32-layer W8A8 stack plus the fp16 LM head [32003 x 4096] (torch
-    F.linear: the LM head is not a W8A8 linear)."""
+def lm_head(m: int, device):
+    """The fp16 LM head [32003 x 4096] of config 4 and its input rows (torch
+    F.linear: the LM head is not a W8A8 linear), with its algorithmic bytes."""
     import torch
 
     from nanopointllm_amd import workloads as W
@@ -451,15 +474,19 @@ def stack_with_lm_head(layers, m: int, device) -> dict:
     g.manual_seed(99)
     lm = (torch.randn(W.VOCAB, W.HIDDEN, generator=g, device=device) * 0.02).to(torch.float16)
     xh = W.decode_activations(m, W.HIDDEN, seed=98).to(device)
+    nbytes = W.VOCAB * W.HIDDEN * 2 + 2 * m * W.HIDDEN + 2 * m * W.VOCAB
+    return lm, xh, nbytes
 
+
+def stack_without_lm_head(layers, m: int, device) -> dict:
+    """The 32-layer W8A8 stack alone (the headline step less the LM head)."""
     def step():
         for layer in layers:
             layer.step()
-        torch.nn.functional.linear(xh, lm)
 
     ms, gr = time_graph(step, steps=10, warmup=3)
     del gr
-    nbytes = step_bytes(m, len(layers)) + W.VOCAB * W.HIDDEN * 2 + 2 * m * W.HIDDEN + 2 * m * W.VOCAB
+    nbytes = step_bytes(m, len(layers))
     return {"ms": round(ms, 4), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1), "bytes": nbytes}
 
 
@@ -716,13 +743,16 @@ def main() -> int:
         print(json.dumps({"profile_gateup": roof, "calibration_copy_bytes": CALIBRATION_COPY_BYTES}))
         return 0
 
+    lm, xh, lm_bytes = lm_head(m, device)
+
     def step():
         for layer in layers:
             layer.step()
+        torch.nn.functional.linear(xh, lm)
 
     log("capturing step graph")
     ms_per_step, graph = time_graph(step, args.steps, args.warmup)
-    nbytes = step_bytes(m, args.layers)
+    nbytes = step_bytes(m, args.layers) + lm_bytes
     value = nbytes / (ms_per_step * 1e-3) / 1e9
     log(f"step {ms_per_step:.4f} ms, {value:.1f} GB/s")
     del graph
@@ -741,8 +771,8 @@ def main() -> int:
         extra["qkv_m_sweep"] = qkv_m_sweep(layers, device)
         log("mixed M=567 int8 chain")
         extra["mixed_567_gateup_down_int8_chain"] = mixed_chain(layers, device)
-        log("stack + fp16 LM head")
-        extra["stack_with_fp16_lm_head"] = stack_with_lm_head(layers, m, device)
+        log("stack without the LM head")
+        extra["stack_without_lm_head"] = stack_without_lm_head(layers, m, device)
         log("decode step with the int8 MLP chain")
         extra["decode_step_int8_mlp_chain"] = decode_step_int8_mlp(layers, m, device)
         log("runner decode step (32 layers, fused norms, LM head)")
@@ -770,9 +800,11 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "int8",
         "data": "synthetic",
-        "config": {"workload": f"llama7b_decode_w8a8_linear_stack_{args.layers}L_without_lm_head",
+        "config": {"workload": f"llama7b_decode_w8a8_linear_stack_{args.layers}L_plus_fp16_lm_head",
                    "m": m, "layers": args.layers,
                    "projections": {p.name: [p.n, p.k] for p in W.PROJECTIONS},
+                   "lm_head": {"shape": [W.VOCAB, W.HIDDEN], "dtype": "fp16",
+                               "op": "torch F.linear (not a W8A8 linear)"},
                    "weights": "random-init ~N(0,0.02), per-output int8, packed",
                    "bytes_per_step": nbytes, "graph": True},
         "roofline": roofline,

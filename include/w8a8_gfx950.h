@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 4
+#define W8A8_ABI_VERSION 5
 
 typedef enum w8a8_dtype {
   W8A8_F32 = 0,
@@ -253,6 +253,21 @@ int w8a8_linear_i8in(const int8_t* xq, int64_t ldq, const float* x_scale,
                      int epilogue, void* y, int y_dtype, int64_t ldy, float y_scale,
                      int inter_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
                      int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * As w8a8_linear_i8in for activations already in the packed 16x64 tile
+ * layout of an [m, k] int8 operand (w8a8_packed_bytes(m, k) bytes, as
+ * w8a8_pack_rows with W8A8_ROWS_AS_IS writes them; pad rows and columns
+ * zero): the MFMA GEMM runs directly on them, with no packing pass and no
+ * workspace, for any m.  Epilogues as w8a8_linear_i8in.  No counterpart in
+ * the reference (its linears take row-major activations): for callers that
+ * keep activations packed between kernels, and to time the GEMM kernel
+ * alone.
+ */
+int w8a8_linear_packed(const int8_t* xq_packed, const float* x_scale, const int8_t* w_packed,
+                       const float* w_scale, const float* bias, int epilogue, void* y,
+                       int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,
+                       int64_t n, int64_t k, hipStream_t stream);
 
 /*
  * Packed gate/up with SiLU*mul and the two-phase per-token dynamic int8

@@ -533,6 +533,23 @@ int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* res
   return status_of(gemv ? launch_gemv(op, stream) : launch_gemm(op, stream));
 }
 
+int w8a8_linear_packed(const int8_t* xq_packed, const float* x_scale, const int8_t* w_packed,
+                       const float* w_scale, const float* bias, int epilogue, void* y,
+                       int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,
+                       int64_t n, int64_t k, hipStream_t stream) {
+  if (epilogue == W8A8_EPI_REQUANT) return W8A8_ERR_DTYPE;  // w8a8_linear_i8in_requant
+  if (epilogue == W8A8_EPI_DEQUANT_BF16_EXACT && bias != nullptr) return W8A8_ERR_DTYPE;
+  int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
+                        n, k);
+  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
+  if (xq_packed == nullptr || (epilogue != W8A8_EPI_I32 && x_scale == nullptr))
+    return W8A8_ERR_NULL;
+  if (!aligned(xq_packed, 16)) return W8A8_ERR_ALIGN;
+  LinearOperands op = make_ops(xq_packed, round_up(k, kTileK), x_scale, w_packed, w_scale, bias,
+                               epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m, n, k);
+  return status_of(launch_gemm(op, stream));
+}
+
 int w8a8_linear_noalloc(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
                         const float* w_scale, const float* bias, int epilogue, void* y,
                         int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,

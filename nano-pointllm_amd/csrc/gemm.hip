@@ -595,8 +595,6 @@ hipError_t launch_t(const GemmParams& p, hipStream_t st) {
       return launch_cfg<2, 2, 2, 1, 3, 2, 4, EPI, TY, TH>(p, st);
     case kGemmWd7x2:
       return launch_wd<8, 7, 2, 4, EPI, TY, TH>(p, st);
-    case kGemmWd9x1:
-      return launch_wd<4, 9, 1, 6, EPI, TY, TH>(p, st);
     default:
       return launch_cfg<2, 4, 4, 4, 3, 2, 1, EPI, TY, TH>(p, st);
   }
@@ -605,18 +603,16 @@ hipError_t launch_t(const GemmParams& p, hipStream_t st) {
 }  // namespace
 
 int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus) {
-  // Weights-direct tiles when one round of them (one workgroup per CU) fills
-  // at least 85% of the CUs with at least 85% of the tile rows in use:
-  // 112 x 256 (packed QKV at M = 449..560), then 144 x 64 (O and down at
-  // M = 433..576).
+  // The 112 x 256 weights-direct tile when one round of it (one workgroup per
+  // CU) fills at least 85% of the CUs with at least 85% of the tile rows in
+  // use (the packed QKV at M = 449..560).  A 144 x 64 weights-direct tile for
+  // O and down at the same M measured slower than the 128 x 128 deep ring
+  // (27.2 vs 23.5 us and 59.6 vs 51.3 us with the fp16 epilogue), so those
+  // keep the LDS-ring tiles.
   if (MB > 4) {
-    auto fits = [&](int64_t a, int64_t cols) {
-      const int64_t tm = ceil_div(MB, a);
-      const int64_t tiles = tm * ceil_div(NB, cols);
-      return tiles <= cus && 100 * tiles >= 85 * cus && 100 * MB >= 85 * tm * a;
-    };
-    if (fits(7, 16)) return kGemmWd7x2;
-    if (fits(9, 4)) return kGemmWd9x1;
+    const int64_t tm = ceil_div(MB, 7);
+    const int64_t tiles = tm * ceil_div(NB, 16);
+    if (tiles <= cus && 100 * tiles >= 85 * cus && 100 * MB >= 85 * tm * 7) return kGemmWd7x2;
   }
   const int64_t slots = cus * 2;
   const int64_t tiles_m = ceil_div(MB, 8);  // 128-row tiles

@@ -111,7 +111,6 @@ enum GemmTile : int {
   kGemmW256Sq = 7,     // 256x256, 16 waves, 2-stage ring of two k-blocks, 1 per CU
   kGemmMid = 8,        // 64x32, 4 waves, 3-stage ring of four k-blocks, 2 per CU
   kGemmWd7x2 = 9,      // 112x256 weights-direct, 8 waves of 112x32, 4 k-blocks ahead, 1 per CU
-  kGemmWd9x1 = 10,     // 144x64 weights-direct, 4 waves of 144x16, 6 k-blocks ahead, 1 per CU
 };
 int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus);
 

@@ -248,6 +248,35 @@ def linear_i8in(xq: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor,
     return y.reshape(*xq.shape[:-1], cols)
 
 
+def linear_packed(xq_packed: torch.Tensor, x_scale: torch.Tensor, m: int, k: int,
+                  w_packed: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None,
+                  n: int, *, epilogue: int = _lib.EPI_DEQUANT,
+                  out_dtype: torch.dtype | None = None, y_scale: float = 0.0,
+                  inter_dtype: torch.dtype = torch.float16) -> torch.Tensor:
+    """W8A8 linear on int8 activations already in the packed 16x64 tile
+    layout of an [m, k] operand (``pack_rows`` output): the MFMA GEMM alone,
+    no packing pass, no workspace."""
+    device = _lib.require_cuda(xq_packed, x_scale, w_packed, w_scale, bias)
+    if xq_packed.dtype != torch.int8 or xq_packed.numel() < packed_bytes(m, k):
+        raise ValueError("xq_packed must hold the packed tiles of an [m, k] int8 operand")
+    _check_operands(k, w_packed, w_scale, bias, n, k)
+    s = x_scale.detach().to(dtype=torch.float32).reshape(-1).contiguous()
+    if s.numel() != m:
+        raise ValueError("x_scale must have one value per row")
+    if out_dtype is None:
+        out_dtype = _default_out_dtype(epilogue, torch.float16)
+    cols = _out_cols(epilogue, n)
+    y = torch.empty((m, cols), dtype=out_dtype, device=device)
+    if m and n:
+        lib = _lib.load()
+        _lib.check(lib.w8a8_linear_packed(
+            xq_packed.data_ptr(), s.data_ptr(), w_packed.data_ptr(), w_scale.data_ptr(),
+            _lib.ptr(bias), epilogue, y.data_ptr(), _lib.dtype_code(out_dtype), cols,
+            float(y_scale), _lib.dtype_code(inter_dtype), m, n, k,
+            _lib.stream_handle(device)), "w8a8_linear_packed")
+    return y
+
+
 class TwoPhaseOutput(NamedTuple):
     h: torch.Tensor      # SiLU(g) * u, 16-bit [..., n/2]
     hq: torch.Tensor     # int8 [..., n/2], per-token dynamic quantization of h

@@ -6,15 +6,16 @@ machine without a GPU."""
 from __future__ import annotations
 
 CONFIG_NAMES = ("tiny-deep", "small-deep", "big-deep", "big", "w192", "w224", "w256",
-                "w256sq", "mid", "wd7x2", "wd9x1")
+                "w256sq", "mid", "wd7x2")
 
 
-def wd_fits(m: int, n: int, a: int, cols: int, cus: int = 256) -> bool:
-    """The weights-direct rule: one round of 16a x 16cols tiles fills at
-    least 85% of the CUs, with at least 85% of the tile rows in use."""
+def wd_fits(m: int, n: int, cus: int = 256) -> bool:
+    """The weights-direct rule: one round of 112 x 256 tiles fills at least
+    85% of the CUs, with at least 85% of the tile rows in use."""
+    a = 7
     mb, nb = -(-m // 16), -(-n // 16)
     tm = -(-mb // a)
-    tiles = tm * -(-nb // cols)
+    tiles = tm * -(-nb // 16)
     return mb > 4 and tiles <= cus and 100 * tiles >= 85 * cus and 100 * mb >= 85 * tm * a
 
 

@@ -74,6 +74,16 @@ def test_invalid_arguments_return_status_without_launch():
     assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_DEQUANT, fake,
                            _lib.F16, 16, 0.0, _lib.F16, 9, 16, 64, None, fake, 10,
                            None) == _lib.ERR_WORKSPACE
+    # packed activations: misaligned, or a missing scale vector
+    assert lib.w8a8_linear_packed(ctypes.c_void_p(0x1008), fake, fake, fake, None,
+                                  _lib.EPI_DEQUANT, fake, _lib.F16, 16, 0.0, _lib.F16, 96, 16,
+                                  64, None) == _lib.ERR_ALIGN
+    assert lib.w8a8_linear_packed(fake, None, fake, fake, None, _lib.EPI_DEQUANT, fake,
+                                  _lib.F16, 16, 0.0, _lib.F16, 96, 16, 64,
+                                  None) == _lib.ERR_NULL
+    assert lib.w8a8_linear_packed(fake, fake, fake, fake, None, _lib.EPI_REQUANT, fake,
+                                  _lib.I8, 16, 0.0, _lib.F16, 96, 16, 64,
+                                  None) == _lib.ERR_DTYPE
     # misaligned packed weights
     assert lib.w8a8_gemm_i32(fake, 64, ctypes.c_void_p(0x1001), fake, 16, 1, 16, 64, fake,
                              1 << 20, None) == _lib.ERR_ALIGN

@@ -14,8 +14,8 @@ QKV, O, GATEUP, DOWN = 12288, 4096, 22016, 4096
 
 @pytest.mark.parametrize("m,n,cfg", [
     (560, QKV, "wd7x2"), (768, QKV, "w192"), (1024, QKV, "w192"), (2048, QKV, "w256"),
-    (560, O, "wd9x1"), (567, O, "wd9x1"), (567, QKV, "big"), (768, O, "big-deep"),
-    (1024, O, "big-deep"), (480, QKV, "wd7x2"), (500, O, "wd9x1"),
+    (560, O, "big-deep"), (567, O, "big-deep"), (567, QKV, "big"), (768, O, "big-deep"),
+    (1024, O, "big-deep"), (480, QKV, "wd7x2"), (500, O, "small-deep"), (560, DOWN, "big-deep"),
     (560, GATEUP, "w224"), (768, GATEUP, "big"), (1024, GATEUP, "w256"),
     (64, QKV, "tiny-deep"), (128, O, "mid"), (256, O, "mid"), (65, DOWN, "mid"),
     (100, 1000, "tiny-deep"), (160, 8192, "small-deep"), (128, 8192, "mid"),
@@ -34,9 +34,8 @@ def test_every_config_fits_one_round_or_is_the_widest():
     for m in range(65, 4097, 37):
         for n in (4096, 11008, 12288, 22016, 32000):
             cfg = gemm_config(m, n)
-            wd = "wd7x2" if wd_fits(m, n, 7, 16) else "wd9x1" if wd_fits(m, n, 9, 4) else None
-            assert (cfg == wd) if wd else cfg not in ("wd7x2", "wd9x1"), (m, n, cfg)
-            if wd:
+            assert (cfg == "wd7x2") == wd_fits(m, n), (m, n, cfg)
+            if cfg == "wd7x2":
                 continue
             mb, nb = -(-m // 16), -(-n // 16)
             tm = -(-mb // 8)
@@ -55,7 +54,7 @@ def test_every_config_fits_one_round_or_is_the_widest():
             mb, nb = -(-m // 16), -(-n // 16)
             mid = -(-mb // 4) * -(-nb // 2)
             fits = mb > 4 and 128 <= mid <= 512 and -(-mb // 8) * -(-nb // 8) <= 512
-            if wd_fits(m, n, 7, 16) or wd_fits(m, n, 9, 4):
+            if wd_fits(m, n):
                 continue
             assert (gemm_config(m, n) == "mid") == fits, (m, n)
 

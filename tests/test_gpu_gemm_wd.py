@@ -1,7 +1,6 @@
-"""The weights-direct GEMM tiles (csrc/gemm.hip ``gemm_wd_kernel``): 112 x 256
-(8 wavefronts of 112 x 32) and 144 x 64 (4 wavefronts of 144 x 16), taken
-when one round of them fills the CUs, as for the packed QKV, O and down
-projections at M ~ 560 (paged_attention.py:1349-1352, 1488;
+"""The weights-direct GEMM tile (csrc/gemm.hip ``gemm_wd_kernel``): 112 x 256
+(8 wavefronts of 112 x 32), taken when one round of it fills the CUs, as for
+the packed QKV projection at M ~ 560 (paged_attention.py:1349-1352;
 lightweight_runner.py:389-404).  Weight fragments go straight from memory into
 registers several k-blocks ahead; only the activations pass through LDS.
 
@@ -47,8 +46,7 @@ SHAPES = [
     # (m, n, k, tile): ragged rows / columns, K from one k-block to 11008
     (560, 12288, 4096, "wd7x2"), (500, 12000, 1000, "wd7x2"), (545, 12100, 64, "wd7x2"),
     (480, 12288, 200, "wd7x2"), (555, 11900, 2700, "wd7x2"),
-    (560, 4096, 4096, "wd9x1"), (567, 4096, 11008, "wd9x1"), (550, 4000, 130, "wd9x1"),
-    (500, 4090, 64, "wd9x1"), (530, 4096, 1111, "wd9x1"),
+    (400, 16000, 1111, "wd7x2"), (470, 11100, 64, "wd7x2"), (465, 13000, 130, "wd7x2"),
 ]
 
 
@@ -76,7 +74,7 @@ def test_wd_int32_and_dequant(cuda, m, n, k, cfg):
 
 
 @pytest.mark.parametrize("m,inter,k,cfg", [(520, 6100, 4096, "wd7x2"), (560, 6144, 333, "wd7x2"),
-                                            (550, 2000, 4096, "wd9x1"), (540, 2046, 640, "wd9x1")])
+                                            (470, 6000, 1000, "wd7x2"), (400, 7500, 640, "wd7x2")])
 def test_wd_silu_mul_int8_chain_and_two_phase(cuda, m, inter, k, cfg):
     from nanopointllm_amd import _lib, w8a8
 
@@ -107,7 +105,7 @@ def test_wd_silu_mul_int8_chain_and_two_phase(cuda, m, inter, k, cfg):
     np.testing.assert_array_equal(out.scale.cpu().numpy(), ts[:, 0])
 
 
-@pytest.mark.parametrize("m,n,k,cfg", [(560, 12288, 1000, "wd7x2"), (560, 4096, 2000, "wd9x1")])
+@pytest.mark.parametrize("m,n,k,cfg", [(560, 12288, 1000, "wd7x2"), (400, 15000, 2000, "wd7x2")])
 def test_wd_integer_epilogues(cuda, m, n, k, cfg):
     """requant1 (multiplier / shift int8 out) and the single-rounding
     int32 -> bf16 dequant on the weights-direct tiles."""
@@ -140,3 +138,28 @@ def test_wd_integer_epilogues(cuda, m, n, k, cfg):
         want = O.dequantize_int32_to_bf16(int(acc[i, j]), int(sa_bits[i]), int(sw_bits[j]))
         got = int(yb[i, j].view(torch.int16).item()) & 0xFFFF
         assert got == want, (i, j)
+
+
+@pytest.mark.parametrize("m,n,k,epi", [(8, 4096, 4096, "f16"), (96, 1000, 700, "i32"),
+                                       (560, 12288, 4096, "f16"), (560, 4096, 11008, "bf16"),
+                                       (567, 22016, 4096, "silu"), (1024, 4096, 4096, "f32")])
+def test_linear_packed_equals_linear_i8in(cuda, m, n, k, epi):
+    """w8a8_linear_packed (activations already in packed tiles, the GEMM
+    alone) gives the bits of w8a8_linear_i8in on the same row-major rows."""
+    from nanopointllm_amd import _lib, w8a8
+
+    xq, wq, sx, sw, bias = _case(m, n, k, seed=31 + m)
+    layout = _lib.ROWS_INTERLEAVE_HALVES if epi == "silu" else _lib.ROWS_AS_IS
+    note(f"linear_packed m={m} n={n} k={k} {epi} tile={gemm_config(m, n)}")
+    xd, wp = xq.to(cuda), w8a8.pack_rows(wq.to(cuda), layout)
+    sxt, swt, bt = (torch.from_numpy(a).to(cuda) for a in (sx, sw, bias))
+    code = {"i32": _lib.EPI_I32, "silu": _lib.EPI_SILU_MUL}.get(epi, _lib.EPI_DEQUANT)
+    dt = {"i32": torch.int32, "f16": torch.float16, "bf16": torch.bfloat16,
+          "f32": torch.float32, "silu": torch.float16}[epi]
+    b = bt if epi in ("f16", "f32") else None
+    ref = w8a8.linear_i8in(xd, sxt, wp, swt, b, n, epilogue=code, out_dtype=dt)
+    got = w8a8.linear_packed(w8a8.pack_rows(xd), sxt, m, k, wp, swt, b, n, epilogue=code,
+                             out_dtype=dt)
+    assert torch.equal(got, ref)
+    with pytest.raises(ValueError, match="packed tiles"):
+        w8a8.linear_packed(xd[: m // 2], sxt, m, k, wp, swt, b, n, epilogue=code, out_dtype=dt)
