@@ -311,8 +311,7 @@ def prefill_sweep(layers, device, m: int = 560) -> dict:
 
     lib = _lib.load()
     cus = torch.cuda.get_device_properties(device).multi_processor_count
-    names = ("tiny-deep", "small-deep", "big-deep", "big", "w192", "w224", "w256", "w256sq",
-             "mid", "wd7x2")
+    names = _lib.GEMM_TILE_NAMES
     out = {}
     for spec in W.PROJECTIONS:
         x16 = W.prefill_activations(m, spec.k, seed=11).to(device)

@@ -115,7 +115,9 @@ int64_t w8a8_workspace_bytes(int64_t m, int64_t k);
  * 64x64 (stages of four k-blocks), 2 = 128x128 (one workgroup per CU, stages
  * of two k-blocks), 3 = 128x128, 4 = 128x192, 5 = 128x224, 6 = 128x256,
  * 7 = 256x256 (one workgroup per CU, stages of two k-blocks), 8 = 64x32
- * (stages of four k-blocks, past 64 rows); -1
+ * (stages of four k-blocks, past 64 rows), 9 = 112x256 (weights straight
+ * to registers four k-blocks ahead, one workgroup per CU), 10 = 112x96
+ * (stages of three k-blocks), 11 = 128x96 (stages of four k-blocks); -1
  * for a negative or zero size.  A pure function of its arguments (no device
  * call): it lets tests name the configuration a shape exercises.  No
  * counterpart in the reference, whose products are dense F.linear calls. */

@@ -111,6 +111,8 @@ enum GemmTile : int {
   kGemmW256Sq = 7,     // 256x256, 16 waves, 2-stage ring of two k-blocks, 1 per CU
   kGemmMid = 8,        // 64x32, 4 waves, 3-stage ring of four k-blocks, 2 per CU
   kGemmWd7x2 = 9,      // 112x256 weights-direct, 8 waves of 112x32, 4 k-blocks ahead, 1 per CU
+  kGemmT112x96 = 10,   // 112x96, 14 waves of 16x48, 3-stage ring of three k-blocks, 1 per CU
+  kGemmT128x96 = 11,   // 128x96, 8 waves of 32x48, 2-stage ring of four k-blocks, 1 per CU
 };
 int gemm_tile_choice(int64_t MB, int64_t NB, int64_t cus);
 

@@ -26,6 +26,10 @@ ERR_TOO_LARGE = -7
 ERR_OVERLAP = -8
 NOALLOC_SCRATCH_BYTES = 64 << 20
 
+# Names of the GEMM tiles w8a8_gemm_tile_config returns, by code.
+GEMM_TILE_NAMES = ("tiny-deep", "small-deep", "big-deep", "big", "w192", "w224", "w256",
+                   "w256sq", "mid", "wd7x2", "t112x96", "t128x96")
+
 _TORCH_TO_CODE = {
     torch.float32: F32,
     torch.float16: F16,

@@ -7,15 +7,16 @@ from __future__ import annotations
 
 import pytest
 
-from gemm_tiles import gemm_config, wd_fits
+from gemm_tiles import gemm_config, narrow_fits, wd_fits
 
 QKV, O, GATEUP, DOWN = 12288, 4096, 22016, 4096
 
 
 @pytest.mark.parametrize("m,n,cfg", [
     (560, QKV, "wd7x2"), (768, QKV, "w192"), (1024, QKV, "w192"), (2048, QKV, "w256"),
-    (560, O, "big-deep"), (567, O, "big-deep"), (567, QKV, "big"), (768, O, "big-deep"),
-    (1024, O, "big-deep"), (480, QKV, "wd7x2"), (500, O, "small-deep"), (560, DOWN, "big-deep"),
+    (560, O, "t112x96"), (567, O, "t128x96"), (567, QKV, "big"), (768, O, "big-deep"),
+    (1024, O, "big-deep"), (480, QKV, "wd7x2"), (500, O, "t112x96"), (560, DOWN, "t112x96"),
+    (640, O, "t128x96"), (641, O, "big-deep"), (448, O, "small-deep"),
     (560, GATEUP, "w224"), (768, GATEUP, "big"), (1024, GATEUP, "w256"),
     (64, QKV, "tiny-deep"), (128, O, "mid"), (256, O, "mid"), (65, DOWN, "mid"),
     (100, 1000, "tiny-deep"), (160, 8192, "small-deep"), (128, 8192, "mid"),
@@ -37,6 +38,11 @@ def test_every_config_fits_one_round_or_is_the_widest():
             assert (cfg == "wd7x2") == wd_fits(m, n), (m, n, cfg)
             if cfg == "wd7x2":
                 continue
+            narrow = ("t112x96" if narrow_fits(m, n, 7) else
+                      "t128x96" if narrow_fits(m, n, 8) else None)
+            assert (cfg == narrow) if narrow else cfg not in ("t112x96", "t128x96"), (m, n, cfg)
+            if narrow:
+                continue
             mb, nb = -(-m // 16), -(-n // 16)
             tm = -(-mb // 8)
             tiles = {"w192": tm * -(-nb // 12), "w224": tm * -(-nb // 14),
@@ -54,7 +60,7 @@ def test_every_config_fits_one_round_or_is_the_widest():
             mb, nb = -(-m // 16), -(-n // 16)
             mid = -(-mb // 4) * -(-nb // 2)
             fits = mb > 4 and 128 <= mid <= 512 and -(-mb // 8) * -(-nb // 8) <= 512
-            if wd_fits(m, n):
+            if wd_fits(m, n) or narrow_fits(m, n, 7) or narrow_fits(m, n, 8):
                 continue
             assert (gemm_config(m, n) == "mid") == fits, (m, n)
 

@@ -56,9 +56,9 @@ def _case(m, n, k, seed):
 # 3100 -> 49 (a last 128-K stage of one k-block), 4250 -> 67 (a last 256-K
 # stage of three), 11008 -> 172, and 70 (one 256-K stage of two).
 SHAPES = [
-    (600, 4000, 4197, "big-deep"),
-    (520, 4100, 3100, "big-deep"),
-    (640, 4096, 70, "big-deep"),
+    (760, 4096, 4197, "big-deep"),
+    (800, 4100, 3100, "big-deep"),
+    (800, 4096, 70, "big-deep"),
     (1000, 4096, 1000, "big-deep"),
     (700, 4100, 70, "big-deep"),
     (130, 12288, 3100, "big-deep"),
@@ -95,7 +95,7 @@ def test_deep_stage_int32_and_dequant(cuda, m, n, k, cfg):
                                           err_msg=f"{dt} bias={b is not None}")
 
 
-@pytest.mark.parametrize("m,inter,k", [(600, 2000, 4197), (300, 3000, 4250), (100, 500, 4250),
+@pytest.mark.parametrize("m,inter,k", [(760, 2048, 4197), (300, 3000, 4250), (100, 500, 4250),
                                       (96, 2048, 4197)])
 def test_deep_stage_silu_mul_and_int8_chain(cuda, m, inter, k):
     from nanopointllm_amd import _lib, w8a8
@@ -122,7 +122,7 @@ def test_deep_stage_silu_mul_and_int8_chain(cuda, m, inter, k):
     np.testing.assert_array_equal(hq.cpu().numpy(), eq)
 
 
-@pytest.mark.parametrize("m,n,k", [(600, 4000, 4197), (300, 6000, 4250), (100, 1000, 4250),
+@pytest.mark.parametrize("m,n,k", [(760, 4096, 4197), (300, 6000, 4250), (100, 1000, 4250),
                                    (128, 4096, 3100)])
 def test_deep_stage_requant1_epilogue(cuda, m, n, k):
     from nanopointllm_amd import integer_epilogues as E, w8a8
