@@ -360,11 +360,14 @@ def prefill_sweep_all(layers, device) -> dict:
     return {f"M{m}": prefill_sweep(layers, device, m) for m in (560, 768, 1024)}
 
 
-def qkv_m_sweep(layers, device, ms_list=(1, 2, 4, 16, 64, 256, 2048)) -> dict:
-    """GEMV -> MFMA crossover on the packed QKV shape (fused linear, fp16 in)."""
-    from nanopointllm_amd import w8a8, workloads as W
+def m_sweep(layers, device, proj: str, ms_list) -> dict:
+    """Per-launch time of one projection's fused linear (fp16 in: quantize +
+    product, or the fused decode kernel) across row counts: the GEMV / MFMA
+    crossover and the 17..64-row regime of batched decode."""
+    from nanopointllm_amd import _lib, w8a8, workloads as W
 
-    spec = {p.name: p for p in W.PROJECTIONS}["qkv"]
+    spec = {p.name: p for p in W.PROJECTIONS}[proj]
+    epi = _lib.EPI_SILU_MUL if spec.silu else _lib.EPI_DEQUANT
     sub = layers[:8]
     out = {}
     for m in ms_list:
@@ -373,13 +376,13 @@ def qkv_m_sweep(layers, device, ms_list=(1, 2, 4, 16, 64, 256, 2048)) -> dict:
 
         def run(x16=x16):
             for layer in sub:
-                p = layer.weights["qkv"]
-                w8a8.linear_dynamic(x16, p.packed, p.scale, None, p.out_features)
+                p = layer.weights[proj]
+                w8a8.linear_dynamic(x16, p.packed, p.scale, None, p.out_features, epilogue=epi)
 
         ms, g = time_graph(run, steps=10, warmup=3)
         del g
         per = ms / len(sub)
-        nbytes = W.algorithmic_bytes(m, spec.n, spec.k)
+        nbytes = W.algorithmic_bytes(m, spec.n, spec.k, silu=spec.silu)
         out[f"M{m}"] = {"us": round(per * 1e3, 2),
                         "GBps": round(nbytes / (per * 1e-3) / 1e9, 1),
                         "TOPS": round(W.algorithmic_ops(m, spec.n, spec.k) / (per * 1e-3) / 1e12, 1)}
@@ -767,7 +770,9 @@ def main() -> int:
         log("prefill sweep M=560,768,1024")
         extra["prefill"] = prefill_sweep_all(layers, device)
         log("QKV M sweep")
-        extra["qkv_m_sweep"] = qkv_m_sweep(layers, device)
+        extra["qkv_m_sweep"] = m_sweep(layers, device, "qkv",
+                                       (1, 2, 4, 16, 17, 24, 32, 48, 64, 256, 2048))
+        extra["gateup_m_sweep"] = m_sweep(layers, device, "gateup", (17, 24, 32, 48, 64))
         log("mixed M=567 int8 chain")
         extra["mixed_567_gateup_down_int8_chain"] = mixed_chain(layers, device)
         log("stack without the LM head")

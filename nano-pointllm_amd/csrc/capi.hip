@@ -168,11 +168,13 @@ LinearOperands make_ops(const int8_t* a, int64_t lda, const float* sx, const int
 
 // GEMV or GEMM for an m x n product.  The GEMV's time grows with M (each
 // weight fragment meets M activation rows) while the GEMM's barely does at
-// M <= 64; measured on MI355X with LLaMA-7B shapes at M = 24..64, the GEMM
-// wins once M * N >= 32 * 12288 (QKV from M = 32, gate/up from M = 24) and
-// the GEMV keeps the N = 4096 projections (O, down) up to M = 64.
+// M <= 64; measured on MI355X with LLaMA-7B shapes at M = 17..64 (quantize
+// + product), the GEMV takes every projection up to M = 32 (QKV at M = 32 in
+// 15.8 against 19.8 us, gate/up 24.5 against 25.8) and those with N <= 12288
+// up to M = 64 (QKV at M = 48 / 64 18.7 / 20.6 against 20.9 / 21.1), while
+// the GEMM keeps gate/up past 32 rows (26.9 against 31.0 us at M = 48).
 inline bool use_gemv(int64_t m, int64_t n) {
-  return m <= kGemvMaxRows && (m <= 16 || m * n < 32 * 12288);
+  return m <= kGemvMaxRows && (m <= 32 || n <= 12288);
 }
 
 // Runs the int8 product for activations already staged in `act` (row-major
