@@ -88,7 +88,8 @@ def profile_proj(device, name: str, m: int) -> dict:
     after a 256 MiB copy that calibrates the traffic counters."""
     import torch
 
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
 
     src = torch.empty(CALIBRATION_COPY_BYTES, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
@@ -117,7 +118,8 @@ def profile_gemm(device) -> dict:
     layers' cold weights, after a 256 MiB copy that calibrates the counters."""
     import torch
 
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
 
     src = torch.empty(CALIBRATION_COPY_BYTES, dtype=torch.uint8, device=device)
     dst = torch.empty_like(src)
@@ -144,7 +146,8 @@ class Layer:
     def __init__(self, idx: int, m: int, device):
         import torch
 
-        from nanopointllm_amd import _lib, w8a8, workloads as W
+        from nanopointllm_amd import _lib, w8a8
+        import workloads as W
         from nanopointllm_amd.linear import PackedW8A8Weight
 
         self.weights = {}
@@ -170,7 +173,7 @@ class Layer:
 
 
 def step_bytes(m: int, layers: int) -> int:
-    from nanopointllm_amd import workloads as W
+    import workloads as W
 
     return layers * sum(W.algorithmic_bytes(m, p.n, p.k, silu=p.silu) for p in W.PROJECTIONS)
 
@@ -222,7 +225,8 @@ def gateup_kernel_roofline(layers, m: int, device) -> dict:
     quantization and the GEMV launch are both counted."""
     import torch
 
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
 
     spec = {p.name: p for p in W.PROJECTIONS}["gateup"]
     x = layers[0].x["gateup"]
@@ -270,7 +274,8 @@ def projection_sweep(layers, device, ms_list=(1, 4, 8)) -> dict:
     """Decode GB/s per projection (graph of 32 launches over distinct weights)."""
     import torch
 
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
 
     out = {}
     for m in ms_list:
@@ -307,7 +312,8 @@ def prefill_sweep(layers, device, m: int = 560) -> dict:
       (``w8a8_linear_packed``), with the tile the library picks."""
     import torch
 
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
 
     lib = _lib.load()
     cus = torch.cuda.get_device_properties(device).multi_processor_count
@@ -364,7 +370,8 @@ def m_sweep(layers, device, proj: str, ms_list) -> dict:
     """Per-launch time of one projection's fused linear (fp16 in: quantize +
     product, or the fused decode kernel) across row counts: the GEMV / MFMA
     crossover and the 17..64-row regime of batched decode."""
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
 
     spec = {p.name: p for p in W.PROJECTIONS}[proj]
     epi = _lib.EPI_SILU_MUL if spec.silu else _lib.EPI_DEQUANT
@@ -394,7 +401,8 @@ def mixed_chain(layers, device, h_scale_m: int = 567) -> dict:
     requant (static scale) -> int8-in down projection."""
     import torch
 
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
 
     m = h_scale_m
     x = torch.cat([W.decode_activations(7, W.HIDDEN, seed=21),
@@ -431,7 +439,8 @@ def decode_step_int8_mlp(layers, m: int, device) -> dict:
     launch.  QKV and O are as in the default step."""
     import torch
 
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
     from nanopointllm_amd.w8a8 import static_activation_scale
 
     x0, gu0 = layers[0].x["gateup"], layers[0].weights["gateup"]
@@ -470,7 +479,7 @@ def lm_head(m: int, device):
     F.linear: the LM head is not a W8A8 linear), with its algorithmic bytes."""
     import torch
 
-    from nanopointllm_amd import workloads as W
+    import workloads as W
 
     g = torch.Generator(device=device)
     g.manual_seed(99)
@@ -507,7 +516,7 @@ def runner_decode_step(m: int, device, steps: int = 20, warmup: int = 5) -> dict
     lightweight_runner.py:362-379)."""
     import torch
 
-    from nanopointllm_amd import workloads as W
+    import workloads as W
     from nanopointllm_amd.runner import DecodeGraphBucket, W8A8LlamaRunner
     from nanopointllm_amd.w8a8 import static_activation_scale
 
@@ -603,7 +612,7 @@ def cpu_baseline(layers, m: int) -> dict:
     headline's unit."""
     import torch
 
-    from nanopointllm_amd import workloads as W
+    import workloads as W
     from oracle import torch_path as T, w8a8_oracle as O
 
     cores = len(os.sched_getaffinity(0))
@@ -664,7 +673,8 @@ def parity_report(layers, m: int, device) -> dict:
     path's binary32 values and the fraction bit-equal to its fp16 result."""
     import torch
 
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
     from nanopointllm_amd.linear import PackedW8A8Weight
     from oracle import torch_path as T, w8a8_oracle as O
 
@@ -714,7 +724,8 @@ def main() -> int:
         return 2
     import torch
 
-    from nanopointllm_amd import _lib, workloads as W
+    from nanopointllm_amd import _lib
+    import workloads as W
 
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)

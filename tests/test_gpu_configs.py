@@ -59,7 +59,7 @@ def _errors(got16: np.ndarray, ref32: np.ndarray) -> tuple[float, float]:
 def _weights(proj: str):
     """Config weights quantized per output row by the oracle; gate/up in the
     interleaved packed row order.  Returns (int8 [N, K], f32 scales [N])."""
-    from nanopointllm_amd import workloads as W
+    import workloads as W
 
     if proj == "gateup":
         _, qg, sg = O.per_output_weight_qdq(W.linear_weight(INTER, HIDDEN, seed=21).float().numpy())
@@ -110,7 +110,8 @@ def test_silu_mul_against_torch_cpu_silu(cuda, m):
     against torch's CPU ``F.silu`` applied to the kernel's own dequantized
     gate and up (the same product with the dequant epilogue): bit-equal,
     the sign of zero included."""
-    from nanopointllm_amd import _lib, workloads as W
+    from nanopointllm_amd import _lib
+    import workloads as W
 
     n = 2 * INTER
     x = (W.decode_activations(m, HIDDEN, seed=60) if m <= 16 else
@@ -174,7 +175,8 @@ def test_decode_gateup_fused_silu_full_shape(cuda, m):
     """fp16 x -> fused per-token quant -> 22016 x 4096 int8 GEMV -> SiLU*mul
     (and its int8 requant twin) in one launch: a call without workspace
     succeeds only on the fused decode kernel."""
-    from nanopointllm_amd import _lib, workloads as W
+    from nanopointllm_amd import _lib
+    import workloads as W
 
     n = 2 * INTER
     x = W.decode_activations(m, HIDDEN, seed=40 + m)
@@ -212,7 +214,8 @@ def test_decode_gateup_fused_silu_full_shape(cuda, m):
 @pytest.mark.parametrize("m", [1, 4, 8])
 @pytest.mark.parametrize("proj", ["qkv", "o", "down"])
 def test_decode_projections(cuda, proj, m):
-    from nanopointllm_amd import w8a8, workloads as W
+    from nanopointllm_amd import w8a8
+    import workloads as W
 
     q, s = _weights(proj)
     n, k = q.shape
@@ -235,7 +238,8 @@ def test_decode_projections(cuda, proj, m):
 @pytest.mark.parametrize("m", [768, 1024])
 @pytest.mark.parametrize("proj", ["qkv", "o", "gateup", "down"])
 def test_prefill_projections(cuda, proj, m):
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
 
     q, s = _weights(proj)
     n, k = q.shape
@@ -261,7 +265,8 @@ def test_prefill_projections(cuda, proj, m):
 # ------------------------------------------------------------- config 5
 @pytest.mark.parametrize("m", [64, 256, 2048])
 def test_qkv_m_sweep(cuda, m):
-    from nanopointllm_amd import w8a8, workloads as W
+    from nanopointllm_amd import w8a8
+    import workloads as W
 
     q, s = _weights("qkv")
     n, k = q.shape
@@ -282,7 +287,8 @@ def test_mixed_step_int8_mlp_chain_full_shape(cuda):
     """M = 567 (7 decode rows + one 560-row prefill chunk) through packed
     gate/up with SiLU*mul and static int8 requant, then the int8-in down
     projection, checked stage by stage at the LLaMA-7B shapes."""
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
 
     x = torch.cat([W.decode_activations(7, HIDDEN, seed=80),
                    W.prefill_activations(560, HIDDEN, seed=81)])
@@ -327,7 +333,8 @@ def test_decode_mlp_two_phase_full_shape(cuda, m):
     """The decode MLP with the two-phase per-token requantization of h at the
     LLaMA-7B shapes: gate/up 22016 x 4096 (fused decode kernel folding |h|max)
     -> per-token int8 h -> down 4096 x 11008 on it, checked stage by stage."""
-    from nanopointllm_amd import w8a8, workloads as W
+    from nanopointllm_amd import w8a8
+    import workloads as W
 
     x = W.decode_activations(m, HIDDEN, seed=90 + m)
     wgu, swgu = _device_weight("gateup", cuda)

@@ -48,7 +48,7 @@ def rand_i8(shape, seed):
 def weight_q(n, k, seed):
     """Seeded weight [n, k] and its per-output int8 quantization (cached: the
     arrays are only read)."""
-    from nanopointllm_amd import workloads as W
+    import workloads as W
 
     w = W.linear_weight(n, k, seed=seed)
     _, q, s = O.per_output_weight_qdq(w.float().numpy())
@@ -257,7 +257,8 @@ def _expected_linear(x: torch.Tensor, q: np.ndarray, s: np.ndarray, bias=None):
 
 def test_config1_single_linear_bit_exact(cuda):
     """X fp16 [16,4096] with 8 outlier channels x20, W [4096,4096] ~N(0,0.02), seed 0."""
-    from nanopointllm_amd import linear, workloads as W
+    from nanopointllm_amd import linear
+    import workloads as W
 
     x, w = W.config1(seed=0)
     note("config1 M=16 4096x4096")
@@ -712,7 +713,8 @@ def test_packed_qkv_split_matches_separate_linears(cuda):
 @pytest.mark.parametrize("m", [1, 8, 560])
 @pytest.mark.parametrize("proj", ["qkv", "o", "gateup", "down"])
 def test_llama7b_shapes_exact(cuda, m, proj):
-    from nanopointllm_amd import w8a8, workloads as W
+    from nanopointllm_amd import w8a8
+    import workloads as W
 
     spec = {p.name: p for p in W.PROJECTIONS}[proj]
     x = (W.decode_activations(m, spec.k, seed=m) if m <= 16

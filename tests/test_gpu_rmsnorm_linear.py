@@ -57,7 +57,7 @@ def _ulps(a: np.ndarray, b: np.ndarray, dtype: str) -> np.ndarray:
 def _weights(proj: str, k: int = HIDDEN):
     """int8 [N, K] and binary32 scales [N] quantized per output row by the
     oracle (gate/up in the interleaved packed row order), and a bias."""
-    from nanopointllm_amd import workloads as W
+    import workloads as W
 
     if proj == "gateup":
         _, qg, sg = O.per_output_weight_qdq(W.linear_weight(INTER, k, seed=61).float().numpy())

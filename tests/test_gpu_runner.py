@@ -28,7 +28,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
-from nanopointllm_amd.workloads import LlamaShaped
+from workloads import LlamaShaped
 
 pytestmark = pytest.mark.gpu
 

@@ -57,7 +57,8 @@ CASES = [
 
 @pytest.mark.parametrize("label,m,inter,k,int8_x", CASES)
 def test_two_phase_matches_plain_silu_and_oracle(cuda, label, m, inter, k, int8_x):
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
 
     p = _gateup(inter, k, seed=m + inter, cuda=cuda)
     x = (W.decode_activations(m, k, seed=m) if m <= 16
@@ -87,7 +88,8 @@ def test_mlp_two_phase_chain_equals_plain_dynamic_chain(cuda, m):
     """W8A8MLP's two-phase chain gives the same bits as gate/up -> fp16 h ->
     down with its own per-token quantization, and down on the GPU's int8 h
     is exact against the oracle."""
-    from nanopointllm_amd import linear, workloads as W
+    from nanopointllm_amd import linear
+    import workloads as W
 
     inter, k = 2752, 1024
     g = torch.Generator().manual_seed(9)
@@ -114,7 +116,8 @@ def test_mlp_two_phase_chain_equals_plain_dynamic_chain(cuda, m):
 def test_two_phase_graph_replays(cuda):
     """Captured in a graph and replayed with eager work between replays:
     every replay equals the eager result."""
-    from nanopointllm_amd import w8a8, workloads as W
+    from nanopointllm_amd import w8a8
+    import workloads as W
 
     p = _gateup(2752, 4096, seed=5, cuda=cuda)
     x = W.decode_activations(8, 4096, seed=6).to(cuda)
@@ -185,7 +188,8 @@ def test_two_phase_full_size_gateup(cuda, gateup_full, down_full, m):
     against the oracle's per-token quantization of that h, and the down
     projection on hq is exact against the oracle (on a sample of rows)."""
     from gemm_tiles import gemm_config
-    from nanopointllm_amd import _lib, w8a8, workloads as W
+    from nanopointllm_amd import _lib, w8a8
+    import workloads as W
 
     p = gateup_full
     x = W.prefill_activations(m, 4096, seed=m, point_tokens=min(513, m - 7)).to(cuda)

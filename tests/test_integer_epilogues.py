@@ -147,7 +147,7 @@ def test_dequant_bf16_locked_vectors_and_random(cuda):
 
 
 def _weights(n, k, seed):
-    from nanopointllm_amd import workloads as W
+    import workloads as W
 
     _, q, s = O.per_output_weight_qdq(W.linear_weight(n, k, seed=seed).float().numpy())
     return q, s
@@ -179,7 +179,7 @@ def test_linear_i8in_requant_fused(cuda, m):
 
     # the module: same compile on the GPU-quantized weights
     lin = torch.nn.Linear(k, n, bias=False)
-    from nanopointllm_amd import workloads as W
+    import workloads as W
     lin.weight.data = W.linear_weight(n, k, seed=m).to(cuda)
     mod = E.StaticA8RequantLinear(lin, act_scale, out_scale)
     ym = mod(xq.to(cuda)).cpu().numpy()

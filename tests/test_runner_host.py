@@ -57,7 +57,7 @@ def test_final_norm_routing():
     """Binary32 rows (or a norm weight of another dtype) run the model's own
     norm module on dtype(hidden + residual); 16-bit rows with a matching
     weight go to the activation prologue kernel, which has no host path."""
-    from nanopointllm_amd.workloads import RMSNorm
+    from workloads import RMSNorm
 
     norm = RMSNorm(8)
     with torch.no_grad():

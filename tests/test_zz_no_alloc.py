@@ -24,7 +24,8 @@ def note(msg: str) -> None:
 
 
 def _case(m: int, n: int, k: int, seed: int, cuda):
-    from nanopointllm_amd import w8a8, workloads as W
+    from nanopointllm_amd import w8a8
+    import workloads as W
 
     x = W.prefill_activations(m, k, seed=seed, point_tokens=m // 2).to(cuda)
     g = torch.Generator().manual_seed(seed + 1)

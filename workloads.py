@@ -8,6 +8,9 @@ llama/lightweight_runner.py:57-93).  There is no network, so weights are
 random-initialised ~N(0, 0.02) and activations are seeded normals with
 outlier channels, generated on the CPU with ``torch.Generator`` (the same
 values on every machine) unless a device generator is requested.
+
+Bench and test support (bench.py, __graft_entry__.smoke and tests/), kept
+outside the nanopointllm_amd package: nothing in the package imports it.
 """
 from __future__ import annotations
 
