@@ -76,6 +76,10 @@ def parse_args():
                          "x 5 repetitions, after the counter-calibration copy (the region "
                          "rocprofv3 runs of that projection measure)")
     ap.add_argument("--profile-m", type=int, default=8)
+    ap.add_argument("--profile-timeline", action="store_true",
+                    help="only the start-up timeline of the fused gate/up decode kernel at --m "
+                         "rows: 32 layers' launches in a graph on the timestamp build "
+                         "(libw8a8_gfx950_timeline.so), per-workgroup phases of the last one")
     ap.add_argument("--profile-runner", action="store_true",
                     help="only the whole-model decode step through W8A8LlamaRunner at --m rows "
                          "(32 LLaMA-7B-shaped layers, LM head), captured and replayed (the "
@@ -111,6 +115,76 @@ def profile_proj(device, name: str, m: int) -> dict:
     return {"projection": name, "m": m, "n": spec.n, "k": spec.k, "launches": 20,
             "host_ms_per_call": round(ms, 4),
             "algorithmic_bytes": W.algorithmic_bytes(m, spec.n, spec.k, silu=spec.silu)}
+
+
+def profile_timeline(device, m: int) -> dict:
+    """Per-workgroup start-up timeline of the fused gate/up decode kernel
+    (22016 x 4096, binary16 x of m rows, SiLU*mul), from the timestamp build of
+    the library: 32 layers' launches captured in a graph and replayed, then
+    the stamps of the last launch (100 MHz real-time counter, microseconds
+    from the earliest workgroup's entry; medians and ranges over the
+    workgroups)."""
+    import ctypes
+    import statistics
+
+    import torch
+
+    from nanopointllm_amd import _lib, build as _build, w8a8
+    import workloads as W
+    from nanopointllm_amd.linear import PackedW8A8Weight
+
+    spec = {p.name: p for p in W.PROJECTIONS}["gateup"]
+    weights = [PackedW8A8Weight.from_float(
+        W.linear_weight(spec.n, spec.k, seed=500 + i, device=device), None,
+        layout=_lib.ROWS_INTERLEAVE_HALVES) for i in range(32)]
+    x = W.decode_activations(m, spec.k, seed=5).to(device)
+
+    def run():
+        for p in weights:
+            w8a8.linear_dynamic(x, p.packed, p.scale, None, p.out_features,
+                                epilogue=_lib.EPI_SILU_MUL)
+
+    # The same graph on the library proper, then on the timestamp build.
+    plain_ms, g = time_graph(run, steps=20, warmup=3)
+    del g
+    lib = _lib.load(_build.TIMELINE_LIB_PATH)
+    lib.w8a8_timeline_read.restype = ctypes.c_int
+    lib.w8a8_timeline_read.argtypes = [ctypes.c_void_p, ctypes.c_int]
+    _lib._lib = lib   # the wrappers now call into the timestamp build
+    ms, g = time_graph(run, steps=20, warmup=3)
+    torch.cuda.synchronize()
+    cus = torch.cuda.get_device_properties(device).multi_processor_count
+    nb = -(-spec.n // 16)
+    groups = min(nb, cus)
+    buf = (ctypes.c_ulonglong * (groups * 16))()
+    if lib.w8a8_timeline_read(ctypes.addressof(buf), groups) != 0:
+        raise RuntimeError("w8a8_timeline_read failed")
+    stamps = [[buf[wg * 16 + i] for i in range(16)] for wg in range(groups)]
+    t0 = min(st[0] for st in stamps)
+    us = lambda v: (v - t0) / 100.0  # noqa: E731
+
+    def dist(vals):
+        return {"median": round(statistics.median(vals), 2), "min": round(min(vals), 2),
+                "max": round(max(vals), 2)}
+
+    phases = {"entry": 0, "x_ready": 1, "prologue_done": 2, "first_weight_data": 3,
+              "first_block_done": 4, "end": 15}
+    out = {name: dist([us(st[i]) for st in stamps]) for name, i in phases.items()}
+    # Blocks after the first: the workgroup's steady rate.
+    intervals = []
+    for wg, st in enumerate(stamps):
+        n_mine = (nb - wg + groups - 1) // groups
+        blocks = [st[4 + j] for j in range(min(n_mine, 11))]
+        intervals += [(b - a) / 100.0 for a, b in zip(blocks[1:], blocks[2:])]
+    block_bytes = 16 * spec.k
+    per_block = statistics.median(intervals)
+    return {"kernel": "gemv_fused_kernel (packed gate/up, SiLU*mul)", "m": m, "n": spec.n,
+            "k": spec.k, "workgroups": groups,
+            "us_per_launch_graph_plain": round(plain_ms * 1e3 / 32, 3),
+            "us_per_launch_graph_timeline": round(ms * 1e3 / 32, 3),
+            "phases_us": out, "steady_block_us": round(per_block, 3),
+            "steady_GBps_per_cu": round(block_bytes / (per_block * 1e-6) / 1e9, 1),
+            "steady_TBps_all_cus": round(block_bytes * groups / (per_block * 1e-6) / 1e12, 2)}
 
 
 def profile_gemm(device) -> dict:
@@ -740,6 +814,9 @@ def main() -> int:
                                                         args.profile_m)}))
         return 0
     m = args.m
+    if args.profile_timeline:
+        print(json.dumps({"profile_timeline": profile_timeline(device, m)}))
+        return 0
     if args.profile_runner:
         print(json.dumps({"profile_runner": runner_decode_step(m, device)}))
         return 0

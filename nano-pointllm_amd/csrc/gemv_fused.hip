@@ -94,6 +94,31 @@ __device__ inline i32x4 mfma_16x16x64(i32x4 a, i32x4 b, i32x4 c) {
   return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
 }
 
+// Start-up timeline (diagnostic builds with W8A8_TIMELINE only; the library
+// proper compiles none of it).  Thread 0 of each workgroup notes the 100 MHz
+// real-time counter in LDS at fixed points of the launch (kStamp* below) and
+// copies them to g_stamps at the end; w8a8_timeline_read fetches the last
+// launch's values.
+#if W8A8_TIMELINE
+constexpr int kStampsPerWg = 16;
+constexpr int kStampEntry = 0;      // kernel entry
+constexpr int kStampXReady = 1;     // wavefront 0 has x and its absmax
+constexpr int kStampPrologue = 2;   // quantization done, ring issued, barrier passed
+constexpr int kStampFirstData = 3;  // the first weight step's MFMAs issued (its data arrived)
+constexpr int kStampBlock0 = 4;     // 4 + j: epilogue of block j done (j < 11)
+constexpr int kStampEnd = 15;       // main loop done
+constexpr int kTimelineMaxWg = 1024;
+__device__ unsigned long long g_stamps[kTimelineMaxWg * kStampsPerWg];
+#define W8A8_STAMP(slot, i)                                             \
+  do {                                                                  \
+    if (threadIdx.x == 0) (slot)[(i)] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define W8A8_STAMP(slot, i) \
+  do {                      \
+  } while (0)
+#endif
+
 // |x| of 16-bit floats as unsigned integers (the sign bit cleared): for
 // non-negative binary16 / bfloat16 values the bit patterns order like the
 // values, so the integer max is the absmax.
@@ -197,6 +222,11 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   __shared__ float ss_g[NORM ? kFusedMaxRows : 1][8];  // RMSNorm: per row, 8 groups
   __shared__ float row_s[ROWS];
   __shared__ float ops_lds[kFusedMaxBlocks * 32];  // per block: 16 scales, 16 biases
+#if W8A8_TIMELINE
+  __shared__ unsigned long long stamps[kStampsPerWg];
+  if (threadIdx.x < kStampsPerWg) stamps[threadIdx.x] = 0;
+#endif
+  W8A8_STAMP(stamps, kStampEntry);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -485,6 +515,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   }
   uint32_t am = max(static_cast<uint32_t>(am2[0]), static_cast<uint32_t>(am2[1]));
   am = wave_max_u32(am);
+  W8A8_STAMP(stamps, kStampXReady);
   // The first weight loads go out once x has arrived (the absmax above waits
   // for it) and stream while x is quantized.  Only kFusedPreSteps steps go out
   // before the quantization: a wave that issues more loads than the CU's
@@ -539,6 +570,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   for (int u = kFusedPreSteps; u < RING - 1; ++u) issue(rb[u]);
   __syncthreads();
   }
+  W8A8_STAMP(stamps, kStampPrologue);
 
   // ------------------------------------------------------- stream weights
   const bool a_live = li < M;
@@ -569,14 +601,27 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       __syncthreads();
       const int64_t nb = static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(j) * p.G;
       epilogue<EPI, TY, TH>(p, red[par], row_s, nb, tid, ops_lds + j * 32);
+#if W8A8_TIMELINE
+      if (j < kStampEnd - kStampBlock0) W8A8_STAMP(stamps, kStampBlock0 + j);
+#endif
     }
     j += last ? 1 : 0;
     c = last ? 0 : c + 1;
   };
   for (int t = 0; t < total; t += RING) {
 #pragma unroll
-    for (int u = 0; u < RING; ++u) step(rb[u], rb[(u + RING - 1) % RING], t + u);
+    for (int u = 0; u < RING; ++u) {
+      step(rb[u], rb[(u + RING - 1) % RING], t + u);
+#if W8A8_TIMELINE
+      if (t + u == 0) W8A8_STAMP(stamps, kStampFirstData);
+#endif
+    }
   }
+  W8A8_STAMP(stamps, kStampEnd);
+#if W8A8_TIMELINE
+  if (threadIdx.x < kStampsPerWg && blockIdx.x < kTimelineMaxWg)
+    g_stamps[blockIdx.x * kStampsPerWg + threadIdx.x] = stamps[threadIdx.x];
+#endif
 }
 
 template <int EPI, typename TX, typename TY, typename TH>
@@ -868,3 +913,17 @@ hipError_t launch_gemv_fused_i8(const LinearOperands& op, hipStream_t st) {
 }
 
 }  // namespace w8a8
+
+#if W8A8_TIMELINE
+// Diagnostic export of the timeline build: copies the stamps of the last
+// fused launch (kStampsPerWg per workgroup, workgroups [0, n_wg)) to host
+// memory.  Not part of the C ABI of include/w8a8_gfx950.h.
+extern "C" int w8a8_timeline_read(unsigned long long* host_dst, int n_wg) {
+  if (host_dst == nullptr || n_wg < 0 || n_wg > w8a8::kTimelineMaxWg) return -1;
+  return hipMemcpyFromSymbol(host_dst, HIP_SYMBOL(w8a8::g_stamps),
+                             sizeof(unsigned long long) * w8a8::kStampsPerWg * n_wg, 0,
+                             hipMemcpyDeviceToHost) == hipSuccess
+             ? 0
+             : -6;
+}
+#endif

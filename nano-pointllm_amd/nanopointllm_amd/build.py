@@ -2,7 +2,11 @@
 
 ``python -m nanopointllm_amd.build`` (with ``nano-pointllm_amd`` on
 ``sys.path``) compiles every ``csrc/*.hip`` translation unit in parallel and
-links the shared library next to this file.
+links the shared library next to this file.  It also links the diagnostic
+``libw8a8_gfx950_timeline.so``: the same objects with the fused decode
+kernel rebuilt under ``W8A8_TIMELINE`` (per-workgroup start-up timestamps,
+read back through ``w8a8_timeline_read``), which ``bench.py
+--profile-timeline`` loads.  The library proper contains none of it.
 """
 from __future__ import annotations
 
@@ -20,6 +24,8 @@ INCLUDE = ROOT.parent / "include"          # repository include/ (public C heade
 BUILD_DIR = ROOT / "_build"
 LIB_NAME = "libw8a8_gfx950.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+TIMELINE_LIB_PATH = PKG_DIR / "libw8a8_gfx950_timeline.so"
+TIMELINE_SOURCE = "gemv_fused.hip"
 ARCH = "gfx950"
 
 
@@ -52,9 +58,10 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *compile_flags(), "-c", str(src), "-o", str(obj)]
+def _compile(src: Path, timeline: bool = False) -> Path:
+    obj = BUILD_DIR / (src.stem + ("_timeline" if timeline else "") + ".o")
+    defs = ["-DW8A8_TIMELINE=1"] if timeline else []
+    cmd = [hipcc(), *compile_flags(), *defs, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stdout}\n{proc.stderr}")
@@ -67,19 +74,29 @@ def build(verbose: bool = False) -> Path:
     srcs = sources()
     if not srcs:
         raise RuntimeError(f"no HIP sources under {CSRC}")
-    workers = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    jobs = [(src, False) for src in srcs]
+    jobs += [(src, True) for src in srcs if src.name == TIMELINE_SOURCE]
+    workers = min(len(jobs), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(max_workers=workers) as pool:
-        objs = list(pool.map(_compile, srcs))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+        objs = list(pool.map(lambda job: _compile(*job), jobs))
+    plain = [o for o, (_, tl) in zip(objs, jobs) if not tl]
+    timeline = [o for o, (src, tl) in zip(objs, jobs)
+                if tl or (src.name != TIMELINE_SOURCE)]
+    for path, group in ((LIB_PATH, plain), (TIMELINE_LIB_PATH, timeline)):
+        _link(path, group)
+        if verbose:
+            print(f"built {path}", file=sys.stderr)
+    return LIB_PATH
+
+
+def _link(path: Path, objs: list[Path]) -> None:
+    tmp = path.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp),
            *map(str, objs)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stdout}\n{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
-    if verbose:
-        print(f"built {LIB_PATH}", file=sys.stderr)
-    return LIB_PATH
+    os.replace(tmp, path)
 
 
 if __name__ == "__main__":
