@@ -5,7 +5,8 @@
 // 1488; llama/lightweight_runner.py:320-404) for the int8 contract of
 // integer_linear_per_output_reference (nanopointllm/compression/w8a8.py:118-139).
 //
-// Design (MFMA-bound), chosen by measurement on MI355X:
+// Design (MFMA-bound), chosen by measurement on MI355X (gemm_kernel; the
+// weights-direct gemm_wd_kernel further below keeps the weights out of LDS):
 //   * v_mfma_i32_16x16x64_i8.  Its operand is exactly one packed 16x64
 //     fragment (lane l holds 16 bytes of row l%16), read with one contiguous
 //     ds_read_b128.  On random int8 data it sustains more than the 32x32x32
@@ -17,8 +18,9 @@
 //     of 64x64) when there are enough such tiles to fill every CU twice, else
 //     128x128 (16 wavefronts of 32x32), else 64x64 (4 wavefronts of 32x32,
 //     4 workgroups per CU) when 128x128 tiles would not cover every CU; past
-//     64 rows, 64x32 (4 wavefronts of 32x16) when those fill one round.  The
-//     full rule is at launch_t.
+//     64 rows, 64x32 (4 wavefronts of 32x16) when those fill one round; and
+//     112x96 (14 wavefronts of 16x48) or 128x96 (8 of 32x48), one per CU,
+//     when one round of those fills the CUs.  The full rule is at launch_t.
 //   * Both operands are in the packed 16x64 tile layout, so a k-step (64) of
 //     the workgroup tile is (BM + BN)/16 fragments of 1 KiB.  Each wavefront
 //     copies its share with global_load_lds_dwordx4 straight into a 3- or
@@ -545,6 +547,10 @@ hipError_t launch_cfg(GemmParams p, hipStream_t st) {
 // cold weights, LLaMA-7B projections at M = 256..2048).  A launch is fastest
 // when its tiles fill one round of workgroup slots (2 per CU) as closely as
 // possible, and when several rounds are needed, with the widest tile:
+//   * first the one-workgroup-per-CU tiles taken when one round of them fills
+//     the CUs (gemm_tile_choice): 112x256 weights-direct (gemm_wd_kernel,
+//     packed QKV at M = 449..560), then 112x96 and 128x96 (O and down at
+//     M = 465..640);
 //   * past 64 rows (M > 64), 64x32 tiles (4 waves of 32x16, a 3-stage ring of
 //     four k-blocks, 2 workgroups per CU) when they fit in one round and
 //     number at least half the CUs: O and down at M = 65..128 13-16% faster
