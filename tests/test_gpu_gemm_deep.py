@@ -77,7 +77,7 @@ SHAPES = [
 
 @pytest.mark.parametrize("m,n,k,cfg", SHAPES)
 def test_deep_stage_int32_and_dequant(cuda, m, n, k, cfg):
-    from nanopointllm_amd import w8a8
+    from nanopointllm_amd import _lib, w8a8
 
     assert _config(m, n) == cfg
     xq, wq, sx, sw, bias = _case(m, n, k, seed=m + n + k)
@@ -93,6 +93,15 @@ def test_deep_stage_int32_and_dequant(cuda, m, n, k, cfg):
             want = torch.from_numpy(exp).to(dt).float().numpy()
             np.testing.assert_array_equal(y.float().cpu().numpy(), want,
                                           err_msg=f"{dt} bias={b is not None}")
+    # The GEMM kernel alone on packed activations (below 65 rows the router
+    # gives these shapes to the GEMV).
+    xp = w8a8.pack_rows(xd)
+    got = w8a8.linear_packed(xp, sxt, m, k, wp, swt, None, n, epilogue=_lib.EPI_I32,
+                             out_dtype=torch.int32)
+    np.testing.assert_array_equal(got.cpu().numpy(), eacc)
+    got = w8a8.linear_packed(xp, sxt, m, k, wp, swt, bt, n, out_dtype=torch.float16)
+    want = O.dequant_epilogue(eacc, sx, sw, bias).astype(np.float16)
+    np.testing.assert_array_equal(got.cpu().numpy(), want)
 
 
 @pytest.mark.parametrize("m,inter,k", [(760, 2048, 4197), (300, 3000, 4250), (100, 500, 4250),

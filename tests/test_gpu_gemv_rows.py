@@ -1,15 +1,21 @@
-"""The GEMV at 17..64 rows (csrc/gemv.hip): past 16 rows a workgroup owns
-three 16-output weight blocks and every activation fragment it loads serves
-all three, the regime of continuously batched decode steps
-(engine/scheduler.py:46-100) through the projections of
+"""The GEMV at 17..64 rows (csrc/gemv.hip), the regime of continuously
+batched decode steps (engine/scheduler.py:46-100) through the projections of
 paged_attention.py:97-124 and lightweight_runner.py:38-54, 329-379.
+
+Two kernels serve it: with K <= 4096 and the int32 / dequant / SiLU*mul
+epilogues the persistent gemv_rows_kernel (each wavefront keeps the x
+fragments of its k-range in registers; one workgroup per CU, several blocks
+each, or one block per CU at N = 4096, or fewer workgroups than CUs), and
+otherwise gemv_kernel (three blocks per workgroup past 512 blocks).
 
 Bars: int32 accumulators bit-exact against the oracle's integer product;
 dequant outputs bit-equal to the oracle's binary32 result rounded once; the
-SiLU*mul epilogue equal to the oracle's and its per-block row maxima giving
-the two-phase hq bit-exact; requant1 and the single-rounding bf16 dequant
-exact.  Block counts that leave a partial group of three (N = 12272 and
-12290: 767 and 769 blocks) and K that is not a multiple of 64 are included.
+SiLU*mul epilogue equal to the oracle's, its int8 twin equal to the oracle's
+quantization of h, and its per-block row maxima giving the two-phase hq
+bit-exact; requant1 and the single-rounding bf16 dequant exact.  Block counts
+that leave a partial group (N = 12272 and 12290), K off the 64 grid, row
+counts that leave a partial row tile (17, 33, 63) and fewer blocks than CUs
+are included.
 """
 from __future__ import annotations
 
@@ -40,27 +46,40 @@ def _case(m, n, k, seed):
     return xq, wq, sx, sw, bias
 
 
+def _rows_kernel(m: int, n: int, k: int) -> bool:
+    # gemv_rows_kernel's shapes (its int32 / dequant / SiLU*mul epilogues).
+    return 16 < m <= 64 and k <= 4096
+
+
 def _uses_gemv(m: int, n: int) -> bool:
     # The library's routing: the GEMV up to 32 rows, and up to 64 for N <= 12288.
     return m <= 32 or (m <= 64 and n <= 12288)
 
 
-SHAPES = [
-    # (m, n, k): LLaMA-7B QKV at every row count of the regime, a partial
-    # group of blocks (767 and 769 blocks), K off the 64 grid, and many blocks at 17 and 32 rows.
-    (17, 12288, 4096), (24, 12288, 4096), (32, 12288, 4096), (48, 12288, 4096),
-    (64, 12288, 4096), (40, 12272, 1000), (32, 12290, 1000), (20, 9000, 130), (32, 22016, 4096),
-    (64, 8200, 72),
+ROWS_SHAPES = [
+    # (m, n, k) on gemv_rows_kernel: LLaMA-7B QKV at every row count of the
+    # regime, a partial group of blocks (767 and 769 blocks), K off the 64
+    # grid, one block per CU (N = 4096), fewer blocks than CUs, and the
+    # widest N at 32 rows.
+    (17, 12288, 4096), (24, 12288, 4096), (32, 12288, 4096), (33, 12288, 4096),
+    (48, 12288, 4096), (64, 12288, 4096), (40, 12272, 1000), (32, 12290, 1000),
+    (20, 9000, 130), (64, 8200, 72), (32, 4096, 4096), (64, 4096, 4000), (17, 1000, 64),
+    (63, 300, 4096), (32, 22016, 4096),
+]
+OLD_SHAPES = [
+    # gemv_kernel: K > 4096, three blocks per workgroup (MT = 2 and 4) and
+    # one block per workgroup at 256 blocks.
+    (24, 12288, 4160), (48, 12272, 5000), (40, 4096, 11008),
 ]
 
 
-@pytest.mark.parametrize("m,n,k", SHAPES)
+@pytest.mark.parametrize("m,n,k", ROWS_SHAPES + OLD_SHAPES)
 def test_gemv_rows_int32_and_dequant(cuda, m, n, k):
     from nanopointllm_amd import w8a8
 
-    assert _uses_gemv(m, n) and -(-n // 16) > 512
+    assert _uses_gemv(m, n)
     xq, wq, sx, sw, bias = _case(m, n, k, seed=m + n + k)
-    note(f"gemv rows m={m} n={n} k={k}")
+    note(f"gemv rows m={m} n={n} k={k} rows_kernel={_rows_kernel(m, n, k)}")
     xd, wp = xq.to(cuda), w8a8.pack_rows(wq.to(cuda))
     eacc = O.int32_matmul_f64(xq.numpy(), wq.numpy())
     np.testing.assert_array_equal(w8a8.gemm_i32(xd, wp, n).cpu().numpy(), eacc)
@@ -78,24 +97,37 @@ def test_gemv_rows_int32_and_dequant(cuda, m, n, k):
 
 
 @pytest.mark.parametrize("m,inter,k", [(17, 11008, 4096), (24, 11008, 4096), (32, 11008, 4096),
-                                      (29, 4500, 700)])
+                                      (48, 6000, 4096), (64, 4000, 2000), (29, 4500, 700),
+                                      (33, 2000, 1000), (20, 11008, 4160)])
 def test_gemv_rows_silu_mul_and_two_phase(cuda, m, inter, k):
     from nanopointllm_amd import _lib, w8a8
 
     n = 2 * inter
-    assert _uses_gemv(m, n) and -(-n // 16) > 512
+    assert _uses_gemv(m, n)
     xq, wq, sx, sw, _ = _case(m, n, k, seed=11 + k + m)
-    note(f"gemv rows silu m={m} inter={inter} k={k}")
+    note(f"gemv rows silu m={m} inter={inter} k={k} rows_kernel={_rows_kernel(m, n, k)}")
     wp = w8a8.pack_rows(wq.to(cuda), _lib.ROWS_INTERLEAVE_HALVES)
     sp = O.pack_gateup_rows(sw[:inter, None], sw[inter:, None], "interleave")[:, 0]
     qp = O.pack_gateup_rows(wq.numpy()[:inter], wq.numpy()[inter:], "interleave")
     xd, sxt = xq.to(cuda), torch.from_numpy(sx).to(cuda)
     spt = torch.from_numpy(np.ascontiguousarray(sp)).to(cuda)
+    acc = O.int32_matmul_f64(xq.numpy(), qp)
+    eh = O.gateup_silu_mul_from_acc(acc, sx, sp, layout="interleave")
+    # bfloat16 chain: g and u rounded to bfloat16, then the reference's act_fn
+    # (torch's CPU F.silu) and the product on bfloat16 tensors.
+    yb = torch.from_numpy(O.dequant_epilogue(acc, sx, sp)).to(torch.bfloat16)
+    ebh = (torch.nn.functional.silu(yb[:, 0::2]) * yb[:, 1::2]).float().numpy()
+    hb = w8a8.linear_i8in(xd, sxt, wp, spt, None, n, epilogue=_lib.EPI_SILU_MUL,
+                          out_dtype=torch.bfloat16)
+    np.testing.assert_array_equal(hb.float().cpu().numpy(), ebh)
     h = w8a8.linear_i8in(xd, sxt, wp, spt, None, n, epilogue=_lib.EPI_SILU_MUL,
                          out_dtype=torch.float16)
-    eh = O.gateup_silu_mul_from_acc(O.int32_matmul_f64(xq.numpy(), qp), sx, sp,
-                                    layout="interleave")
     np.testing.assert_array_equal(h.cpu().numpy(), eh.astype(np.float16))
+    h_scale = float(O.static_activation_scale(float(h.float().abs().max().item())))
+    hq = w8a8.linear_i8in(xd, sxt, wp, spt, None, n, epilogue=_lib.EPI_SILU_MUL_Q8,
+                          out_dtype=torch.int8, y_scale=h_scale)
+    eq = O.quantize_symmetric(h.cpu().numpy().astype(np.float32), np.float32(h_scale))
+    np.testing.assert_array_equal(hq.cpu().numpy(), eq)
     out = w8a8.gateup_silu_mul_two_phase(xd, wp, spt, None, n, x_scale=sxt, in_features=k)
     np.testing.assert_array_equal(out.h.cpu().numpy(), h.cpu().numpy())
     tq, ts = O.dynamic_per_token_quant(h.cpu().numpy().astype(np.float32))
@@ -103,11 +135,13 @@ def test_gemv_rows_silu_mul_and_two_phase(cuda, m, inter, k):
     np.testing.assert_array_equal(out.scale.cpu().numpy(), ts[:, 0])
 
 
-def test_gemv_rows_integer_epilogues(cuda):
+@pytest.mark.parametrize("m,n,k", [(24, 12290, 1000), (48, 12288, 4096)])
+def test_gemv_rows_integer_epilogues(cuda, m, n, k):
+    """requant1 and the single-rounding bf16 dequant stay on gemv_kernel at
+    every K (gemv_rows_kernel does not take them)."""
     from nanopointllm_amd import _lib, integer_epilogues as E, w8a8
 
-    m, n, k = 24, 12290, 1000
-    xq, wq, sx, sw, _ = _case(m, n, k, seed=3)
+    xq, wq, sx, sw, _ = _case(m, n, k, seed=3 + m)
     comp = [O.compile_fp16_requant_scale(0.02, float(w), 0.5) for w in sw]
     mult = np.array([c[0] for c in comp], np.uint32)
     shift = np.array([c[1] for c in comp], np.int32)
@@ -130,3 +164,22 @@ def test_gemv_rows_integer_epilogues(cuda):
         want = O.dequantize_int32_to_bf16(int(acc[i, j]), int(sa_bits[i]), int(sw_bits[j]))
         got = int(yb[i, j].view(torch.int16).item()) & 0xFFFF
         assert got == want, (i, j)
+
+
+def test_gemv_rows_strided_and_padded_rows(cuda):
+    """Caller int8 rows with a leading dimension past K (read in place when
+    K % 64 == 0, else padded into the workspace) give the bits of contiguous
+    rows."""
+    from nanopointllm_amd import w8a8
+
+    for m, n, k, ld in [(40, 12288, 4096, 4160), (33, 5000, 1000, 1040)]:
+        xq, wq, sx, sw, bias = _case(m, n, k, seed=7 + m)
+        note(f"gemv rows strided m={m} n={n} k={k} ld={ld}")
+        big = torch.zeros((m, ld), dtype=torch.int8)
+        big[:, :k] = xq
+        xd = big.to(cuda)[:, :k]
+        wp = w8a8.pack_rows(wq.to(cuda))
+        sxt, swt, bt = (torch.from_numpy(a).to(cuda) for a in (sx, sw, bias))
+        y = w8a8.linear_i8in(xd, sxt, wp, swt, bt, n, out_dtype=torch.float16)
+        exp = O.dequant_epilogue(O.int32_matmul_f64(xq.numpy(), wq.numpy()), sx, sw, bias)
+        np.testing.assert_array_equal(y.cpu().numpy(), exp.astype(np.float16))
