@@ -626,12 +626,16 @@ def runner_decode_step(m: int, device, steps: int = 20, warmup: int = 5) -> dict
     ops_pf = W.LAYERS * sum(W.algorithmic_ops(pm, p.n, p.k) for p in W.PROJECTIONS)
     ops_pf += 2 * pm * W.VOCAB * W.HIDDEN
     # Calibrate: each layer's max |h| (the down projection's input) over one
-    # eager step, then every MLP switches to the static int8 chain.
+    # eager step, then every MLP switches to the static int8 chain.  The step
+    # runs layer by layer on the route whose down projection is a module call
+    # (the same h as the decode route).
     h_max: dict[int, torch.Tensor] = {}
     hooks = [layer.mlp.down.register_forward_hook(
         lambda mod, args, out, i=i: h_max.__setitem__(i, args[0].detach().abs().max()))
         for i, layer in enumerate(runner.layers)]
-    runner(ids)
+    hidden, residual = runner.embed_tokens(ids), None
+    for layer in runner.layers:
+        hidden, residual = layer.forward_carry(hidden, residual)
     for h in hooks:
         h.remove()
     for i, layer in enumerate(runner.layers):

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 5
+#define W8A8_ABI_VERSION 6
 
 typedef enum w8a8_dtype {
   W8A8_F32 = 0,
@@ -243,6 +243,54 @@ int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* res
                         int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,
                         int64_t n, int64_t k, float* x_scale_out, void* x_out, int64_t ld_x_out,
                         void* workspace, int64_t workspace_bytes, hipStream_t stream);
+
+/*
+ * The residual add of a decoder layer folded into the dequant linear, with
+ * the RMSNorm sums of squares its next norm needs: the reference's
+ * `residual = hidden + attn_out` and `hidden + mlp_out` in the activation
+ * dtype (lightweight_runner.py:247-257, 552; residual_norm), after the
+ * o_proj / down_proj F.linear of lightweight_runner.py:329-383.
+ *   y = dtype(dtype(x W^T dequant (+ bias)) + residual): each product
+ *   rounded to y's dtype, then the sum rounded once (as torch does on two
+ *   16-bit tensors); y_dtype F16/BF16, residual [m, ld_residual] of y's
+ *   dtype; ss_parts (nullable) [m, ld_parts >= ceil(n/8)] binary32 receives,
+ *   per row and 8-column chunk c, fl(...fl(y[8c]^2) + ... + y[8c+7]^2) in
+ *   column order (columns past n count 0): the partial sums of
+ *   w8a8_rmsnorm_linear_ss.
+ * x, workspace and errors as w8a8_linear (epilogue DEQUANT).  y, residual
+ * and ss_parts must not overlap (W8A8_ERR_OVERLAP).  The decode routes add
+ * in their epilogue; the GEMM route runs one elementwise pass after it.
+ */
+int w8a8_linear_residual(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
+                         const float* w_scale, const float* bias, void* y, int y_dtype,
+                         int64_t ldy, const void* residual, int64_t ld_residual, float* ss_parts,
+                         int64_t ld_parts, int64_t m, int64_t n, int64_t k, void* workspace,
+                         int64_t workspace_bytes, hipStream_t stream);
+
+/* w8a8_linear_residual on int8 activations with per-row scales (as
+ * w8a8_linear_i8in). */
+int w8a8_linear_i8in_residual(const int8_t* xq, int64_t ldq, const float* x_scale,
+                              const int8_t* w_packed, const float* w_scale, const float* bias,
+                              void* y, int y_dtype, int64_t ldy, const void* residual,
+                              int64_t ld_residual, float* ss_parts, int64_t ld_parts, int64_t m,
+                              int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                              hipStream_t stream);
+
+/*
+ * w8a8_rmsnorm_linear without a residual, on rows x that a residual-add
+ * linear wrote together with their sums of squares ss_parts (nullable,
+ * [m, ld_parts >= ceil(k/8)]): the one-kernel decode route reads those sums
+ * instead of summing x in every workgroup, which removes the barrier in front
+ * of its weight stream; the other routes sum x themselves.  Every route
+ * gives the bits of w8a8_rmsnorm_linear on x (the sums are taken in the norm
+ * kernels' order), provided ss_parts are the sums of these very rows.
+ */
+int w8a8_rmsnorm_linear_ss(const void* x, int x_dtype, int64_t ldx, const float* ss_parts,
+                           int64_t ld_parts, const void* norm_weight, float eps,
+                           const int8_t* w_packed, const float* w_scale, const float* bias,
+                           int epilogue, void* y, int y_dtype, int64_t ldy, float y_scale,
+                           int inter_dtype, int64_t m, int64_t n, int64_t k, float* x_scale_out,
+                           void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /*
  * As w8a8_linear for already-quantized activations xq (int8 [m, ldq]) with

@@ -178,9 +178,65 @@ inline bool use_gemv(int64_t m, int64_t n) {
 }
 
 // Runs the int8 product for activations already staged in `act` (row-major
-// [m, round_up(k,64)] for the GEMV, packed tiles for the GEMM).
+// [m, round_up(k,64)] for the GEMV, packed tiles for the GEMM).  The GEMV
+// kernels take the residual-add epilogue (op.res) themselves; the GEMM
+// writes its output first and the add runs over it.
 inline hipError_t run_product(const LinearOperands& op, hipStream_t st) {
-  return use_gemv(op.M, op.N) ? launch_gemv(op, st) : launch_gemm(op, st);
+  if (use_gemv(op.M, op.N)) return launch_gemv(op, st);
+  if (op.res == nullptr) return launch_gemm(op, st);
+  LinearOperands plain = op;
+  plain.res = nullptr;
+  plain.ss_parts = nullptr;
+  const hipError_t e = launch_gemm(plain, st);
+  if (e != hipSuccess) return e;
+  return launch_add_rows_ss(op.y, op.y_dtype, op.ldy, op.res, op.ld_res, op.ss_parts,
+                            op.ld_parts, op.M, op.N, st);
+}
+
+// The residual add of a decoder layer folded into a linear's epilogue
+// (w8a8_linear_residual and friends): y = dtype(dtype(x W^T) + res), and
+// with parts (nullable) the RMSNorm sums of squares of y per 8 columns.
+struct ResidualAdd {
+  const void* res;
+  int64_t ld_res;
+  float* parts;
+  int64_t ld_parts;
+};
+
+// Whether the byte ranges of [rows, ka] at a (lda, ea-byte elements) and
+// [rows, kb] at b (ldb, eb) share a byte; null pointers overlap nothing.
+inline bool overlap2(const void* a, int64_t lda, int64_t ea, int64_t ka, const void* b,
+                     int64_t ldb, int64_t eb, int64_t kb, int64_t rows) {
+  if (a == nullptr || b == nullptr || rows <= 0 || ka <= 0 || kb <= 0) return false;
+  using u128 = unsigned __int128;
+  const u128 a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+  const u128 a1 = a0 + (static_cast<u128>(rows - 1) * static_cast<u128>(lda) + ka) * ea;
+  const u128 b1 = b0 + (static_cast<u128>(rows - 1) * static_cast<u128>(ldb) + kb) * eb;
+  return a0 < b1 && b0 < a1;
+}
+
+// Checks of the residual-add operands for an [m, n] 16-bit output y.
+inline int check_residual(const ResidualAdd& ra, const void* y, int y_dtype, int64_t ldy,
+                          int64_t m, int64_t n) {
+  if (!half_dtype(y_dtype)) return W8A8_ERR_DTYPE;
+  if (m == 0 || n == 0) return W8A8_OK;
+  if (ra.res == nullptr) return W8A8_ERR_NULL;
+  const int64_t chunks = ceil_div(n, 8);
+  if (ra.ld_res < n || (ra.parts != nullptr && ra.ld_parts < chunks)) return W8A8_ERR_SHAPE;
+  if (!aligned(ra.res, 2) || !aligned(ra.parts, 4)) return W8A8_ERR_ALIGN;
+  if (overlap2(y, ldy, 2, n, ra.res, ra.ld_res, 2, n, m) ||
+      overlap2(ra.parts, ra.ld_parts, 4, chunks, y, ldy, 2, n, m) ||
+      overlap2(ra.parts, ra.ld_parts, 4, chunks, ra.res, ra.ld_res, 2, n, m))
+    return W8A8_ERR_OVERLAP;
+  return W8A8_OK;
+}
+
+inline void set_residual(LinearOperands& op, const ResidualAdd* ra) {
+  if (ra == nullptr) return;
+  op.res = ra->res;
+  op.ld_res = ra->ld_res;
+  op.ss_parts = ra->parts;
+  op.ld_parts = ra->ld_parts;
 }
 
 // Stages caller int8 activations for run_product: the GEMV reads them in
@@ -211,7 +267,7 @@ int linear_impl(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
                 const float* w_scale, const float* bias, int epilogue, void* y, int y_dtype,
                 int64_t ldy, float y_scale, int inter_dtype, int64_t m, int64_t n, int64_t k,
                 float* x_scale_out, void* workspace, int64_t workspace_bytes,
-                float* absmax_parts, hipStream_t stream) {
+                float* absmax_parts, hipStream_t stream, const ResidualAdd* ra = nullptr) {
   if (!float_dtype(x_dtype)) return W8A8_ERR_DTYPE;
   // The integer requant needs int8 activations with a static scale
   // (w8a8_linear_i8in_requant); the single-rounding bf16 dequant has no bias.
@@ -229,6 +285,7 @@ int linear_impl(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
     LinearOperands op = make_ops(nullptr, 0, nullptr, w_packed, w_scale, bias, epilogue, y,
                                  y_dtype, ldy, y_scale, inter_dtype, m, n, k);
     op.absmax_parts = absmax_parts;
+    set_residual(op, ra);
     return status_of(launch_gemv_fused(x, x_dtype, ldx, op, x_scale_out, stream));
   }
   if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
@@ -244,6 +301,7 @@ int linear_impl(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
   LinearOperands op = make_ops(act, kp, sx, w_packed, w_scale, bias, epilogue, y, y_dtype, ldy,
                                y_scale, inter_dtype, m, n, k);
   op.absmax_parts = absmax_parts;
+  set_residual(op, ra);
   return status_of(run_product(op, stream));
 }
 
@@ -252,7 +310,8 @@ int linear_i8in_impl(const int8_t* xq, int64_t ldq, const float* x_scale,
                      const int8_t* w_packed, const float* w_scale, const float* bias,
                      int epilogue, void* y, int y_dtype, int64_t ldy, float y_scale,
                      int inter_dtype, int64_t m, int64_t n, int64_t k, void* workspace,
-                     int64_t workspace_bytes, float* absmax_parts, hipStream_t stream) {
+                     int64_t workspace_bytes, float* absmax_parts, hipStream_t stream,
+                     const ResidualAdd* ra = nullptr) {
   if (epilogue == W8A8_EPI_REQUANT) return W8A8_ERR_DTYPE;  // w8a8_linear_i8in_requant
   if (epilogue == W8A8_EPI_DEQUANT_BF16_EXACT && bias != nullptr) return W8A8_ERR_DTYPE;
   int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
@@ -271,7 +330,89 @@ int linear_i8in_impl(const int8_t* xq, int64_t ldq, const float* x_scale,
   LinearOperands op = make_ops(a, lda, x_scale, w_packed, w_scale, bias, epilogue, y, y_dtype,
                                ldy, y_scale, inter_dtype, m, n, k);
   op.absmax_parts = absmax_parts;
+  set_residual(op, ra);
   return status_of(run_product(op, stream));
+}
+
+// w8a8_rmsnorm_linear; ss_in (nullable, only without a residual): the
+// RMSNorm sums of squares of x per 8 columns as a residual-add epilogue wrote
+// them, which the one-kernel route reads instead of summing x itself (the
+// same bits: the epilogue sums in the norm kernels' order); the other routes
+// sum x in the activation prologue.
+int rmsnorm_linear_impl(const void* x, int x_dtype, int64_t ldx, const void* residual,
+                        int64_t ld_residual, void* residual_out, int64_t ld_residual_out,
+                        const void* norm_weight, float eps, const int8_t* w_packed,
+                        const float* w_scale, const float* bias, int epilogue, void* y,
+                        int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,
+                        int64_t n, int64_t k, float* x_scale_out, void* x_out, int64_t ld_x_out,
+                        void* workspace, int64_t workspace_bytes, hipStream_t stream,
+                        const float* ss_in, int64_t ld_ss_in) {
+  if (!half_dtype(x_dtype)) return W8A8_ERR_DTYPE;
+  if (epilogue == W8A8_EPI_REQUANT) return W8A8_ERR_DTYPE;
+  if (epilogue == W8A8_EPI_DEQUANT_BF16_EXACT && bias != nullptr) return W8A8_ERR_DTYPE;
+  int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
+                        n, k);
+  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
+  if (k > prologue_max_k()) return W8A8_ERR_SHAPE;
+  if (x == nullptr || norm_weight == nullptr) return W8A8_ERR_NULL;
+  if (residual != nullptr && residual_out == nullptr) return W8A8_ERR_NULL;
+  if (ldx < k || (residual != nullptr && (ld_residual < k || ld_residual_out < k)) ||
+      (x_out != nullptr && ld_x_out < k))
+    return W8A8_ERR_SHAPE;
+  if (!(eps >= 0.0f)) return W8A8_ERR_SHAPE;
+  const uintptr_t xs = static_cast<uintptr_t>(elem_size(x_dtype));
+  if (!aligned(x, xs) || !aligned(residual, xs) || !aligned(residual_out, xs) ||
+      !aligned(norm_weight, xs) || !aligned(x_out, xs) || !aligned(x_scale_out, 4))
+    return W8A8_ERR_ALIGN;
+  LinearOperands op = make_ops(nullptr, 0, nullptr, w_packed, w_scale, bias, epilogue, y, y_dtype,
+                               ldy, y_scale, inter_dtype, m, n, k);
+  // residual_out and x_out are written row by row after the row is read
+  // (the prologue), so each may be the very rows of an input; no other
+  // overlap is allowed.  The one-kernel route has workgroup 0 write them
+  // while the others still read x and the residual, so it is taken only
+  // when they overlap neither input.
+  const int64_t es = elem_size(x_dtype);
+  const void* r_out = residual != nullptr ? residual_out : nullptr;  // written only with a residual
+  if (!rows_alias_ok(r_out, ld_residual_out, es, x, ldx, es, m, k) ||
+      !rows_alias_ok(r_out, ld_residual_out, es, residual, ld_residual, es, m, k) ||
+      !rows_alias_ok(x_out, ld_x_out, es, x, ldx, es, m, k) ||
+      !rows_alias_ok(x_out, ld_x_out, es, residual, ld_residual, es, m, k) ||
+      overlap(r_out, ld_residual_out, es, x_out, ld_x_out, es, m, k))
+    return W8A8_ERR_OVERLAP;
+  const bool in_place = overlap(r_out, ld_residual_out, es, x, ldx, es, m, k) ||
+                        overlap(r_out, ld_residual_out, es, residual, ld_residual, es, m, k) ||
+                        overlap(x_out, ld_x_out, es, x, ldx, es, m, k) ||
+                        overlap(x_out, ld_x_out, es, residual, ld_residual, es, m, k);
+  const bool fused_epilogue = epilogue <= W8A8_EPI_SILU_MUL || epilogue == W8A8_EPI_SILU_MUL_Q8;
+  if (k > 0 && fused_epilogue && !in_place &&
+      fused_norm_supported(x, x_dtype, ldx, residual, ld_residual, residual_out,
+                           ld_residual_out, norm_weight, x_out, ld_x_out, m, n, k)) {
+    // One kernel: residual add, RMSNorm, per-token quantization, GEMV, epilogue.
+    return status_of(launch_gemv_fused_norm(x, x_dtype, ldx, residual, ld_residual, residual_out,
+                                            ld_residual_out, norm_weight, eps, x_out, ld_x_out,
+                                            op, x_scale_out, stream,
+                                            residual == nullptr ? ss_in : nullptr, ld_ss_in));
+  }
+  // Otherwise the activation prologue writes the int8 rows the product
+  // reads: row-major for the GEMV, the packed tiles for the GEMM.
+  if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
+    return W8A8_ERR_WORKSPACE;
+  if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
+  float* sx = x_scale_out != nullptr ? x_scale_out : static_cast<float*>(workspace);
+  int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
+  const int64_t kp = round_up(k, kTileK);
+  const bool gemv = use_gemv(m, n);
+  // The GEMV reads whole 64-column blocks: the prologue writes zeros in the
+  // pad columns K..kp of its row-major rows.
+  hipError_t e = launch_prologue_quant(x, x_dtype, ldx, residual, ld_residual, residual_out,
+                                       ld_residual_out, norm_weight, x_dtype, eps, nullptr,
+                                       nullptr, m, k, act, kp, sx, x_out, ld_x_out, stream, !gemv,
+                                       kp);
+  if (e != hipSuccess) return status_of(e);
+  op.a = act;
+  op.lda = kp;
+  op.sx = sx;
+  return status_of(gemv ? launch_gemv(op, stream) : launch_gemm(op, stream));
 }
 
 // Looks up (once per device) the current device's address of `scratch`.
@@ -468,71 +609,55 @@ int w8a8_rmsnorm_linear(const void* x, int x_dtype, int64_t ldx, const void* res
                         int y_dtype, int64_t ldy, float y_scale, int inter_dtype, int64_t m,
                         int64_t n, int64_t k, float* x_scale_out, void* x_out, int64_t ld_x_out,
                         void* workspace, int64_t workspace_bytes, hipStream_t stream) {
-  if (!half_dtype(x_dtype)) return W8A8_ERR_DTYPE;
-  if (epilogue == W8A8_EPI_REQUANT) return W8A8_ERR_DTYPE;
-  if (epilogue == W8A8_EPI_DEQUANT_BF16_EXACT && bias != nullptr) return W8A8_ERR_DTYPE;
-  int rc = check_linear(w_packed, w_scale, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m,
-                        n, k);
-  if (rc != W8A8_OK || m == 0 || n == 0) return rc;
-  if (k > prologue_max_k()) return W8A8_ERR_SHAPE;
-  if (x == nullptr || norm_weight == nullptr) return W8A8_ERR_NULL;
-  if (residual != nullptr && residual_out == nullptr) return W8A8_ERR_NULL;
-  if (ldx < k || (residual != nullptr && (ld_residual < k || ld_residual_out < k)) ||
-      (x_out != nullptr && ld_x_out < k))
-    return W8A8_ERR_SHAPE;
-  if (!(eps >= 0.0f)) return W8A8_ERR_SHAPE;
-  const uintptr_t xs = static_cast<uintptr_t>(elem_size(x_dtype));
-  if (!aligned(x, xs) || !aligned(residual, xs) || !aligned(residual_out, xs) ||
-      !aligned(norm_weight, xs) || !aligned(x_out, xs) || !aligned(x_scale_out, 4))
-    return W8A8_ERR_ALIGN;
-  LinearOperands op = make_ops(nullptr, 0, nullptr, w_packed, w_scale, bias, epilogue, y, y_dtype,
-                               ldy, y_scale, inter_dtype, m, n, k);
-  // residual_out and x_out are written row by row after the row is read
-  // (the prologue), so each may be the very rows of an input; no other
-  // overlap is allowed.  The one-kernel route has workgroup 0 write them
-  // while the others still read x and the residual, so it is taken only
-  // when they overlap neither input.
-  const int64_t es = elem_size(x_dtype);
-  const void* r_out = residual != nullptr ? residual_out : nullptr;  // written only with a residual
-  if (!rows_alias_ok(r_out, ld_residual_out, es, x, ldx, es, m, k) ||
-      !rows_alias_ok(r_out, ld_residual_out, es, residual, ld_residual, es, m, k) ||
-      !rows_alias_ok(x_out, ld_x_out, es, x, ldx, es, m, k) ||
-      !rows_alias_ok(x_out, ld_x_out, es, residual, ld_residual, es, m, k) ||
-      overlap(r_out, ld_residual_out, es, x_out, ld_x_out, es, m, k))
-    return W8A8_ERR_OVERLAP;
-  const bool in_place = overlap(r_out, ld_residual_out, es, x, ldx, es, m, k) ||
-                        overlap(r_out, ld_residual_out, es, residual, ld_residual, es, m, k) ||
-                        overlap(x_out, ld_x_out, es, x, ldx, es, m, k) ||
-                        overlap(x_out, ld_x_out, es, residual, ld_residual, es, m, k);
-  const bool fused_epilogue = epilogue <= W8A8_EPI_SILU_MUL || epilogue == W8A8_EPI_SILU_MUL_Q8;
-  if (k > 0 && fused_epilogue && !in_place &&
-      fused_norm_supported(x, x_dtype, ldx, residual, ld_residual, residual_out,
-                           ld_residual_out, norm_weight, x_out, ld_x_out, m, n, k)) {
-    // One kernel: residual add, RMSNorm, per-token quantization, GEMV, epilogue.
-    return status_of(launch_gemv_fused_norm(x, x_dtype, ldx, residual, ld_residual, residual_out,
-                                            ld_residual_out, norm_weight, eps, x_out, ld_x_out,
-                                            op, x_scale_out, stream));
+  return rmsnorm_linear_impl(x, x_dtype, ldx, residual, ld_residual, residual_out,
+                             ld_residual_out, norm_weight, eps, w_packed, w_scale, bias, epilogue,
+                             y, y_dtype, ldy, y_scale, inter_dtype, m, n, k, x_scale_out, x_out,
+                             ld_x_out, workspace, workspace_bytes, stream, nullptr, 0);
+}
+
+int w8a8_rmsnorm_linear_ss(const void* x, int x_dtype, int64_t ldx, const float* ss_parts,
+                           int64_t ld_parts, const void* norm_weight, float eps,
+                           const int8_t* w_packed, const float* w_scale, const float* bias,
+                           int epilogue, void* y, int y_dtype, int64_t ldy, float y_scale,
+                           int inter_dtype, int64_t m, int64_t n, int64_t k, float* x_scale_out,
+                           void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  if (m > 0 && n > 0 && k > 0 && ss_parts != nullptr) {
+    if (ld_parts < ceil_div(k, 8)) return W8A8_ERR_SHAPE;
+    if (!aligned(ss_parts, 4)) return W8A8_ERR_ALIGN;
   }
-  // Otherwise the activation prologue writes the int8 rows the product
-  // reads: row-major for the GEMV, the packed tiles for the GEMM.
-  if (workspace == nullptr || workspace_bytes < w8a8_workspace_bytes(m, k))
-    return W8A8_ERR_WORKSPACE;
-  if (!aligned(workspace, 16)) return W8A8_ERR_ALIGN;
-  float* sx = x_scale_out != nullptr ? x_scale_out : static_cast<float*>(workspace);
-  int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
-  const int64_t kp = round_up(k, kTileK);
-  const bool gemv = use_gemv(m, n);
-  // The GEMV reads whole 64-column blocks: the prologue writes zeros in the
-  // pad columns K..kp of its row-major rows.
-  hipError_t e = launch_prologue_quant(x, x_dtype, ldx, residual, ld_residual, residual_out,
-                                       ld_residual_out, norm_weight, x_dtype, eps, nullptr,
-                                       nullptr, m, k, act, kp, sx, x_out, ld_x_out, stream, !gemv,
-                                       kp);
-  if (e != hipSuccess) return status_of(e);
-  op.a = act;
-  op.lda = kp;
-  op.sx = sx;
-  return status_of(gemv ? launch_gemv(op, stream) : launch_gemm(op, stream));
+  return rmsnorm_linear_impl(x, x_dtype, ldx, nullptr, 0, nullptr, 0, norm_weight, eps, w_packed,
+                             w_scale, bias, epilogue, y, y_dtype, ldy, y_scale, inter_dtype, m, n,
+                             k, x_scale_out, nullptr, 0, workspace, workspace_bytes, stream,
+                             ss_parts, ld_parts);
+}
+
+int w8a8_linear_residual(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
+                         const float* w_scale, const float* bias, void* y, int y_dtype,
+                         int64_t ldy, const void* residual, int64_t ld_residual, float* ss_parts,
+                         int64_t ld_parts, int64_t m, int64_t n, int64_t k, void* workspace,
+                         int64_t workspace_bytes, hipStream_t stream) {
+  const ResidualAdd ra{residual, ld_residual, ss_parts, ld_parts};
+  if (m < 0 || n < 0) return W8A8_ERR_SHAPE;
+  const int rc = check_residual(ra, y, y_dtype, ldy, m, n);
+  if (rc != W8A8_OK) return rc;
+  return linear_impl(x, x_dtype, ldx, w_packed, w_scale, bias, W8A8_EPI_DEQUANT, y, y_dtype, ldy,
+                     0.0f, y_dtype, m, n, k, nullptr, workspace, workspace_bytes, nullptr, stream,
+                     &ra);
+}
+
+int w8a8_linear_i8in_residual(const int8_t* xq, int64_t ldq, const float* x_scale,
+                              const int8_t* w_packed, const float* w_scale, const float* bias,
+                              void* y, int y_dtype, int64_t ldy, const void* residual,
+                              int64_t ld_residual, float* ss_parts, int64_t ld_parts, int64_t m,
+                              int64_t n, int64_t k, void* workspace, int64_t workspace_bytes,
+                              hipStream_t stream) {
+  const ResidualAdd ra{residual, ld_residual, ss_parts, ld_parts};
+  if (m < 0 || n < 0) return W8A8_ERR_SHAPE;
+  const int rc = check_residual(ra, y, y_dtype, ldy, m, n);
+  if (rc != W8A8_OK) return rc;
+  return linear_i8in_impl(xq, ldq, x_scale, w_packed, w_scale, bias, W8A8_EPI_DEQUANT, y, y_dtype,
+                          ldy, 0.0f, y_dtype, m, n, k, workspace, workspace_bytes, nullptr, stream,
+                          &ra);
 }
 
 int w8a8_linear_packed(const int8_t* xq_packed, const float* x_scale, const int8_t* w_packed,

@@ -40,6 +40,12 @@ struct GemvParams {
   const int32_t* rq_shift;
   const int32_t* rq_bias;
   float* absmax_parts;  // kEpiSilu: [M][NB] per-block row |h|max (nullable)
+  // kEpiDequant (gemv_kernel only, nullable): the residual-add epilogue and
+  // its RMSNorm chunk sums (LinearOperands::res / ss_parts).
+  const void* res;
+  int64_t ld_res;
+  float* ss_parts;
+  int64_t ld_parts;
   int M;
   int N;
   int KB;
@@ -89,6 +95,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
   for (int j = 0; j < NBW; ++j)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[j][mt] = i32x4{0, 0, 0, 0};
+
+  // Residual-add epilogue: the residual of this thread's first output is
+  // requested before the weights, so the epilogue does not wait a memory
+  // round trip for it (later outputs, when a thread has several, load then).
+  [[maybe_unused]] TY res_first{};
+  if constexpr (EPI == kEpiDequant) {
+    if (p.res != nullptr && tid < NBW * TB) {
+      const int m = ((tid % TB) >> 8) * 16 + ((tid & 255) >> 4);
+      const int64_t nb = nb0 + tid / TB;
+      const int64_t n = nb * 16 + (tid & 15);
+      if (m < p.M && nb < p.NB && n < p.N) res_first = static_cast<const TY*>(p.res)[m * p.ld_res + n];
+    }
+  }
 
   i32x4 wb0[NBW][CH], wb1[NBW][CH];
   i32x4 ab0[MT][CH], ab1[MT][CH];
@@ -154,6 +173,28 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
       const int m = ((e % TB) >> 8) * 16 + ((e & 255) >> 4);
       const int64_t nb = nb0 + e / TB;
       const int64_t n = nb * 16 + (e & 15);
+      if constexpr (EPI == kEpiDequant) {
+        if (p.res != nullptr) {
+          // Residual-add epilogue: the chunk sums need every lane, so no lane
+          // leaves before them (NBW * TB and NT are multiples of 64).
+          const bool ok = m < p.M && nb < p.NB && n < p.N;
+          float v = 0.0f;
+          if (ok) {
+            int32_t s = 0;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) s += red[w][e];
+            const TY r = e == tid ? res_first : static_cast<const TY*>(p.res)[m * p.ld_res + n];
+            const TY o = add_rounded(from_f32<TY>(dequant1(s, p.sx[m], p.sw[n], p.bias, n)), r);
+            static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] = o;
+            v = to_f32(o);
+          }
+          if (p.ss_parts != nullptr) {
+            const float cs = chunk_sumsq8(v);
+            if ((e & 7) == 0 && ok) p.ss_parts[m * p.ld_parts + (n >> 3)] = cs;
+          }
+          continue;
+        }
+      }
       if (m >= p.M || nb >= p.NB || n >= p.N) continue;
       int32_t s = 0;
 #pragma unroll
@@ -548,6 +589,10 @@ hipError_t launch_gemv(const LinearOperands& op, hipStream_t st) {
   p.rq_shift = op.rq_shift;
   p.rq_bias = op.rq_bias;
   p.absmax_parts = op.absmax_parts;
+  p.res = op.res;
+  p.ld_res = op.ld_res;
+  p.ss_parts = op.ss_parts;
+  p.ld_parts = op.ld_parts;
   p.M = static_cast<int>(op.M);
   p.N = static_cast<int>(op.N);
   p.KB = static_cast<int>(ceil_div(op.K, kTileK));
@@ -556,7 +601,7 @@ hipError_t launch_gemv(const LinearOperands& op, hipStream_t st) {
   p.G = static_cast<int>(nblocks < cu_count() ? nblocks : cu_count());
   if (op.M <= 0 || nblocks == 0) return hipSuccess;
   if (fused_gemv_i8_supported(op.M, op.N, op.K, op.lda, op.epi)) return launch_gemv_fused_i8(op, st);
-  if (gemv_rows_supported(op.M, op.N, op.K, op.lda, op.epi)) {
+  if (op.res == nullptr && gemv_rows_supported(op.M, op.N, op.K, op.lda, op.epi)) {
     switch (op.epi) {
       case kEpiI32:
         return launch_rows_m<kEpiI32, int32_t, float>(p, st);

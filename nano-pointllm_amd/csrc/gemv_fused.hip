@@ -81,6 +81,18 @@ struct FusedParams {
   void* x_out;
   int64_t ld_xout;
   float* absmax_parts;  // kEpiSilu: [M][NB] per-block row |h|max (nullable)
+  // kEpiDequant (nullable): the residual-add epilogue and its RMSNorm chunk
+  // sums (LinearOperands::res / ss_parts).
+  const void* add_res;
+  int64_t ld_add_res;
+  float* ss_out;
+  int64_t ld_ss_out;
+  // NORM kernels (nullable): the RMSNorm sums of squares of x per 8-column
+  // chunk, as the residual-add epilogue of the launch that produced x wrote
+  // them; x is then taken as the summed rows (no residual) and the sums
+  // replace the workgroup's own.
+  const float* ss_in;
+  int64_t ld_ss_in;
   float out_scale;
   int M;
   int N;
@@ -128,9 +140,39 @@ typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 // `ops` holds the block's 16 weight scales followed by its 16 biases.
 template <int EPI, typename TY, typename TH>
 __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
-                                const float* row_s, int64_t nb, int tid, const float* ops) {
+                                const float* row_s, int64_t nb, int tid, const float* ops,
+                                const TY* res_pre = nullptr) {
   const bool has_bias = p.bias != nullptr;
   const int M = p.M;
+  if constexpr (EPI == kEpiDequant) {
+    if (p.add_res != nullptr) {
+      // Residual-add epilogue; threads below 256 fill whole wavefronts, so
+      // the chunk sums run in uniform control flow.
+      if (tid < 256) {
+        const int m = tid >> 4;
+        const int64_t n = nb * 16 + (tid & 15);
+        const bool ok = m < M && n < p.N;
+        float v = 0.0f;
+        if (ok) {
+          int32_t s = 0;
+#pragma unroll
+          for (int w = 0; w < kFusedWaves; ++w) s += red[w][tid];
+          const int r = tid & 15;
+          const TY rv = res_pre != nullptr ? *res_pre
+                                           : static_cast<const TY*>(p.add_res)[m * p.ld_add_res + n];
+          const TY o = add_rounded(from_f32<TY>(dequant1b(s, row_s[m], ops[r], has_bias, ops[16 + r])),
+                                   rv);
+          static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] = o;
+          v = to_f32(o);
+        }
+        if (p.ss_out != nullptr) {
+          const float cs = chunk_sumsq8(v);
+          if ((tid & 7) == 0 && ok) p.ss_out[m * p.ld_ss_out + (n >> 3)] = cs;
+        }
+      }
+      return;
+    }
+  }
   if constexpr (EPI == kEpiI32 || EPI == kEpiDequant) {
     if (tid < 256) {
       const int m = tid >> 4;
@@ -282,6 +324,18 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
 
   i32x4 rb[RING][kFusedCH];
 
+  // Residual-add epilogue: the residual of this thread's output in the
+  // first block is requested before anything else, so that epilogue does not
+  // wait behind the weight loads in flight (later blocks load theirs then).
+  [[maybe_unused]] TY res0{};
+  if constexpr (EPI == kEpiDequant) {
+    if (p.add_res != nullptr && tid < 256) {
+      const int m = tid >> 4;
+      const int64_t n = static_cast<int64_t>(blockIdx.x) * 16 + (tid & 15);
+      if (m < M && n < p.N) res0 = static_cast<const TY*>(p.add_res)[m * p.ld_add_res + n];
+    }
+  }
+
   // The epilogue operands of all this workgroup's blocks (n_mine <= 64, one
   // per thread) go to LDS up front: vmcnt counts loads in issue order, so a
   // scale loaded at epilogue time would wait for every weight load in flight.
@@ -395,6 +449,25 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
                      wrsrc, row_live && c * 8 < K ? c * 16 : kOutside, 0, 0));
     }
   }
+  // With the producer's chunk sums (ss_in): lane l of each wavefront of row
+  // `row` takes the sums of chunks 64 g + l, g < 8 (zeros past the row).
+  [[maybe_unused]] float pv[NORM ? 8 : 1];
+  if constexpr (NORM) {
+    if (p.ss_in != nullptr) {
+      const int nck = (K + 7) / 8;
+      const int nrec = __builtin_amdgcn_readfirstlane(
+          static_cast<int>(((M - 1) * p.ld_ss_in + nck) * 4));
+      const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<float*>(p.ss_in), 0, nrec, kBufferWord3);
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        const int c = 64 * g + lane;
+        const int off =
+            row_live && c < nck ? static_cast<int>((row * p.ld_ss_in + c) * 4) : kOutside;
+        pv[g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srsrc, off, 0, 0));
+      }
+    }
+  }
   load_ops();
   if constexpr (NORM) {
     // Every workgroup normalizes the same rows identically; workgroup 0
@@ -450,34 +523,46 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
                                     static_cast<int64_t>(c) * 8) = raw[i];
         }
       }
-      float ss = 0.0f;
+      if (p.ss_in == nullptr) {
+        float ss = 0.0f;
 #pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const float lo = bits_to_f32<TX>(raw[i][q] & 0xffffu);
-        const float hi = bits_to_f32<TX>(raw[i][q] >> 16);
-        if constexpr (kHalf) {
-          ss = __builtin_fmaf(lo, lo, ss);
-          ss = __builtin_fmaf(hi, hi, ss);
-        } else {
-          ss = __fadd_rn(ss, __fmul_rn(lo, lo));
-          ss = __fadd_rn(ss, __fmul_rn(hi, hi));
+        for (int q = 0; q < 4; ++q) {
+          const float lo = bits_to_f32<TX>(raw[i][q] & 0xffffu);
+          const float hi = bits_to_f32<TX>(raw[i][q] >> 16);
+          if constexpr (kHalf) {
+            ss = __builtin_fmaf(lo, lo, ss);
+            ss = __builtin_fmaf(hi, hi, ss);
+          } else {
+            ss = __fadd_rn(ss, __fmul_rn(lo, lo));
+            ss = __fadd_rn(ss, __fmul_rn(hi, hi));
+          }
+        }
+        sq[i] = wave_sum_xor(ss);
+      }
+    }
+    float tot;
+    if (p.ss_in == nullptr) {
+      if (lane == 0 && row_live) {
+#pragma unroll
+        for (int i = 0; i < NCH; ++i) {
+          const int c = j0 + i * tpr;  // lane 0's chunk: the group's first
+          if (c < 512) ss_g[row][c >> 6] = sq[i];
         }
       }
-      sq[i] = wave_sum_xor(ss);
-    }
-    if (lane == 0 && row_live) {
+      __syncthreads();
+      // Groups past the row's chunks hold zeros in the prologue kernel:
+      // adding them changes nothing, so only the written groups are summed.
+      const int ngroups = min(8, (tpr >> 6) * NCH);
+      tot = ss_g[row_live ? row : 0][0];
+      for (int g = 1; g < ngroups; ++g) tot = __fadd_rn(tot, ss_g[row_live ? row : 0][g]);
+    } else {
+      // The same butterflies and group sums on the producer's chunk sums,
+      // by every wavefront of the row on its own: no barrier, and the
+      // weight stream starts as early as in the kernel without the norm.
+      tot = wave_sum_xor(pv[0]);
 #pragma unroll
-      for (int i = 0; i < NCH; ++i) {
-        const int c = j0 + i * tpr;  // lane 0's chunk: the group's first
-        if (c < 512) ss_g[row][c >> 6] = sq[i];
-      }
+      for (int g = 1; g < 8; ++g) tot = __fadd_rn(tot, wave_sum_xor(pv[g]));
     }
-    __syncthreads();
-    // Groups past the row's chunks hold zeros in the prologue kernel: adding
-    // them changes nothing, so only the written groups are summed.
-    const int ngroups = min(8, (tpr >> 6) * NCH);
-    float tot = ss_g[row_live ? row : 0][0];
-    for (int g = 1; g < ngroups; ++g) tot = __fadd_rn(tot, ss_g[row_live ? row : 0][g]);
     const float var = tot / static_cast<float>(p.K);
     const float rstd = 1.0f / sqrtf(__fadd_rn(var, p.eps));
 #pragma unroll
@@ -600,7 +685,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       acc = i32x4{0, 0, 0, 0};
       __syncthreads();
       const int64_t nb = static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(j) * p.G;
-      epilogue<EPI, TY, TH>(p, red[par], row_s, nb, tid, ops_lds + j * 32);
+      epilogue<EPI, TY, TH>(p, red[par], row_s, nb, tid, ops_lds + j * 32, j == 0 ? &res0 : nullptr);
 #if W8A8_TIMELINE
       if (j < kStampEnd - kStampBlock0) W8A8_STAMP(stamps, kStampBlock0 + j);
 #endif
@@ -781,6 +866,12 @@ hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const Line
   p.x_out = nullptr;
   p.ld_xout = 0;
   p.absmax_parts = op.absmax_parts;
+  p.add_res = op.res;
+  p.ld_add_res = op.ld_res;
+  p.ss_out = op.ss_parts;
+  p.ld_ss_out = op.ld_parts;
+  p.ss_in = nullptr;
+  p.ld_ss_in = 0;
   p.out_scale = op.out_scale;
   p.M = static_cast<int>(op.M);
   p.N = static_cast<int>(op.N);
@@ -828,7 +919,8 @@ bool fused_norm_supported(const void* x, int x_dtype, int64_t ldx, const void* r
 hipError_t launch_gemv_fused_norm(const void* x, int x_dtype, int64_t ldx, const void* residual,
                                   int64_t ld_res, void* residual_out, int64_t ld_res_out,
                                   const void* norm_w, float eps, void* x_out, int64_t ld_xout,
-                                  const LinearOperands& op, float* sx_out, hipStream_t st) {
+                                  const LinearOperands& op, float* sx_out, hipStream_t st,
+                                  const float* ss_in, int64_t ld_ss_in) {
   FusedParams p;
   p.x = x;
   p.ldx = ldx;
@@ -848,6 +940,12 @@ hipError_t launch_gemv_fused_norm(const void* x, int x_dtype, int64_t ldx, const
   p.eps = eps;
   p.x_out = x_out;
   p.ld_xout = ld_xout;
+  p.add_res = nullptr;
+  p.ld_add_res = 0;
+  p.ss_out = nullptr;
+  p.ld_ss_out = 0;
+  p.ss_in = ss_in;
+  p.ld_ss_in = ld_ss_in;
   p.out_scale = op.out_scale;
   p.M = static_cast<int>(op.M);
   p.N = static_cast<int>(op.N);
@@ -901,6 +999,12 @@ hipError_t launch_gemv_fused_i8(const LinearOperands& op, hipStream_t st) {
   p.x_out = nullptr;
   p.ld_xout = 0;
   p.absmax_parts = op.absmax_parts;
+  p.add_res = op.res;
+  p.ld_add_res = op.ld_res;
+  p.ss_out = op.ss_parts;
+  p.ld_ss_out = op.ld_parts;
+  p.ss_in = nullptr;
+  p.ld_ss_in = 0;
   p.out_scale = op.out_scale;
   p.M = static_cast<int>(op.M);
   p.N = static_cast<int>(op.N);

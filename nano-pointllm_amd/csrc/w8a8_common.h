@@ -359,6 +359,31 @@ __device__ inline uint32_t wave_max_u32(uint32_t v) {
   return wave_butterfly(v, [](uint32_t x, uint32_t y) { return x > y ? x : y; });
 }
 
+// ------------------------------------------------- residual-add epilogue
+// The residual add of a decoder layer in the activation dtype (hidden +
+// attn_out, hidden + mlp_out: lightweight_runner.py:247-257, 552): the
+// linear's output already rounded to T plus the residual, rounded to T once
+// (binary32 holds the sum of two binary16 / bfloat16 values closely enough
+// that its rounding to T is the correct rounding of the exact sum).
+template <typename T>
+__device__ inline T add_rounded(T y, T r) {
+  return from_f32<T>(__fadd_rn(to_f32(y), to_f32(r)));
+}
+
+// RMSNorm sums of squares per 8-column chunk, in the order of the norm
+// kernels (per chunk in element order from +0, each square rounded to
+// binary32 and added with one rounding): lanes 8j .. 8j+7 hold elements 0..7
+// of one chunk (0 for an element past the row) and every lane of the group
+// returns the chunk's sum.  Every lane of the wavefront must be active.
+__device__ inline float chunk_sumsq8(float v) {
+  const float sq = __fmul_rn(v, v);
+  const int base = static_cast<int>(__lane_id()) & ~7;
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s = __fadd_rn(s, __shfl(sq, base + j));
+  return s;
+}
+
 // Packed-tile byte offset of element (r, k) of a [rows, K] operand.
 __host__ __device__ inline int64_t packed_offset(int64_t r, int64_t k, int64_t KB) {
   int64_t tile = (r >> 4) * KB + (k >> 6);

@@ -40,6 +40,15 @@ struct LinearOperands {
   // (m, nb) with m < M is written by exactly one thread, so no atomics and no
   // initialization are needed.
   float* absmax_parts = nullptr;
+  // kEpiDequant with a 16-bit output only (nullable): y = dtype(dtype(dequant)
+  // + res[m, n]) (res [M, ld_res] of y's dtype), and with ss_parts the
+  // RMSNorm sums of squares of y per 8-column chunk (chunk_sumsq8),
+  // ss_parts[m * ld_parts + n / 8].  Taken by gemv_kernel and the fused
+  // decode kernels; launch_gemv routes such calls to them.
+  const void* res = nullptr;
+  int64_t ld_res = 0;
+  float* ss_parts = nullptr;
+  int64_t ld_parts = 0;
   int64_t M, N, K;
   int epi;
 };
@@ -73,6 +82,13 @@ hipError_t launch_requant_i32(const int32_t* acc, int64_t ld_acc, const int32_t*
 hipError_t launch_dequant_i32_bf16(const int32_t* acc, int64_t ld_acc, const uint16_t* sa_bits,
                                    const uint16_t* sw_bits, uint16_t* y, int64_t ldy, int64_t M,
                                    int64_t N, hipStream_t st);
+
+// y[m, n] = dtype(y[m, n] + res[m, n]) over 16-bit rows (dtype kF16 / kBF16)
+// and, with parts (nullable), their RMSNorm sums of squares per 8-column
+// chunk (chunk_sumsq8) into parts[m * ld_parts + n / 8].
+hipError_t launch_add_rows_ss(void* y, int dtype, int64_t ldy, const void* res, int64_t ld_res,
+                              float* parts, int64_t ld_parts, int64_t M, int64_t N,
+                              hipStream_t st);
 
 // Quantizes each row of x (scale_in == nullptr: dynamic per-row scale).
 // Row-major output writes columns [0, ncols_out) (zeros past K); packed
@@ -143,9 +159,13 @@ bool fused_norm_supported(const void* x, int x_dtype, int64_t ldx, const void* r
                           int64_t ld_res, const void* residual_out, int64_t ld_res_out,
                           const void* norm_w, const void* x_out, int64_t ld_xout, int64_t M,
                           int64_t N, int64_t K);
+// ss_in (nullable, [M, ld_ss_in] binary32): the RMSNorm sums of squares of
+// x per 8-column chunk as the residual-add epilogue wrote them (residual
+// must then be null); they replace the workgroup's own sums (same bits).
 hipError_t launch_gemv_fused_norm(const void* x, int x_dtype, int64_t ldx, const void* residual,
                                   int64_t ld_res, void* residual_out, int64_t ld_res_out,
                                   const void* norm_w, float eps, void* x_out, int64_t ld_xout,
-                                  const LinearOperands& op, float* sx_out, hipStream_t st);
+                                  const LinearOperands& op, float* sx_out, hipStream_t st,
+                                  const float* ss_in = nullptr, int64_t ld_ss_in = 0);
 
 }  // namespace w8a8

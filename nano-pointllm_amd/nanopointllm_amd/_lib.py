@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libw8a8_gfx950.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 F32, F16, BF16, I32, I8 = 0, 1, 2, 3, 4
 EPI_I32, EPI_DEQUANT, EPI_SILU_MUL, EPI_SILU_MUL_Q8 = 0, 1, 2, 3
@@ -52,6 +52,9 @@ EXPORTED_SYMBOLS = (
     "w8a8_linear",
     "w8a8_linear_noalloc",
     "w8a8_rmsnorm_linear",
+    "w8a8_rmsnorm_linear_ss",
+    "w8a8_linear_residual",
+    "w8a8_linear_i8in_residual",
     "w8a8_linear_i8in",
     "w8a8_linear_packed",
     "w8a8_linear_i8in_requant",
@@ -88,6 +91,13 @@ _SIGNATURES = {
     "w8a8_rmsnorm_linear": (_int, [_vp, _int, _i64, _vp, _i64, _vp, _i64, _vp, _f32, _vp, _vp,
                                    _vp, _int, _vp, _int, _i64, _f32, _int, _i64, _i64, _i64,
                                    _vp, _vp, _i64, _vp, _i64, _vp]),
+    "w8a8_rmsnorm_linear_ss": (_int, [_vp, _int, _i64, _vp, _i64, _vp, _f32, _vp, _vp, _vp,
+                                      _int, _vp, _int, _i64, _f32, _int, _i64, _i64, _i64, _vp,
+                                      _vp, _i64, _vp]),
+    "w8a8_linear_residual": (_int, [_vp, _int, _i64, _vp, _vp, _vp, _vp, _int, _i64, _vp, _i64,
+                                    _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
+    "w8a8_linear_i8in_residual": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _int, _i64, _vp,
+                                         _i64, _vp, _i64, _i64, _i64, _i64, _vp, _i64, _vp]),
     "w8a8_linear_i8in": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _int, _vp, _int, _i64, _f32,
                                 _int, _i64, _i64, _i64, _vp, _i64, _vp]),
     "w8a8_linear_packed": (_int, [_vp, _vp, _vp, _vp, _vp, _int, _vp, _int, _i64, _f32, _int,

@@ -172,6 +172,24 @@ class W8A8Linear(nn.Module):
         return _w.linear_i8in(xq, x_scale, p.packed, p.scale, p.bias, p.out_features,
                               out_dtype=out_dtype, in_features=p.in_features)
 
+    def forward_residual(self, x: torch.Tensor, residual: torch.Tensor) -> _w.ResidualOutput:
+        """``residual + self(x)`` in the activation dtype with the RMSNorm
+        chunk sums of the result (``linear_residual``): the residual add of a
+        decoder layer after o_proj / down_proj (lightweight_runner.py:247-257,
+        552) in this linear's epilogue.  Dynamic per-token activations only."""
+        if self.smooth is not None or self.static_scale is not None:
+            raise ValueError("the residual-add epilogue takes per-token dynamic activations")
+        p = self.weight_q
+        return _w.linear_residual(x, p.packed, p.scale, p.bias, p.out_features, residual,
+                                  in_features=p.in_features)
+
+    def forward_i8_residual(self, xq: torch.Tensor, x_scale: torch.Tensor,
+                            residual: torch.Tensor) -> _w.ResidualOutput:
+        """:meth:`forward_residual` on int8 activations with per-row scales."""
+        p = self.weight_q
+        return _w.linear_i8in_residual(xq, x_scale, p.packed, p.scale, p.bias, p.out_features,
+                                       residual, in_features=p.in_features)
+
     def accumulators(self, x: torch.Tensor) -> torch.Tensor:
         """Raw int32 accumulators of ``forward`` (for exactness checks)."""
         p = self.weight_q
@@ -237,6 +255,18 @@ class W8A8PackedQKV(nn.Module):
                                 residual=_rows2(residual), in_features=lin.in_features)
         q, k, v = self._split(out.y)
         return q, k, v, out.residual
+
+    def project_rmsnorm_ss(self, hidden_states: torch.Tensor, ss_parts: torch.Tensor,
+                           norm: nn.Module
+                           ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+        """:meth:`project_rmsnorm` on rows that a residual-add linear wrote
+        with their RMSNorm chunk sums ``ss_parts``: the one-kernel decode
+        route reads the sums instead of summing the rows (the same bits)."""
+        lin = self.linear.weight_q
+        out = _w.rmsnorm_linear(_rows2(hidden_states), norm.weight, _norm_eps(norm), lin.packed,
+                                lin.scale, lin.bias, lin.out_features,
+                                in_features=lin.in_features, ss_parts=ss_parts)
+        return self._split(out.y)
 
     def _split(self, qkv: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
         q_size = self.num_heads * self.head_dim
@@ -397,6 +427,24 @@ class W8A8MLP(nn.Module):
             return first.residual, self.down(first.y)
         return first.residual, self.down.forward_i8(first.y, self._h_rows(first.y),
                                                     out_dtype=hidden_states.dtype)
+
+    def forward_rmsnorm_ss_residual(self, hidden_states: torch.Tensor, ss_parts: torch.Tensor,
+                                    norm: nn.Module) -> _w.ResidualOutput:
+        """``hidden_states + mlp(norm(hidden_states))`` for rows that a
+        residual-add linear wrote with their RMSNorm chunk sums ``ss_parts``
+        (the o_proj of :meth:`W8A8Linear.forward_residual`): the norm and
+        gate/up run as one launch that reads the sums, and down adds the
+        rows back in its epilogue and returns the next norm's sums
+        (lightweight_runner.py:247-257, 320-383, 552)."""
+        p = self.gate_up.weight_q
+        epi = _lib.EPI_SILU_MUL if self.h_scale is None else _lib.EPI_SILU_MUL_Q8
+        h = _w.rmsnorm_linear(hidden_states, norm.weight, _norm_eps(norm), p.packed, p.scale,
+                              p.bias, p.out_features, epilogue=epi,
+                              y_scale=0.0 if self.h_scale is None else self.h_scale,
+                              in_features=p.in_features, ss_parts=ss_parts).y
+        if self.h_scale is None:
+            return self.down.forward_residual(h, hidden_states)
+        return self.down.forward_i8_residual(h, self._h_rows(h), hidden_states)
 
     def forward_i8(self, xq: torch.Tensor, x_scale: torch.Tensor, *,
                    out_dtype: torch.dtype = torch.float16) -> torch.Tensor:

@@ -27,6 +27,12 @@ with the quantization of its output:
    (lightweight_runner.py:320-383);
 7. the final residual add in the activation dtype, as the reference does.
 
+At decode batches (at most 8 rows) the residual adds move into the
+epilogues of o_proj and down, which also write the RMSNorm sums of squares
+of their rows per 8 columns; the next norm + projection launch reads those
+sums instead of summing the rows in every workgroup
+(:meth:`W8A8LlamaLayer.forward_stream`), with the same bits.
+
 After the last layer, its residual add and the final ``norm``
 (``LightweightRMSNorm``, lightweight_runner.py:609, 675) run as one launch of
 the activation prologue, the same kernel and formula as the in-layer norms,
@@ -126,6 +132,30 @@ class W8A8LlamaLayer(nn.Module):
         return mlp_out, residual
 
 
+    @torch.no_grad()
+    def forward_stream(self, hidden_states: torch.Tensor, ss_parts: torch.Tensor | None,
+                       attention_state: Any = None) -> tuple[torch.Tensor, torch.Tensor]:
+        """The layer on the residual stream itself: ``hidden_states`` are the
+        layer's input rows with every residual add done, ``ss_parts`` their
+        RMSNorm sums of squares per 8 columns when a residual-add linear wrote
+        them (None for rows from elsewhere).  o_proj and down add the
+        residual in their epilogues (lightweight_runner.py:247-257, 552) and
+        return the sums their rows' norms need, so the RMSNorm launches in
+        front of the packed QKV and gate/up read those sums instead of summing
+        every row in every workgroup.  Returns ``(output rows, their sums)``;
+        the bits are those of :meth:`forward`.  Needs per-token dynamic
+        activations on o_proj."""
+        rows = _rows(hidden_states)
+        if ss_parts is None:
+            q, k, v = self.qkv.project_rmsnorm(rows, self.input_layernorm)
+        else:
+            q, k, v = self.qkv.project_rmsnorm_ss(rows, ss_parts, self.input_layernorm)
+        context = self.attention_core(q, k, v, self.layer_index, attention_state)
+        summed, parts = self.o_proj.forward_residual(context, rows)
+        out = self.mlp.forward_rmsnorm_ss_residual(summed, parts, self.post_attention_layernorm)
+        return out.y, out.ss_parts
+
+
 class W8A8LlamaRunner(nn.Module):
     """``LightweightLlamaRunner`` (lightweight_runner.py:563-737) with W8A8
     decoder layers: ``embed_tokens`` -> layers -> ``norm`` -> ``lm_head``.
@@ -161,13 +191,32 @@ class W8A8LlamaRunner(nn.Module):
             hidden_states = self.embed_tokens(input_ids)
         else:
             hidden_states = inputs_embeds
+        shape = hidden_states.shape
+        rows = _rows(hidden_states)
+        if self.stream_route(rows):
+            # Decode: o_proj and down add the residual in their epilogues and
+            # hand the next norm its sums of squares (forward_stream).
+            hidden, parts = rows, None
+            for layer in self.layers:
+                hidden, parts = layer.forward_stream(hidden, parts, attention_state)
+            return self.lm_head(self.final_norm(hidden, None).view(shape))
         # Each layer's final residual add (lightweight_runner.py:552) runs in
         # the next layer's RMSNorm + QKV launch; the last one in the final norm's.
-        shape = hidden_states.shape
-        hidden, residual = _rows(hidden_states), None
+        hidden, residual = rows, None
         for layer in self.layers:
             hidden, residual = layer.forward_carry(hidden, residual, attention_state)
         return self.lm_head(self.final_norm(hidden, residual).view(shape))
+
+    def stream_route(self, rows: torch.Tensor) -> bool:
+        """Whether a forward over ``rows`` takes :meth:`W8A8LlamaLayer.forward_stream`:
+        decode batches (at most 8 rows, where the RMSNorm + projection runs as
+        one kernel per CU and the sums spare each CU the row sums) of 16-bit
+        rows, with per-token dynamic o_proj activations.  Both routes give the
+        same bits; larger batches keep the residual adds in the norm
+        launches, which sum the rows once per row, not once per CU."""
+        return (rows.shape[0] <= 8 and rows.dtype in (torch.float16, torch.bfloat16)
+                and all(layer.o_proj.smooth is None and layer.o_proj.static_scale is None
+                        for layer in self.layers))
 
     def final_norm(self, hidden: torch.Tensor, residual: torch.Tensor | None) -> torch.Tensor:
         """``norm(dtype(hidden + residual))`` for ``[T, hidden]`` rows

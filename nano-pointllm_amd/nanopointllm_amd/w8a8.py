@@ -215,6 +215,90 @@ def linear_dynamic(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tenso
     return y.reshape(*x.shape[:-1], cols)
 
 
+class ResidualOutput(NamedTuple):
+    y: torch.Tensor                 # dtype(linear(x) + residual): the new residual stream
+    ss_parts: torch.Tensor | None   # [rows, ceil(n/8)] binary32 RMSNorm chunk sums of y
+
+
+def _residual_rows(residual: torch.Tensor, m: int, n: int,
+                   dtype: torch.dtype) -> tuple[torch.Tensor, int]:
+    if residual.dtype != dtype or residual.shape[-1] != n or residual.numel() != m * n:
+        raise ValueError("residual must be [rows, n] rows of the output dtype")
+    return _rows_view(residual)
+
+
+def _residual_call(name: str, args: list, m: int, k: int, device, *, retry: bool) -> None:
+    lib = _lib.load()
+    stream = _lib.stream_handle(device)
+    fn = getattr(lib, name)
+    if retry:
+        rc = fn(*args, None, 0, stream)
+        if rc == _lib.ERR_WORKSPACE:
+            ws = _workspace(m, k, device)
+            rc = fn(*args, ws.data_ptr(), ws.numel(), stream)
+    else:
+        ws = _workspace(m, k, device)
+        rc = fn(*args, ws.data_ptr(), ws.numel(), stream)
+    _lib.check(rc, name)
+
+
+def linear_residual(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor,
+                    bias: torch.Tensor | None, n: int, residual: torch.Tensor, *,
+                    ss_parts: bool = True, in_features: int | None = None) -> ResidualOutput:
+    """``residual + linear(x)`` in the activation dtype, the residual add of a
+    decoder layer after its o_proj / down_proj (``residual_norm``,
+    lightweight_runner.py:247-257, 552), folded into the dequant epilogue of
+    the per-token dynamic W8A8 linear (``w8a8_linear_residual``).  With
+    ``ss_parts`` the RMSNorm sums of squares of the result per 8 columns come
+    back too, for :func:`rmsnorm_linear` on the same rows."""
+    device = _lib.require_cuda(x, w_packed, w_scale, bias, residual)
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("the residual stream is float16 / bfloat16")
+    x2, ldx = _rows_view(x)
+    m, k = x2.shape
+    _check_operands(k, w_packed, w_scale, bias, n, in_features)
+    r2, ldr = _residual_rows(residual, m, n, x.dtype)
+    y = torch.empty((m, n), dtype=x.dtype, device=device)
+    nck = (n + 7) // 8
+    parts = torch.empty((m, nck), dtype=torch.float32, device=device) if ss_parts else None
+    if m and n:
+        args = [x2.data_ptr(), _lib.dtype_code(x.dtype), ldx, w_packed.data_ptr(),
+                w_scale.data_ptr(), _lib.ptr(bias), y.data_ptr(), _lib.dtype_code(x.dtype), n,
+                r2.data_ptr(), ldr, _lib.ptr(parts), nck, m, n, k]
+        # Decode shapes run fused and need no workspace (as linear_dynamic).
+        _residual_call("w8a8_linear_residual", args, m, k, device, retry=True)
+    return ResidualOutput(y.reshape(*x.shape[:-1], n), parts)
+
+
+def linear_i8in_residual(xq: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor,
+                         w_scale: torch.Tensor, bias: torch.Tensor | None, n: int,
+                         residual: torch.Tensor, *, ss_parts: bool = True,
+                         in_features: int | None = None) -> ResidualOutput:
+    """:func:`linear_residual` on int8 activations with per-row scales
+    (``w8a8_linear_i8in_residual``); the output has the residual's dtype."""
+    device = _lib.require_cuda(xq, x_scale, w_packed, w_scale, bias, residual)
+    if xq.dtype != torch.int8:
+        raise ValueError("linear_i8in_residual expects int8 activations")
+    if residual.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError("the residual stream is float16 / bfloat16")
+    x2, ldq = _rows_view(xq)
+    m, k = x2.shape
+    _check_operands(k, w_packed, w_scale, bias, n, in_features)
+    s = x_scale.detach().to(dtype=torch.float32).reshape(-1).contiguous()
+    if s.numel() != m:
+        raise ValueError("x_scale must have one value per row")
+    r2, ldr = _residual_rows(residual, m, n, residual.dtype)
+    y = torch.empty((m, n), dtype=residual.dtype, device=device)
+    nck = (n + 7) // 8
+    parts = torch.empty((m, nck), dtype=torch.float32, device=device) if ss_parts else None
+    if m and n:
+        args = [x2.data_ptr(), ldq, s.data_ptr(), w_packed.data_ptr(), w_scale.data_ptr(),
+                _lib.ptr(bias), y.data_ptr(), _lib.dtype_code(residual.dtype), n, r2.data_ptr(),
+                ldr, _lib.ptr(parts), nck, m, n, k]
+        _residual_call("w8a8_linear_i8in_residual", args, m, k, device, retry=False)
+    return ResidualOutput(y.reshape(*xq.shape[:-1], n), parts)
+
+
 def linear_i8in(xq: torch.Tensor, x_scale: torch.Tensor, w_packed: torch.Tensor,
                 w_scale: torch.Tensor, bias: torch.Tensor | None, n: int, *,
                 epilogue: int = _lib.EPI_DEQUANT, out_dtype: torch.dtype | None = None,
@@ -409,7 +493,8 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
                    n: int, *, residual: torch.Tensor | None = None,
                    epilogue: int = _lib.EPI_DEQUANT, out_dtype: torch.dtype | None = None,
                    y_scale: float = 0.0, return_rows: bool = False,
-                   in_features: int | None = None) -> NormLinearOutput:
+                   in_features: int | None = None,
+                   ss_parts: torch.Tensor | None = None) -> NormLinearOutput:
     """``LightweightRMSNorm`` (lightweight_runner.py:239-257, with the
     residual add of ``residual_norm`` when ``residual`` is given) in front of a
     W8A8 linear with per-token dynamic quantization of the normalized rows:
@@ -418,7 +503,12 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     dtype runs through ``w8a8_rmsnorm_linear`` (one kernel at decode shapes;
     otherwise the prologue writes the int8 rows in the product's own layout);
     a binary32 norm weight runs the activation prologue and the int8-in
-    linear."""
+    linear.
+
+    ``ss_parts`` (no residual): the RMSNorm chunk sums of these very rows as
+    :func:`linear_residual` returned them; the one-kernel decode route reads
+    them instead of summing the rows in every workgroup
+    (``w8a8_rmsnorm_linear_ss``, the same bits)."""
     device = _lib.require_cuda(x, norm_weight, w_packed, w_scale, bias, residual)
     if x.dtype not in (torch.float16, torch.bfloat16):
         raise ValueError("the activation prologue takes float16 / bfloat16 rows")
@@ -449,19 +539,35 @@ def rmsnorm_linear(x: torch.Tensor, norm_weight: torch.Tensor, eps: float,
     rows = torch.empty((m, k), dtype=x.dtype, device=device) if return_rows else None
     cols = _out_cols(epilogue, n)
     y = torch.empty((m, cols), dtype=out_dtype, device=device)
+    use_ss = ss_parts is not None and residual is None and not return_rows
+    if use_ss:
+        if (ss_parts.dtype != torch.float32 or ss_parts.dim() != 2
+                or ss_parts.shape[0] != m or ss_parts.shape[1] < (k + 7) // 8
+                or ss_parts.stride(1) != 1 or ss_parts.device != x.device):
+            raise ValueError("ss_parts must be float32 [rows, >= ceil(K/8)] RMSNorm chunk sums")
     if m and n:
         lib = _lib.load()
-        args = [x2.data_ptr(), _lib.dtype_code(x.dtype), ldx, _lib.ptr(res2), ld_res,
-                _lib.ptr(res_out), k, w.data_ptr(), float(eps), w_packed.data_ptr(),
-                w_scale.data_ptr(), _lib.ptr(bias), epilogue, y.data_ptr(),
-                _lib.dtype_code(out_dtype), cols, float(y_scale), _lib.dtype_code(x.dtype), m, n,
-                k, None, _lib.ptr(rows), k]
         stream = _lib.stream_handle(device)
-        rc = lib.w8a8_rmsnorm_linear(*args, None, 0, stream)
+        if use_ss:
+            name = "w8a8_rmsnorm_linear_ss"
+            args = [x2.data_ptr(), _lib.dtype_code(x.dtype), ldx, ss_parts.data_ptr(),
+                    ss_parts.stride(0), w.data_ptr(), float(eps), w_packed.data_ptr(),
+                    w_scale.data_ptr(), _lib.ptr(bias), epilogue, y.data_ptr(),
+                    _lib.dtype_code(out_dtype), cols, float(y_scale), _lib.dtype_code(x.dtype),
+                    m, n, k, None]
+        else:
+            name = "w8a8_rmsnorm_linear"
+            args = [x2.data_ptr(), _lib.dtype_code(x.dtype), ldx, _lib.ptr(res2), ld_res,
+                    _lib.ptr(res_out), k, w.data_ptr(), float(eps), w_packed.data_ptr(),
+                    w_scale.data_ptr(), _lib.ptr(bias), epilogue, y.data_ptr(),
+                    _lib.dtype_code(out_dtype), cols, float(y_scale), _lib.dtype_code(x.dtype),
+                    m, n, k, None, _lib.ptr(rows), k]
+        fn = getattr(lib, name)
+        rc = fn(*args, None, 0, stream)
         if rc == _lib.ERR_WORKSPACE:
             ws = _workspace(m, k, device)
-            rc = lib.w8a8_rmsnorm_linear(*args, ws.data_ptr(), ws.numel(), stream)
-        _lib.check(rc, "w8a8_rmsnorm_linear")
+            rc = fn(*args, ws.data_ptr(), ws.numel(), stream)
+        _lib.check(rc, name)
     lead = x.shape[:-1]
     return NormLinearOutput(y.reshape(*lead, cols),
                             None if res_out is None else res_out.reshape(x.shape),

@@ -200,6 +200,43 @@ def _p(addr):
     return None if addr is None else ctypes.c_void_p(addr)
 
 
+def test_residual_add_arguments_rejected_without_launch():
+    lib = _lib.load()
+    fake, other = ctypes.c_void_p(0x1000), ctypes.c_void_p(0x100000)
+    parts = ctypes.c_void_p(0x200000)
+
+    def lr(y_dtype=_lib.F16, res=other, ld_res=16, ss=parts, ld_ss=2, m=1, n=16, y=fake):
+        return lib.w8a8_linear_residual(fake, _lib.F16, 64, fake, fake, None, y, y_dtype, 16,
+                                        res, ld_res, ss, ld_ss, m, n, 64, fake, 1 << 20, None)
+    # a 16-bit output only; the residual is required; leading dimensions
+    assert lr(y_dtype=_lib.F32) == _lib.ERR_DTYPE
+    assert lr(res=None) == _lib.ERR_NULL
+    assert lr(ld_res=8) == _lib.ERR_SHAPE
+    assert lr(ld_ss=1) == _lib.ERR_SHAPE
+    # misaligned residual or sums
+    assert lr(res=ctypes.c_void_p(0x100001)) == _lib.ERR_ALIGN
+    assert lr(ss=ctypes.c_void_p(0x200002)) == _lib.ERR_ALIGN
+    # y, residual and sums must not overlap
+    assert lr(res=fake) == _lib.ERR_OVERLAP
+    assert lr(ss=ctypes.c_void_p(0x1010)) == _lib.ERR_OVERLAP
+    # empty problems are valid no-ops
+    assert lr(m=0) == _lib.OK
+    assert lib.w8a8_linear_i8in_residual(fake, 64, fake, fake, fake, None, fake, _lib.F32, 16,
+                                         other, 16, parts, 2, 1, 16, 64, fake, 1 << 20,
+                                         None) == _lib.ERR_DTYPE
+    assert lib.w8a8_linear_i8in_residual(fake, 64, fake, fake, fake, None, fake, _lib.F16, 16,
+                                         fake, 16, parts, 2, 1, 16, 64, fake, 1 << 20,
+                                         None) == _lib.ERR_OVERLAP
+    # RMSNorm on residual-stream rows: the sums cover every 8 columns of K
+    assert lib.w8a8_rmsnorm_linear_ss(fake, _lib.F16, 64, parts, 7, fake, 1e-6, fake, fake, None,
+                                      _lib.EPI_DEQUANT, other, _lib.F16, 16, 0.0, _lib.F16, 1,
+                                      16, 64, None, fake, 1 << 20, None) == _lib.ERR_SHAPE
+    assert lib.w8a8_rmsnorm_linear_ss(fake, _lib.F16, 64, ctypes.c_void_p(0x200002), 8, fake,
+                                      1e-6, fake, fake, None, _lib.EPI_DEQUANT, other, _lib.F16,
+                                      16, 0.0, _lib.F16, 1, 16, 64, None, fake, 1 << 20,
+                                      None) == _lib.ERR_ALIGN
+
+
 def test_status_errors_map_to_python_exceptions():
     with pytest.raises(ValueError, match="workspace"):
         _lib.check(_lib.ERR_WORKSPACE, "w8a8_linear")
