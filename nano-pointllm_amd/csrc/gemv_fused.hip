@@ -138,42 +138,39 @@ typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 // Sums the per-wave partials of output block nb and writes its outputs.
 // `ops` holds the block's 16 weight scales followed by its 16 biases.
-template <int EPI, typename TY, typename TH>
+template <int EPI, typename TY, typename TH, bool RES>
 __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
                                 const float* row_s, int64_t nb, int tid, const float* ops,
-                                const TY* res_pre = nullptr) {
+                                const TY* res_pre) {
   const bool has_bias = p.bias != nullptr;
   const int M = p.M;
-  if constexpr (EPI == kEpiDequant) {
-    if (p.add_res != nullptr) {
-      // Residual-add epilogue; threads below 256 fill whole wavefronts, so
-      // the chunk sums run in uniform control flow.
-      if (tid < 256) {
-        const int m = tid >> 4;
-        const int64_t n = nb * 16 + (tid & 15);
-        const bool ok = m < M && n < p.N;
-        float v = 0.0f;
-        if (ok) {
-          int32_t s = 0;
+  if constexpr (RES) {
+    // Residual-add epilogue (kEpiDequant, 16-bit output); threads below 256
+    // fill whole wavefronts, so the chunk sums run in uniform control flow.
+    static_assert(EPI == kEpiDequant, "residual-add epilogue");
+    if (tid < 256) {
+      const int m = tid >> 4;
+      const int64_t n = nb * 16 + (tid & 15);
+      const bool ok = m < M && n < p.N;
+      float v = 0.0f;
+      if (ok) {
+        int32_t s = 0;
 #pragma unroll
-          for (int w = 0; w < kFusedWaves; ++w) s += red[w][tid];
-          const int r = tid & 15;
-          const TY rv = res_pre != nullptr ? *res_pre
-                                           : static_cast<const TY*>(p.add_res)[m * p.ld_add_res + n];
-          const TY o = add_rounded(from_f32<TY>(dequant1b(s, row_s[m], ops[r], has_bias, ops[16 + r])),
-                                   rv);
-          static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] = o;
-          v = to_f32(o);
-        }
-        if (p.ss_out != nullptr) {
-          const float cs = chunk_sumsq8(v);
-          if ((tid & 7) == 0 && ok) p.ss_out[m * p.ld_ss_out + (n >> 3)] = cs;
-        }
+        for (int w = 0; w < kFusedWaves; ++w) s += red[w][tid];
+        const int r = tid & 15;
+        const TY rv = res_pre != nullptr ? *res_pre
+                                         : static_cast<const TY*>(p.add_res)[m * p.ld_add_res + n];
+        const TY o = add_rounded(from_f32<TY>(dequant1b(s, row_s[m], ops[r], has_bias, ops[16 + r])),
+                                 rv);
+        static_cast<TY*>(p.y)[static_cast<int64_t>(m) * p.ldy + n] = o;
+        v = to_f32(o);
       }
-      return;
+      if (p.ss_out != nullptr) {
+        const float cs = chunk_sumsq8(v);
+        if ((tid & 7) == 0 && ok) p.ss_out[m * p.ld_ss_out + (n >> 3)] = cs;
+      }
     }
-  }
-  if constexpr (EPI == kEpiI32 || EPI == kEpiDequant) {
+  } else if constexpr (EPI == kEpiI32 || EPI == kEpiDequant) {
     if (tid < 256) {
       const int m = tid >> 4;
       const int64_t n = nb * 16 + (tid & 15);
@@ -245,7 +242,7 @@ __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
 // rows per A fragment in LDS, 8 (M <= 8, half a fragment; the other half is
 // zero) or 16 (M <= 16, K <= 6144).
 template <int EPI, typename TX, typename TY, typename TH, int NCH, int RING, int ROWS,
-          bool NORM = false>
+          bool NORM = false, bool RES = false>
 __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p) {
   static_assert(NCH <= kFusedMaxChunks && RING >= 2 && kFusedPreSteps < RING,
                 "fused kernel shape");
@@ -328,8 +325,8 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   // first block is requested before anything else, so that epilogue does not
   // wait behind the weight loads in flight (later blocks load theirs then).
   [[maybe_unused]] TY res0{};
-  if constexpr (EPI == kEpiDequant) {
-    if (p.add_res != nullptr && tid < 256) {
+  if constexpr (RES) {
+    if (tid < 256) {
       const int m = tid >> 4;
       const int64_t n = static_cast<int64_t>(blockIdx.x) * 16 + (tid & 15);
       if (m < M && n < p.N) res0 = static_cast<const TY*>(p.add_res)[m * p.ld_add_res + n];
@@ -410,11 +407,16 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   const int j0 = tid - row * tpr;
   const int nchunk = KB * 8;  // 8-element chunks per padded row
   const bool row_live = row < M;
-  // Branch-free raw buffer loads of x (and of the RMSNorm operands): each
-  // descriptor's range ends with row M-1's K elements (M * ld * 2 < 2^30),
-  // and a chunk outside the rows (of a row >= M, or past K) gets an offset
-  // beyond every range, so it reads zeros without a memory access.  Loads
-  // under a branch would each wait for the one before.
+  // x and the RMSNorm operands.  The NORM kernels use branch-free raw buffer
+  // loads: each descriptor's range ends with row M-1's K elements (M * ld * 2
+  // < 2^30), and a chunk outside the rows (of a row >= M, or past K) gets an
+  // offset beyond every range, so it reads zeros without a memory access.
+  // The others load only the chunks inside the row, under a per-lane
+  // condition: an out-of-range buffer load still takes its turn in the
+  // CU's address unit, and with several chunks per thread past the row (one
+  // row of 4096, or down's 11008 at M = 4) those turns delay the x every
+  // wavefront waits for (measured on MI355X, graphs of 32 layers: O at
+  // M = 1 6.6 against 7.2 us, down at M = 4 12.5 against 13.4 us).
   constexpr int kOutside = 0x7ffffff0;
   const int K = p.K;
   auto rows_rsrc = [&](const void* base, int64_t ld) {
@@ -427,10 +429,22 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
   };
   const __amdgpu_buffer_rsrc_t xrsrc = rows_rsrc(p.x, p.ldx);
   u32x4 raw[NCH];
+  if constexpr (NORM) {
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) {
-    raw[i] = __builtin_bit_cast(
-        u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, chunk_off(j0 + i * tpr, p.ldx), 0, 0));
+    for (int i = 0; i < NCH; ++i) {
+      raw[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             xrsrc, chunk_off(j0 + i * tpr, p.ldx), 0, 0));
+    }
+  } else {
+    const uint16_t* xr =
+        static_cast<const uint16_t*>(p.x) + static_cast<int64_t>(row_live ? row : 0) * p.ldx;
+#pragma unroll
+    for (int i = 0; i < NCH; ++i) {
+      const int c = j0 + i * tpr;
+      raw[i] = u32x4{0u, 0u, 0u, 0u};
+      if (row_live && c * 8 < K)
+        raw[i] = *reinterpret_cast<const u32x4*>(xr + static_cast<int64_t>(c) * 8);
+    }
   }
   // RMSNorm operands, loaded with x (before any weight load is queued); a
   // null residual has an empty range.
@@ -599,7 +613,19 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       am2 = __builtin_elementwise_max(am2, __builtin_bit_cast(u16x2, raw[i][q] & 0x7fff7fffu));
   }
   uint32_t am = max(static_cast<uint32_t>(am2[0]), static_cast<uint32_t>(am2[1]));
-  am = wave_max_u32(am);
+  // At 3-4 rows (4 wavefronts per row) the LDS-permute butterfly instead of
+  // the DPP one: a wavefront that finishes its absmax sooner issues its first
+  // weight step while other wavefronts' x loads still queue for the address
+  // unit, and the workgroup's barriers then wait on them (O at M = 4: 6.7
+  // against 7.2 us; start-up timelines: quantization done at 3.3 against
+  // 3.8 us).  Both give the same maximum.
+  if (NORM || mpad != 4) {
+    am = wave_max_u32(am);
+  } else {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1)
+      am = max(am, static_cast<uint32_t>(__shfl_xor(static_cast<int>(am), off)));
+  }
   W8A8_STAMP(stamps, kStampXReady);
   // The first weight loads go out once x has arrived (the absmax above waits
   // for it) and stream while x is quantized.  Only kFusedPreSteps steps go out
@@ -685,7 +711,8 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       acc = i32x4{0, 0, 0, 0};
       __syncthreads();
       const int64_t nb = static_cast<int64_t>(blockIdx.x) + static_cast<int64_t>(j) * p.G;
-      epilogue<EPI, TY, TH>(p, red[par], row_s, nb, tid, ops_lds + j * 32, j == 0 ? &res0 : nullptr);
+      epilogue<EPI, TY, TH, RES>(p, red[par], row_s, nb, tid, ops_lds + j * 32,
+                                 j == 0 ? &res0 : nullptr);
 #if W8A8_TIMELINE
       if (j < kStampEnd - kStampBlock0) W8A8_STAMP(stamps, kStampBlock0 + j);
 #endif
@@ -709,7 +736,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
 #endif
 }
 
-template <int EPI, typename TX, typename TY, typename TH>
+template <int EPI, typename TX, typename TY, typename TH, bool RES = false>
 hipError_t launch_f(const FusedParams& p, hipStream_t st) {
   // x chunks per thread: rows spread over 1024 / mpad(M) threads each.
   const int mpad = p.M <= 1 ? 1 : (p.M <= 2 ? 2 : (p.M <= 4 ? 4 : (p.M <= 8 ? 8 : 16)));
@@ -718,20 +745,24 @@ hipError_t launch_f(const FusedParams& p, hipStream_t st) {
   const dim3 grid(p.G), block(kFusedThreads);
   constexpr int R8 = kFusedMaxRows, R16 = kFusedMaxRows16;
   if constexpr (std::is_same<TX, int8_t>::value) {
-    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 1, 3, R8>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 1, 3, R8, false, RES>), grid, block, 0,
+                       st, p);
   } else if (p.M > kFusedMaxRows) {
     if (per_thread <= 8)
-      hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 8, 3, R16>), grid, block, 0, st, p);
+      hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 8, 3, R16, false, RES>), grid, block,
+                         0, st, p);
     else
-      hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, kFusedMaxChunks, 3, R16>), grid,
-                         block, 0, st, p);
+      hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, kFusedMaxChunks, 3, R16, false, RES>),
+                         grid, block, 0, st, p);
   } else if (per_thread <= 2) {
-    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 2, 3, R8>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 2, 3, R8, false, RES>), grid, block, 0,
+                       st, p);
   } else if (per_thread <= 4) {
-    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 4, 3, R8>), grid, block, 0, st, p);
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, 4, 3, R8, false, RES>), grid, block, 0,
+                       st, p);
   } else {
-    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, kFusedMaxChunks, 3, R8>), grid, block,
-                       0, st, p);
+    hipLaunchKernelGGL((gemv_fused_kernel<EPI, TX, TY, TH, kFusedMaxChunks, 3, R8, false, RES>),
+                       grid, block, 0, st, p);
   }
   return hipGetLastError();
 }
@@ -780,6 +811,11 @@ hipError_t dispatch_f(const FusedParams& p, int epi, int y_dtype, int h_dtype, h
     case kEpiI32:
       return launch_f<kEpiI32, TX, int32_t, float>(p, st);
     case kEpiDequant:
+      if (p.add_res != nullptr) {  // the residual-add epilogue: 16-bit outputs
+        if (y_dtype == kF16) return launch_f<kEpiDequant, TX, __half, float, true>(p, st);
+        if (y_dtype == kBF16) return launch_f<kEpiDequant, TX, __hip_bfloat16, float, true>(p, st);
+        return hipErrorInvalidValue;
+      }
       if (y_dtype == kF16) return launch_f<kEpiDequant, TX, __half, float>(p, st);
       if (y_dtype == kBF16) return launch_f<kEpiDequant, TX, __hip_bfloat16, float>(p, st);
       if (y_dtype == kF32) return launch_f<kEpiDequant, TX, float, float>(p, st);
