@@ -258,7 +258,7 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       int8_t a_lds[ROWS == kFusedMaxRows ? kFusedMaxKB * 512 : kFusedMaxKB16 * 1024];
   __shared__ int32_t red[2][kFusedWaves][256];
   __shared__ uint32_t amax_w[kFusedWaves];
-  __shared__ float ss_g[NORM ? kFusedMaxRows : 1][8];  // RMSNorm: per row, 8 groups
+  __shared__ float ss_t[NORM ? kFusedMaxRows : 1][64];  // RMSNorm: per row, 64 tree sums
   __shared__ float row_s[ROWS];
   __shared__ float ops_lds[kFusedMaxBlocks * 32];  // per block: 16 scales, 16 biases
 #if W8A8_TIMELINE
@@ -464,7 +464,9 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
     }
   }
   // With the producer's chunk sums (ss_in): lane l of each wavefront of row
-  // `row` takes the sums of chunks 64 g + l, g < 8 (zeros past the row).
+  // `row` takes the sums of chunks 8 l .. 8 l + 7 (zeros past the row), as
+  // two 16-byte loads where all four are inside the row and four 4-byte
+  // loads for the one ragged quad of a row of K % 32 != 0.
   [[maybe_unused]] float pv[NORM ? 8 : 1];
   if constexpr (NORM) {
     if (p.ss_in != nullptr) {
@@ -473,12 +475,24 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
           static_cast<int>(((M - 1) * p.ld_ss_in + nck) * 4));
       const __amdgpu_buffer_rsrc_t srsrc = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<float*>(p.ss_in), 0, nrec, kBufferWord3);
+      const int rbase = static_cast<int>(row * p.ld_ss_in) * 4;
 #pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        const int c = 64 * g + lane;
-        const int off =
-            row_live && c < nck ? static_cast<int>((row * p.ld_ss_in + c) * 4) : kOutside;
-        pv[g] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(srsrc, off, 0, 0));
+      for (int h = 0; h < 2; ++h) {
+        const int c = 8 * lane + 4 * h;
+        if (!row_live || c + 4 <= nck) {
+          const u32x4 v = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                         srsrc, row_live ? rbase + c * 4 : kOutside, 0, 0));
+#pragma unroll
+          for (int j = 0; j < 4; ++j) pv[4 * h + j] = __uint_as_float(v[j]);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            pv[4 * h + j] = c + j < nck ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+                                              srsrc, rbase + (c + j) * 4, 0, 0))
+                                        : 0.0f;
+          }
+        }
       }
     }
   }
@@ -491,13 +505,12 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
       return static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<TX>(lo))) |
              (static_cast<uint32_t>(__builtin_bit_cast(uint16_t, from_f32<TX>(hi))) << 16);
     };
-    // The binary32 sum of squares follows the activation prologue kernel's
-    // order exactly (prologue.hip, 512 threads of one 8-element chunk each
-    // for K <= 4096): per chunk in element order, a butterfly over 64
-    // consecutive chunks, then the 8 groups of 64 in order.  Chunk c of the
-    // row is held here by thread c % TPR as its chunk c / TPR, and TPR is a
-    // multiple of 64, so lane l of a wavefront holds chunk 64 g + l of some
-    // group g and the butterfly is the same.
+    // The binary32 sum of squares takes the order every RMSNorm route shares
+    // for K <= 4096: per chunk in element order, tree8_sum over 8
+    // consecutive chunks, then one butterfly over the 64 tree sums.  Chunk c
+    // of the row is held here by thread c % TPR as its chunk c / TPR, and TPR
+    // is a multiple of 64, so lanes 8 j .. 8 j + 7 of a wavefront hold 8
+    // consecutive chunks starting at a multiple of 8.
     // Every CU normalizes all M rows, so at M = 8 this arithmetic is a large
     // part of the prologue.  For binary16 rows three steps take one packed or
     // mixed-precision instruction and give the same bits as the binary32
@@ -551,31 +564,28 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
             ss = __fadd_rn(ss, __fmul_rn(hi, hi));
           }
         }
-        sq[i] = wave_sum_xor(ss);
+        sq[i] = tree8_sum(ss);
       }
     }
     float tot;
     if (p.ss_in == nullptr) {
-      if (lane == 0 && row_live) {
+      if ((lane & 7) == 0 && row_live) {
 #pragma unroll
         for (int i = 0; i < NCH; ++i) {
-          const int c = j0 + i * tpr;  // lane 0's chunk: the group's first
-          if (c < 512) ss_g[row][c >> 6] = sq[i];
+          const int c = j0 + i * tpr;  // the first of the lane group's 8 chunks
+          if (c < 512) ss_t[row][c >> 3] = sq[i];
         }
       }
       __syncthreads();
-      // Groups past the row's chunks hold zeros in the prologue kernel:
-      // adding them changes nothing, so only the written groups are summed.
-      const int ngroups = min(8, (tpr >> 6) * NCH);
-      tot = ss_g[row_live ? row : 0][0];
-      for (int g = 1; g < ngroups; ++g) tot = __fadd_rn(tot, ss_g[row_live ? row : 0][g]);
+      // Tree sums past the row's chunks are zeros in the other routes:
+      // adding them changes nothing, so the unwritten ones read as zero.
+      const int ntree = min(64, (tpr * NCH) >> 3);
+      tot = wave_sum_xor(lane < ntree ? ss_t[row_live ? row : 0][lane] : 0.0f);
     } else {
-      // The same butterflies and group sums on the producer's chunk sums,
-      // by every wavefront of the row on its own: no barrier, and the
-      // weight stream starts as early as in the kernel without the norm.
-      tot = wave_sum_xor(pv[0]);
-#pragma unroll
-      for (int g = 1; g < 8; ++g) tot = __fadd_rn(tot, wave_sum_xor(pv[g]));
+      // The same tree and butterfly on the producer's chunk sums, by every
+      // wavefront of the row on its own: no barrier, and the weight stream
+      // starts as early as in the kernel without the norm.
+      tot = wave_sum_xor(tree8_sum_lane(pv));
     }
     const float var = tot / static_cast<float>(p.K);
     const float rstd = 1.0f / sqrtf(__fadd_rn(var, p.eps));

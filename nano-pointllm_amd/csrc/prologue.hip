@@ -18,9 +18,12 @@
 //
 // One workgroup per row; each thread keeps REG chunks of 8 elements in
 // registers between the reductions (sum of squares, absmax) and the writes,
-// so x is read once.  The sum of squares is a binary32 sum in the kernel's
-// own order (per thread, then a wavefront butterfly, then across wavefronts);
-// every other step is an exactly rounded elementwise operation.
+// so x is read once.  The sum of squares is a binary32 sum: for K <= 4096
+// (one chunk per thread) in the order every RMSNorm route shares (per chunk,
+// pairwise over 8 consecutive chunks, then a wavefront butterfly over the 64
+// tree sums), for longer rows per thread, then a wavefront butterfly, then
+// across wavefronts; every other step is an exactly rounded elementwise
+// operation.
 #include <type_traits>
 
 #include "w8a8_internal.h"
@@ -81,6 +84,26 @@ __device__ inline float block_reduce(float v, float* red) {
 #pragma unroll
   for (int w = 1; w < kProThreads / 64; ++w) r = MAX ? fmaxf(r, red[w]) : r + red[w];
   return r;
+}
+
+// The RMSNorm sum of squares of a row of K <= 4096 (REG == 1): thread t
+// holds chunk t's sum, every thread gets the row's sum in the shared order
+// (tree8_sum over 8 consecutive chunks, then one butterfly over the 64 tree
+// sums).  red holds kProThreads / 8 floats.
+__device__ inline float block_tree_sum(float v, float* red) {
+  static_assert(kProThreads / 8 == 64, "one tree sum per lane");
+  v = tree8_sum(v);
+  const int tid = threadIdx.x;
+  __syncthreads();  // red[] may still be read from a previous reduction
+  if ((tid & 7) == 0) red[tid >> 3] = v;
+  __syncthreads();
+  return wave_sum_xor(red[tid & 63]);
+}
+
+template <int REG>
+__device__ inline float row_sumsq(float v, float* red) {
+  if constexpr (REG == 1) return block_tree_sum(v, red);
+  else return block_reduce<false>(v, red);
 }
 
 // TX: input / residual / smooth dtype (binary16 or bfloat16).  TW: RMSNorm
@@ -159,7 +182,7 @@ __device__ inline void prologue_vec(const PrologueParams& p, float* red) {
         if constexpr (kHalf) ss = __builtin_fmaf(v[c][j], v[c][j], ss);
         else ss = __fadd_rn(ss, __fmul_rn(v[c][j], v[c][j]));
       }
-    ss = block_reduce<false>(ss, red);
+    ss = row_sumsq<REG>(ss, red);
     const float var = ss / static_cast<float>(K);
     const float rs = 1.0f / sqrtf(__fadd_rn(var, p.eps));
 #pragma unroll
@@ -255,7 +278,7 @@ __device__ inline void prologue_vec(const PrologueParams& p, float* red) {
 template <typename TX, typename TW, int REG, bool VEC>
 __global__ __launch_bounds__(kProThreads) void prologue_quant_kernel(PrologueParams p) {
   using TY = TW;
-  __shared__ float red[kProThreads / 64];
+  __shared__ float red[kProThreads / 8];
   const int64_t row = blockIdx.x;
   const int tid = threadIdx.x;
   const int64_t K = p.K;
@@ -303,7 +326,7 @@ __global__ __launch_bounds__(kProThreads) void prologue_quant_kernel(ProloguePar
     for (int c = 0; c < REG; ++c)
 #pragma unroll
       for (int j = 0; j < 8; ++j) ss = __fadd_rn(ss, __fmul_rn(v[c][j], v[c][j]));
-    ss = block_reduce<false>(ss, red);
+    ss = row_sumsq<REG>(ss, red);
     const float var = ss / static_cast<float>(K);
     const float rr = 1.0f / sqrtf(__fadd_rn(var, p.eps));
     const TW* w = static_cast<const TW*>(p.norm_weight);

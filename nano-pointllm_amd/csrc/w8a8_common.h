@@ -384,6 +384,35 @@ __device__ inline float chunk_sumsq8(float v) {
   return s;
 }
 
+// The RMSNorm sum of squares of a row of K <= 4096 elements, in the order
+// every route takes (activation prologue, fused decode kernels, the chunk
+// sums of the residual-add epilogue): s_c per 8-column chunk (chunk_sumsq8),
+// then T_L = ((s_8L + s_8L+1) + (s_8L+2 + s_8L+3)) + ((s_8L+4 + s_8L+5) +
+// (s_8L+6 + s_8L+7)) for L < 64 (chunks past the row count 0), then the xor
+// butterfly of wave_sum_xor over T_0 .. T_63.
+//
+// tree8_sum: lanes 8j .. 8j+7 holding s_8L .. s_8L+7 all return T_L (quad
+// permutations for the first two levels, the half-row mirror for the third:
+// after two levels lanes 0-3 of a group hold the first half's sum and lanes
+// 4-7 the second's, and the mirror pairs each lane with the other half).
+// Every lane of the wavefront must be active.
+__device__ inline float tree8_sum(float v) {
+  constexpr int kQuadXor1 = 0xb1, kQuadXor2 = 0x4e, kRowHalfMirror = 0x141;
+  uint32_t u = __float_as_uint(v);
+  v = __fadd_rn(v, __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, kQuadXor1, 0xf, 0xf, false)));
+  u = __float_as_uint(v);
+  v = __fadd_rn(v, __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, kQuadXor2, 0xf, 0xf, false)));
+  u = __float_as_uint(v);
+  return __fadd_rn(v, __uint_as_float(__builtin_amdgcn_update_dpp(0u, u, kRowHalfMirror, 0xf,
+                                                                  0xf, false)));
+}
+
+// T_L of eight consecutive chunk sums held by one lane, the same tree.
+__device__ inline float tree8_sum_lane(const float (&s)[8]) {
+  return __fadd_rn(__fadd_rn(__fadd_rn(s[0], s[1]), __fadd_rn(s[2], s[3])),
+                   __fadd_rn(__fadd_rn(s[4], s[5]), __fadd_rn(s[6], s[7])));
+}
+
 // Packed-tile byte offset of element (r, k) of a [rows, K] operand.
 __host__ __device__ inline int64_t packed_offset(int64_t r, int64_t k, int64_t KB) {
   int64_t tile = (r >> 4) * KB + (k >> 6);
