@@ -5,7 +5,9 @@ Workload (one "step"): the W8A8 linear stack of one LLaMA-7B decode step at
 M decode rows (default 8) plus the fp16 LM head, as the full-stack config
 names it: 32 layers x {packed QKV [12288x4096], O [4096x4096], packed gate/up
 [22016x4096] with fused SiLU*mul -> [M, 11008], down [4096x11008]}, then the
-fp16 LM head [32003x4096] (torch F.linear: it is not a W8A8 linear).  Every
+fp16 LM head [32003x4096] (not a W8A8 linear: the reference's F.linear of the
+decode rows, here the hand-written dense GEMV of nanopointllm_amd.lm_head at
+M <= 16, binary32 accumulation).  Every
 layer has its own random-init weights (~N(0, 0.02), per-output int8, 6.48 GB
 packed in HBM) so nothing is served from the 256 MB Infinity Cache; RMSNorm
 and attention are stubbed by seeded fp16 activations, and the down projection
@@ -22,8 +24,9 @@ path on all host cores (rank 0, N=1 only), and `parity` reports the GPU
 outputs' max-abs / max-relative error against it.  `extra` carries
 per-projection decode GB/s at M=1,4,8, the prefill TOPS at M=560/768/1024
 (the quantize + GEMM call, the int8-in call with its packing pass, and the
-GEMM kernel alone), the stack without the LM head, and the whole-model step
-through the runner.
+GEMM kernel alone), the stack without the LM head, the LM head alone (the
+dense GEMV and torch's F.linear), and the whole-model step through the
+runner.
 
     python bench.py [--steps K] [--warmup W] [--m 8] [--no-extra] [--no-cpu]
 """
@@ -549,8 +552,8 @@ def decode_step_int8_mlp(layers, m: int, device) -> dict:
 
 
 def lm_head(m: int, device):
-    """The fp16 LM head [32003 x 4096] of config 4 and its input rows (torch
-    F.linear: the LM head is not a W8A8 linear), with its algorithmic bytes."""
+    """The fp16 LM head [32003 x 4096] of config 4 and its input rows (a
+    plain 16-bit linear, not a W8A8 one), with its algorithmic bytes."""
     import torch
 
     import workloads as W
@@ -561,6 +564,29 @@ def lm_head(m: int, device):
     xh = W.decode_activations(m, W.HIDDEN, seed=98).to(device)
     nbytes = W.VOCAB * W.HIDDEN * 2 + 2 * m * W.HIDDEN + 2 * m * W.VOCAB
     return lm, xh, nbytes
+
+
+def lm_head_alone(lm, xh, nbytes: int) -> dict:
+    """The decode LM head by itself: the dense GEMV against torch's F.linear
+    (the reference's op) on the same rows, in graphs that alternate the
+    weight with a second copy so that neither is served from the 256 MB
+    Infinity Cache (as in the decode step, where the layers' weights evict
+    it)."""
+    import torch
+
+    from nanopointllm_amd.lm_head import dense_gemv
+
+    lm2 = lm.clone()
+    out = {}
+    for name, fn in (("dense_gemv", dense_gemv), ("torch_F_linear", torch.nn.functional.linear)):
+        if name == "dense_gemv" and xh.shape[0] > 16:
+            continue
+        ms, gr = time_graph(lambda: (fn(xh, lm), fn(xh, lm2)), steps=20, warmup=3)
+        del gr
+        ms /= 2
+        out[name] = {"us": round(ms * 1e3, 2), "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    del lm2
+    return out
 
 
 def stack_without_lm_head(layers, m: int, device) -> dict:
@@ -803,6 +829,7 @@ def main() -> int:
     import torch
 
     from nanopointllm_amd import _lib
+    from nanopointllm_amd.lm_head import dense_gemv
     import workloads as W
 
     if not torch.cuda.is_available():
@@ -838,11 +865,13 @@ def main() -> int:
         return 0
 
     lm, xh, lm_bytes = lm_head(m, device)
+    # The decode LM head: the dense GEMV up to 16 rows, torch's GEMM beyond.
+    head = dense_gemv if m <= 16 else torch.nn.functional.linear
 
     def step():
         for layer in layers:
             layer.step()
-        torch.nn.functional.linear(xh, lm)
+        head(xh, lm)
 
     log("capturing step graph")
     ms_per_step, graph = time_graph(step, args.steps, args.warmup)
@@ -869,6 +898,8 @@ def main() -> int:
         extra["mixed_567_gateup_down_int8_chain"] = mixed_chain(layers, device)
         log("stack without the LM head")
         extra["stack_without_lm_head"] = stack_without_lm_head(layers, m, device)
+        log("LM head alone")
+        extra["lm_head"] = lm_head_alone(lm, xh, lm_bytes)
         log("decode step with the int8 MLP chain")
         extra["decode_step_int8_mlp_chain"] = decode_step_int8_mlp(layers, m, device)
         log("runner decode step (32 layers, fused norms, LM head)")
@@ -900,7 +931,9 @@ def main() -> int:
                    "m": m, "layers": args.layers,
                    "projections": {p.name: [p.n, p.k] for p in W.PROJECTIONS},
                    "lm_head": {"shape": [W.VOCAB, W.HIDDEN], "dtype": "fp16",
-                               "op": "torch F.linear (not a W8A8 linear)"},
+                               "op": ("dense_gemv: HIP fp16 GEMV, binary32 accumulation "
+                                      "(not a W8A8 linear)" if m <= 16 else
+                                      "torch F.linear (not a W8A8 linear)")},
                    "weights": "random-init ~N(0,0.02), per-output int8, packed",
                    "bytes_per_step": nbytes, "graph": True},
         "roofline": roofline,

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define W8A8_ABI_VERSION 6
+#define W8A8_ABI_VERSION 7
 
 typedef enum w8a8_dtype {
   W8A8_F32 = 0,
@@ -409,6 +409,27 @@ int w8a8_requantize_i32(const int32_t* acc, int64_t ld_acc, const int32_t* bias_
 int w8a8_dequant_i32_bf16(const int32_t* acc, int64_t ld_acc, const uint16_t* sa_bits,
                           const uint16_t* sw_bits, uint16_t* y, int64_t ldy, int64_t m,
                           int64_t n, hipStream_t stream);
+
+/*
+ * The LM head at decode batches: a plain 16-bit linear, y = x @ w^T (+ bias),
+ * which replaces _decode_linear_rows / _decode_staged_linear on lm_head
+ * (nanopointllm/llama/lightweight_runner.py:38-43, 96-99, 676-681; the
+ * reference's F.linear on the final-norm rows).  x [m, ldx], w [n, ldw]
+ * (nn.Linear's own row-major weight), bias [n] (nullable) and y [m, ldy] are
+ * all of `dtype` (W8A8_F16 or W8A8_BF16); products are accumulated in
+ * binary32 (per half of each 64-column step: 32 columns per matrix
+ * instruction, the steps of one of 16 column ranges in order; then the two
+ * halves, then the 16 ranges in order), the bias added, and the sum rounded
+ * once to `dtype`.  The order is the same for every row and batch size: the
+ * result is deterministic and a row's values do not depend on the other
+ * rows.  1 <= m <= 16, k % 8 == 0, k <= 8192, ldx and
+ * ldw multiples of 8 with x and w 16-byte aligned, m * ldx and 16 * ldw
+ * below 2^30; y must not overlap x, w or bias (W8A8_ERR_OVERLAP).  Larger
+ * batches belong to a GEMM (the reference's F.linear).
+ */
+int w8a8_dense_gemv(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                    void* y, int64_t ldy, int dtype, int64_t m, int64_t n, int64_t k,
+                    hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -3,6 +3,7 @@
 // alignment and workspace are checked here and reported as status codes; the
 // kernels live in quant.hip, gemv.hip and gemm.hip.
 #include <mutex>
+#include <utility>
 
 #include "w8a8_gfx950.h"
 #include "w8a8_internal.h"
@@ -791,6 +792,34 @@ int w8a8_dequant_i32_bf16(const int32_t* acc, int64_t ld_acc, const uint16_t* sa
   if (!aligned(acc, 4) || !aligned(sa_bits, 2) || !aligned(sw_bits, 2) || !aligned(y, 2))
     return W8A8_ERR_ALIGN;
   return status_of(launch_dequant_i32_bf16(acc, ld_acc, sa_bits, sw_bits, y, ldy, m, n, stream));
+}
+
+int w8a8_dense_gemv(const void* x, int64_t ldx, const void* w, int64_t ldw, const void* bias,
+                    void* y, int64_t ldy, int dtype, int64_t m, int64_t n, int64_t k,
+                    hipStream_t stream) {
+  if (!half_dtype(dtype)) return W8A8_ERR_DTYPE;
+  if (m < 0 || n < 0 || k < 0 || m > 16) return W8A8_ERR_SHAPE;
+  if (m == 0 || n == 0) return W8A8_OK;
+  if (k == 0 || k % 8 != 0 || k > dense_gemv_max_k()) return W8A8_ERR_SHAPE;
+  if (ldx < k || ldw < k || ldy < n || ldx % 8 != 0 || ldw % 8 != 0) return W8A8_ERR_SHAPE;
+  if (m * ldx * 2 >= (int64_t{1} << 31) || 16 * ldw * 2 >= (int64_t{1} << 31))
+    return W8A8_ERR_SHAPE;
+  if (x == nullptr || w == nullptr || y == nullptr) return W8A8_ERR_NULL;
+  if (!aligned(x, 16) || !aligned(w, 16) || !aligned(y, 2) || !aligned(bias, 2))
+    return W8A8_ERR_ALIGN;
+  // y is written while x, w and bias are read by other workgroups.
+  auto span = [](const void* p, int64_t rows, int64_t ld, int64_t cols) {
+    const uintptr_t b = reinterpret_cast<uintptr_t>(p);
+    return std::make_pair(b, b + static_cast<uintptr_t>(((rows - 1) * ld + cols) * 2));
+  };
+  auto meets = [](std::pair<uintptr_t, uintptr_t> a, std::pair<uintptr_t, uintptr_t> b) {
+    return a.first < b.second && b.first < a.second;
+  };
+  const auto ys = span(y, m, ldy, n);
+  if (meets(ys, span(x, m, ldx, k)) || meets(ys, span(w, n, ldw, k)) ||
+      (bias != nullptr && meets(ys, span(bias, 1, n, n))))
+    return W8A8_ERR_OVERLAP;
+  return status_of(launch_gemv_dense(x, ldx, w, ldw, bias, y, ldy, dtype, m, n, k, stream));
 }
 
 }  // extern "C"

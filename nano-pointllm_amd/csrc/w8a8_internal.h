@@ -168,4 +168,13 @@ hipError_t launch_gemv_fused_norm(const void* x, int x_dtype, int64_t ldx, const
                                   const LinearOperands& op, float* sx_out, hipStream_t st,
                                   const float* ss_in = nullptr, int64_t ld_ss_in = 0);
 
+// Dense 16-bit GEMV (gemv_dense.hip): y[M, ldy] = dtype(x[M, ldx] @ w[N, ldw]^T
+// (+ bias)) with binary32 accumulation, dtype kF16 or kBF16; 1 <= M <= 16,
+// K % 8 == 0, K <= dense_gemv_max_k(), 16-byte aligned x and w rows,
+// M * ldx * 2 < 2^31 and 16 * ldw * 2 < 2^31 (host-checked).
+int64_t dense_gemv_max_k();
+hipError_t launch_gemv_dense(const void* x, int64_t ldx, const void* w, int64_t ldw,
+                             const void* bias, void* y, int64_t ldy, int dtype, int64_t M,
+                             int64_t N, int64_t K, hipStream_t st);
+
 }  // namespace w8a8

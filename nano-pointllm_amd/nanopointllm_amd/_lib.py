@@ -13,7 +13,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libw8a8_gfx950.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 F32, F16, BF16, I32, I8 = 0, 1, 2, 3, 4
 EPI_I32, EPI_DEQUANT, EPI_SILU_MUL, EPI_SILU_MUL_Q8 = 0, 1, 2, 3
@@ -63,6 +63,7 @@ EXPORTED_SYMBOLS = (
     "w8a8_prologue_quant",
     "w8a8_requantize_i32",
     "w8a8_dequant_i32_bf16",
+    "w8a8_dense_gemv",
 )
 
 _lock = threading.Lock()
@@ -111,6 +112,8 @@ _SIGNATURES = {
                                    _vp, _i64, _i64, _vp, _i64, _vp, _vp, _i64, _vp]),
     "w8a8_requantize_i32": (_int, [_vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "w8a8_dequant_i32_bf16": (_int, [_vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "w8a8_dense_gemv": (_int, [_vp, _i64, _vp, _i64, _vp, _vp, _i64, _int, _i64, _i64, _i64,
+                               _vp]),
 }
 
 

@@ -36,7 +36,9 @@ sums instead of summing the rows in every workgroup
 After the last layer, its residual add and the final ``norm``
 (``LightweightRMSNorm``, lightweight_runner.py:609, 675) run as one launch of
 the activation prologue, the same kernel and formula as the in-layer norms,
-in front of the LM head.
+in front of the LM head, whose decode batches (at most 16 rows) run as the
+dense 16-bit GEMV of :mod:`nanopointllm_amd.lm_head` on the module's own
+weight.
 
 The stack is inference-only (no autograd).  Nothing on it synchronizes with
 the host or allocates outside torch's allocator, so a decode step can be
@@ -53,6 +55,7 @@ import torch.nn as nn
 
 from . import w8a8 as _w
 from .inject import inject_w8a8
+from .lm_head import DecodeLMHead
 from .linear import W8A8Linear, W8A8MLP, W8A8PackedQKV, _norm_eps
 
 AttentionCore = Callable[[torch.Tensor, torch.Tensor, torch.Tensor, int, Any], torch.Tensor]
@@ -179,7 +182,9 @@ class W8A8LlamaRunner(nn.Module):
         self.layers = nn.ModuleList([W8A8LlamaLayer(layer, i, attention_core)
                                      for i, layer in enumerate(model.layers)])
         self.norm = model.norm
-        self.lm_head = hf_model.lm_head
+        # Decode batches take the dense GEMV (lm_head.DecodeLMHead); the
+        # reference calls the module's F.linear (lightweight_runner.py:676-681).
+        self.lm_head = DecodeLMHead(hf_model.lm_head)
 
     @torch.no_grad()
     def forward(self, input_ids: torch.Tensor | None = None, *,

@@ -237,6 +237,51 @@ def test_residual_add_arguments_rejected_without_launch():
                                       None) == _lib.ERR_ALIGN
 
 
+def test_dense_gemv_arguments_rejected_without_launch():
+    lib = _lib.load()
+    x, w, y, b = (ctypes.c_void_p(a) for a in (0x1000, 0x100000, 0x4000000, 0x8000000))
+
+    def dg(x=x, ldx=64, w=w, ldw=64, bias=None, y=y, ldy=32, dtype=_lib.F16, m=8, n=32, k=64):
+        return lib.w8a8_dense_gemv(x, ldx, w, ldw, bias, y, ldy, dtype, m, n, k, None)
+    # 16-bit operands only; at most 16 rows; K a multiple of 8 up to 8192
+    assert dg(dtype=_lib.F32) == _lib.ERR_DTYPE
+    assert dg(dtype=_lib.I8) == _lib.ERR_DTYPE
+    assert dg(m=17) == _lib.ERR_SHAPE
+    assert dg(k=60, ldx=64, ldw=64) == _lib.ERR_SHAPE
+    assert dg(k=8200, ldx=8200, ldw=8200) == _lib.ERR_SHAPE
+    # leading dimensions: at least K (N for y), multiples of 8 for x and w
+    assert dg(ldx=56) == _lib.ERR_SHAPE
+    assert dg(ldw=68) == _lib.ERR_SHAPE
+    assert dg(ldy=16) == _lib.ERR_SHAPE
+    # null and misaligned operands
+    assert dg(w=None) == _lib.ERR_NULL
+    assert dg(x=ctypes.c_void_p(0x1008)) == _lib.ERR_ALIGN
+    assert dg(bias=ctypes.c_void_p(0x8000001)) == _lib.ERR_ALIGN
+    # y must not overlap x, w or the bias
+    assert dg(y=ctypes.c_void_p(0x1040)) == _lib.ERR_OVERLAP
+    assert dg(y=ctypes.c_void_p(0x100800)) == _lib.ERR_OVERLAP
+    assert dg(bias=ctypes.c_void_p(0x4000010)) == _lib.ERR_OVERLAP
+    # empty problems are valid no-ops
+    assert dg(m=0) == _lib.OK
+    assert dg(n=0) == _lib.OK
+
+
+def test_dense_gemv_host_checks():
+    import torch
+
+    from nanopointllm_amd import lm_head
+
+    x = torch.ones(2, 64, dtype=torch.float16)
+    w = torch.ones(32, 64, dtype=torch.float16)
+    assert not lm_head.dense_gemv_supported(x, w)  # CPU tensors
+    with pytest.raises(RuntimeError, match="only on the GPU"):
+        lm_head.dense_gemv(x, w)
+    head = lm_head.DecodeLMHead(torch.nn.Linear(64, 32, bias=False).half())
+    assert head.weight is head.linear.weight
+    with pytest.raises(RuntimeError, match="only on the GPU"):
+        head(x)
+
+
 def test_status_errors_map_to_python_exceptions():
     with pytest.raises(ValueError, match="workspace"):
         _lib.check(_lib.ERR_WORKSPACE, "w8a8_linear")

@@ -28,6 +28,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+from nanopointllm_amd.lm_head import dense_gemv
 from workloads import LlamaShaped
 
 pytestmark = pytest.mark.gpu
@@ -140,8 +141,12 @@ def test_runner_is_the_chain_of_its_primitives(cuda, tokens):
         r, xq, sx = w8a8.rmsnorm_quant(a, layer.post_attention_layernorm.weight, 1e-6, residual=x)
         x = r + layer.mlp.w8a8_mlp.forward_i8(xq, sx, out_dtype=torch.float16)
     norm = model.model.norm
-    expect = model.lm_head(w8a8.prologue_quant(x, norm_weight=norm.weight,
-                                               eps=norm.variance_epsilon, return_rows=True).rows)
+    rows = w8a8.prologue_quant(x, norm_weight=norm.weight, eps=norm.variance_epsilon,
+                               return_rows=True).rows
+    # The LM head: the module's weight, on the dense GEMV up to 16 rows and
+    # F.linear beyond.
+    assert runner.lm_head.linear is model.lm_head
+    expect = dense_gemv(rows, model.lm_head.weight) if tokens <= 16 else model.lm_head(rows)
     assert logits.shape == (1, tokens, 512)
     assert torch.equal(logits[0], expect)
 
@@ -175,31 +180,58 @@ def llama7b_layer(cuda):
                   seed=7)
 
 
+def _check_rows_across_paths(runner, x, step: int, singles: int) -> None:
+    """The final-norm rows of one batch, of chunks of `step` rows and of
+    single rows are bit-equal (every W8A8 kernel path); the logits of chunks
+    and single rows too (both on the dense GEMV), and the batch's (torch's
+    GEMM past 16 rows) within two output ulps of them."""
+    head = runner.lm_head
+    runner.lm_head = torch.nn.Identity()
+    try:
+        whole = runner(inputs_embeds=x)
+        chunks = torch.cat([runner(inputs_embeds=x[:, i:i + step])
+                            for i in range(0, x.shape[1], step)], dim=1)
+        assert torch.equal(whole, chunks)
+        ones = torch.cat([runner(inputs_embeds=x[:, i:i + 1]) for i in range(singles)], dim=1)
+        assert torch.equal(whole[:, :singles], ones)
+    finally:
+        runner.lm_head = head
+    w = head.linear.weight
+    logits = runner(inputs_embeds=x)
+    assert torch.equal(logits, head.linear(whole))
+    spans = range(0, x.shape[1], step)
+    chunk_logits = torch.cat([runner(inputs_embeds=x[:, i:i + step]) for i in spans], dim=1)
+    assert torch.equal(chunk_logits,
+                       torch.cat([dense_gemv(whole[:, i:i + step], w) for i in spans], dim=1))
+    one_logits = torch.cat([runner(inputs_embeds=x[:, i:i + 1]) for i in range(singles)], dim=1)
+    assert torch.equal(one_logits, chunk_logits[:, :singles])
+    # Two roundings of binary32 sums: within two output ulps plus the
+    # accumulation bound K * 2^-24 * sum |x w| of each.
+    ulp = 2.0 ** (torch.floor(torch.log2(logits.float().abs().clamp_min(2.0 ** -30)))
+                  - (10 if x.dtype == torch.float16 else 7))
+    mag = whole.float().abs() @ w.float().abs().t()
+    tol = 2 * ulp + 2 * w.shape[1] * 2.0 ** -24 * mag
+    assert ((chunk_logits.float() - logits.float()).abs() <= tol).all()
+
+
 def test_rows_give_the_same_bits_on_every_kernel_path(cuda, llama7b_layer):
     model = copy.deepcopy(llama7b_layer)
     runner = _runner(model, rowlocal_core)
     x = torch.randn(1, 96, 4096, generator=torch.Generator().manual_seed(3)).half().to(cuda)
     note("runner rows: prefill GEMM vs decode chunks of 8 vs single rows")
-    whole = runner(inputs_embeds=x)
-    chunks = torch.cat([runner(inputs_embeds=x[:, i:i + 8]) for i in range(0, 96, 8)], dim=1)
-    assert torch.equal(whole, chunks)
-    singles = torch.cat([runner(inputs_embeds=x[:, i:i + 1]) for i in range(0, 12)], dim=1)
-    assert torch.equal(whole[:, :12], singles)
+    _check_rows_across_paths(runner, x, 8, 12)
 
 def test_bf16_rows_give_the_same_bits_on_every_kernel_path(cuda):
     """As above for a bfloat16 model: one prefill batch (MFMA GEMM), decode
-    chunks of 8 and single rows (fused decode kernels) give the same bits."""
+    chunks of 8 and single rows (fused decode kernels) give the same bits up to
+    the LM head."""
     model = _model(cuda, hidden=4096, heads=32, kv_heads=32, inter=11008, vocab=256, layers=1,
                    seed=17, dtype=torch.bfloat16)
     runner = _runner(model, rowlocal_core)
     x = torch.randn(1, 80, 4096, generator=torch.Generator().manual_seed(4)).bfloat16().to(cuda)
     note("bf16 runner rows: prefill GEMM vs decode chunks of 8 vs single rows")
-    whole = runner(inputs_embeds=x)
-    assert whole.dtype == torch.bfloat16
-    chunks = torch.cat([runner(inputs_embeds=x[:, i:i + 8]) for i in range(0, 80, 8)], dim=1)
-    assert torch.equal(whole, chunks)
-    singles = torch.cat([runner(inputs_embeds=x[:, i:i + 1]) for i in range(0, 6)], dim=1)
-    assert torch.equal(whole[:, :6], singles)
+    assert runner(inputs_embeds=x[:, :2]).dtype == torch.bfloat16
+    _check_rows_across_paths(runner, x, 8, 6)
 
 
 @pytest.mark.parametrize("rows,dtype", [(1, torch.float16), (8, torch.float16),
