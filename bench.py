@@ -83,6 +83,11 @@ def parse_args():
                     help="only the start-up timeline of the fused gate/up decode kernel at --m "
                          "rows: 32 layers' launches in a graph on the timestamp build "
                          "(libw8a8_gfx950_timeline.so), per-workgroup phases of the last one")
+    ap.add_argument("--profile-lm-head", action="store_true",
+                    help="only the decode LM head (32003 x 4096 binary16, dense GEMV) at --m "
+                         "rows: two weight copies alternating, 10 times each, after the "
+                         "counter-calibration copy (the region rocprofv3 runs of the LM head "
+                         "measure)")
     ap.add_argument("--profile-runner", action="store_true",
                     help="only the whole-model decode step through W8A8LlamaRunner at --m rows "
                          "(32 LLaMA-7B-shaped layers, LM head), captured and replayed (the "
@@ -118,6 +123,31 @@ def profile_proj(device, name: str, m: int) -> dict:
     return {"projection": name, "m": m, "n": spec.n, "k": spec.k, "launches": 20,
             "host_ms_per_call": round(ms, 4),
             "algorithmic_bytes": W.algorithmic_bytes(m, spec.n, spec.k, silu=spec.silu)}
+
+
+def profile_lm_head(device, m: int) -> dict:
+    """The decode LM head on the dense GEMV: two copies of the weight
+    alternating (cold, as in the decode step), 20 launches, after a 256 MiB
+    copy that calibrates the traffic counters."""
+    import torch
+
+    from nanopointllm_amd.lm_head import dense_gemv
+
+    src = torch.empty(CALIBRATION_COPY_BYTES, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+    dst.copy_(src)
+    del src, dst
+    lm, xh, nbytes = lm_head(m, device)
+    lm2 = lm.clone()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(10):
+        dense_gemv(xh, lm)
+        dense_gemv(xh, lm2)
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / 20
+    return {"m": m, "shape": list(lm.shape), "launches": 20, "host_ms_per_call": round(ms, 4),
+            "algorithmic_bytes": nbytes}
 
 
 def profile_timeline(device, m: int) -> dict:
@@ -850,6 +880,9 @@ def main() -> int:
         return 0
     if args.profile_runner:
         print(json.dumps({"profile_runner": runner_decode_step(m, device)}))
+        return 0
+    if args.profile_lm_head:
+        print(json.dumps({"profile_lm_head": profile_lm_head(device, m)}))
         return 0
     log(f"building {args.layers} layers of packed W8A8 weights (M={m})")
     layers = [Layer(i, m, device) for i in range(args.layers)]
