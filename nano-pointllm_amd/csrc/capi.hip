@@ -167,15 +167,16 @@ LinearOperands make_ops(const int8_t* a, int64_t lda, const float* sx, const int
   return op;
 }
 
-// GEMV or GEMM for an m x n product.  The GEMV's time grows with M (each
-// weight fragment meets M activation rows) while the GEMM's barely does at
-// M <= 64; measured on MI355X with LLaMA-7B shapes at M = 17..64 (quantize
-// + product), the GEMV takes every projection up to M = 32 (QKV at M = 32 in
-// 15.8 against 19.8 us, gate/up 24.5 against 25.8) and those with N <= 12288
-// up to M = 64 (QKV at M = 48 / 64 18.7 / 20.6 against 20.9 / 21.1), while
-// the GEMM keeps gate/up past 32 rows (26.9 against 31.0 us at M = 48).
-inline bool use_gemv(int64_t m, int64_t n) {
-  return m <= kGemvMaxRows && (m <= 32 || n <= 12288);
+// GEMV or GEMM for an m x n x k product.  The GEMV's time grows with M
+// (each weight fragment meets M activation rows) while the GEMM's barely
+// does at M <= 64; measured on MI355X with LLaMA-7B shapes at M = 17..64
+// (quantize + product, graphs of 32 layers), the GEMV takes every projection
+// up to M = 32 (QKV at M = 32 in 15.8 against 19.8 us) and those with
+// N <= 12288 up to M = 64 (QKV at M = 48 / 64 16.6 / 17.5 against 20.9 /
+// 21.1), and with K <= 4096 (the 17-64-row kernel, x read in whole lines)
+// gate/up up to M = 64 too (24.6 / 25.8 against 26.5 / 27.2 us on the GEMM).
+inline bool use_gemv(int64_t m, int64_t n, int64_t k) {
+  return m <= kGemvMaxRows && (m <= 32 || n <= 12288 || k <= 4096);
 }
 
 // Runs the int8 product for activations already staged in `act` (row-major
@@ -183,7 +184,7 @@ inline bool use_gemv(int64_t m, int64_t n) {
 // kernels take the residual-add epilogue (op.res) themselves; the GEMM
 // writes its output first and the add runs over it.
 inline hipError_t run_product(const LinearOperands& op, hipStream_t st) {
-  if (use_gemv(op.M, op.N)) return launch_gemv(op, st);
+  if (use_gemv(op.M, op.N, op.K)) return launch_gemv(op, st);
   if (op.res == nullptr) return launch_gemm(op, st);
   LinearOperands plain = op;
   plain.res = nullptr;
@@ -246,7 +247,7 @@ inline void set_residual(LinearOperands& op, const ResidualAdd* ra) {
 inline hipError_t stage_i8(const int8_t* xq, int64_t ldq, int64_t m, int64_t n, int64_t k,
                            int8_t* act, const int8_t** a, int64_t* lda, hipStream_t st) {
   const int64_t kp = round_up(k, kTileK);
-  if (use_gemv(m, n)) {
+  if (use_gemv(m, n, k)) {
     if (k % kTileK == 0 && ldq % 16 == 0 && aligned(xq, 16)) {
       *a = xq;
       *lda = ldq;
@@ -295,7 +296,7 @@ int linear_impl(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
   float* sx = x_scale_out != nullptr ? x_scale_out : static_cast<float*>(workspace);
   int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
   const int64_t kp = round_up(k, kTileK);
-  const bool gemv = use_gemv(m, n);
+  const bool gemv = use_gemv(m, n, k);
   hipError_t e = launch_quant_rows(x, x_dtype, ldx, m, k, nullptr, 0, act, kp, kp, !gemv, sx,
                                    stream);
   if (e != hipSuccess) return status_of(e);
@@ -402,7 +403,7 @@ int rmsnorm_linear_impl(const void* x, int x_dtype, int64_t ldx, const void* res
   float* sx = x_scale_out != nullptr ? x_scale_out : static_cast<float*>(workspace);
   int8_t* act = static_cast<int8_t*>(workspace) + scale_region(m);
   const int64_t kp = round_up(k, kTileK);
-  const bool gemv = use_gemv(m, n);
+  const bool gemv = use_gemv(m, n, k);
   // The GEMV reads whole 64-column blocks: the prologue writes zeros in the
   // pad columns K..kp of its row-major rows.
   hipError_t e = launch_prologue_quant(x, x_dtype, ldx, residual, ld_residual, residual_out,

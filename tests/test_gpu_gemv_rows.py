@@ -51,9 +51,10 @@ def _rows_kernel(m: int, n: int, k: int) -> bool:
     return 16 < m <= 64 and k <= 4096
 
 
-def _uses_gemv(m: int, n: int) -> bool:
-    # The library's routing: the GEMV up to 32 rows, and up to 64 for N <= 12288.
-    return m <= 32 or (m <= 64 and n <= 12288)
+def _uses_gemv(m: int, n: int, k: int) -> bool:
+    # The library's routing: the GEMV up to 32 rows, and up to 64 for
+    # N <= 12288 or K <= 4096.
+    return m <= 32 or (m <= 64 and (n <= 12288 or k <= 4096))
 
 
 ROWS_SHAPES = [
@@ -64,7 +65,7 @@ ROWS_SHAPES = [
     (17, 12288, 4096), (24, 12288, 4096), (32, 12288, 4096), (33, 12288, 4096),
     (48, 12288, 4096), (64, 12288, 4096), (40, 12272, 1000), (32, 12290, 1000),
     (20, 9000, 130), (64, 8200, 72), (32, 4096, 4096), (64, 4096, 4000), (17, 1000, 64),
-    (63, 300, 4096), (32, 22016, 4096),
+    (63, 300, 4096), (32, 22016, 4096), (48, 22016, 4096), (64, 22016, 4096),
 ]
 OLD_SHAPES = [
     # gemv_kernel: K > 4096, three blocks per workgroup (MT = 2 and 4) and
@@ -77,7 +78,7 @@ OLD_SHAPES = [
 def test_gemv_rows_int32_and_dequant(cuda, m, n, k):
     from nanopointllm_amd import w8a8
 
-    assert _uses_gemv(m, n)
+    assert _uses_gemv(m, n, k)
     xq, wq, sx, sw, bias = _case(m, n, k, seed=m + n + k)
     note(f"gemv rows m={m} n={n} k={k} rows_kernel={_rows_kernel(m, n, k)}")
     xd, wp = xq.to(cuda), w8a8.pack_rows(wq.to(cuda))
@@ -98,12 +99,13 @@ def test_gemv_rows_int32_and_dequant(cuda, m, n, k):
 
 @pytest.mark.parametrize("m,inter,k", [(17, 11008, 4096), (24, 11008, 4096), (32, 11008, 4096),
                                       (48, 6000, 4096), (64, 4000, 2000), (29, 4500, 700),
+                                      (48, 11008, 4096), (64, 11008, 4096),
                                       (33, 2000, 1000), (20, 11008, 4160)])
 def test_gemv_rows_silu_mul_and_two_phase(cuda, m, inter, k):
     from nanopointllm_amd import _lib, w8a8
 
     n = 2 * inter
-    assert _uses_gemv(m, n)
+    assert _uses_gemv(m, n, k)
     xq, wq, sx, sw, _ = _case(m, n, k, seed=11 + k + m)
     note(f"gemv rows silu m={m} inter={inter} k={k} rows_kernel={_rows_kernel(m, n, k)}")
     wp = w8a8.pack_rows(wq.to(cuda), _lib.ROWS_INTERLEAVE_HALVES)

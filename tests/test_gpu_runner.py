@@ -241,7 +241,8 @@ def test_carried_residual_equals_the_per_layer_add(cuda, rows, dtype):
     """The runner leaves each layer's final residual add to the next layer's
     RMSNorm + QKV launch (forward_carry); two LLaMA-7B-size layers, so the
     second QKV takes the carried residual, on the fused decode kernel (rows 1
-    and 8) and the prologue + GEMM route (40 rows).  Bits equal to a stack of
+    and 8) and the activation prologue + 17-64-row GEMV route (40 rows).  Bits
+    equal to a stack of
     the reference-form layer.forward calls (lightweight_runner.py:552)."""
     model = _model(cuda, hidden=4096, heads=32, kv_heads=32, inter=11008, vocab=256, layers=2,
                    seed=11, dtype=dtype)
