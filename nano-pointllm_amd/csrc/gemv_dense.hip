@@ -87,10 +87,10 @@ __device__ inline f32x4 mfma_f32_16x16x32(u32x4 a, u32x4 b, f32x4 c) {
   }
 }
 
-// Each weight load covers whole 128-byte lines.  A K-step
-// is 64 columns; weight load q (rows 8q .. 8q+7 of the block) gives lane l
-// row 8q + l%8 at columns 64s + 32h + 8g .. +7 (h = (l/8)%2, g = l/16), so
-// the 8 lanes of a row read its 128 contiguous bytes.  That is the B operand
+// Each weight load covers whole 128-byte lines.  A K-step is 64 columns;
+// weight load q (rows 8q .. 8q+7 of the block) gives lane l row 8q + l%8 at
+// columns 64s + 32h + 8g .. +7 (h = (l/8)%2, g = l/16), so the 8 lanes of a
+// row read its 128 contiguous bytes.  That is the B operand
 // of an MFMA whose 16 columns are (row, half h) pairs; its A operand (lane l:
 // x row l%8, half (l%16)/8, columns 64s + 32 half + 8g .. +7) pairs x row m
 // and half h in its row m + 8h.  Output (m + 8h, r + 8h) of the 16 x 16 tile
