@@ -50,7 +50,7 @@ struct GemvParams {
   int N;
   int KB;
   int NB;
-  int G;  // gemv_rows_kernel: workgroups, min(NB, CUs)
+  int G;  // gemv_rows_kernel: workgroups, balanced_grid(NB)
 };
 
 __device__ inline i32x4 mfma_16x16x64(i32x4 a, i32x4 b, i32x4 c) {
@@ -261,8 +261,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
 }
 
 // Batched decode, 17..64 rows with K <= 4096 (gemv_rows_kernel): a
-// persistent grid of one 16-wavefront workgroup per CU (G = min(NB, CUs));
-// workgroup b takes 16-output blocks b, b + G, b + 2G, ...  Wavefront w owns
+// persistent grid of at most one 16-wavefront workgroup per CU
+// (G = balanced_grid(NB)); workgroup b takes 16-output blocks b, b + G,
+// b + 2G, ...  Wavefront w owns
 // the k-blocks [w kbw, (w + 1) kbw) of every block (kbw = ceil(KB / 16) <=
 // KBW = 4), so it loads the x fragments of its k-range (MT row tiles of 16
 // rows x 64 K, 16 bytes per lane) into registers once and keeps them for the
@@ -634,7 +635,7 @@ hipError_t launch_gemv(const LinearOperands& op, hipStream_t st) {
   p.KB = static_cast<int>(ceil_div(op.K, kTileK));
   const int64_t nblocks = ceil_div(op.N, kTileRows);
   p.NB = static_cast<int>(nblocks);
-  p.G = static_cast<int>(nblocks < cu_count() ? nblocks : cu_count());
+  p.G = balanced_grid(nblocks);  // gate/up at M = 17..64: 0.3-0.5 us faster
   if (op.M <= 0 || nblocks == 0) return hipSuccess;
   if (fused_gemv_i8_supported(op.M, op.N, op.K, op.lda, op.epi)) return launch_gemv_fused_i8(op, st);
   if (op.res == nullptr && gemv_rows_supported(op.M, op.N, op.K, op.lda, op.epi)) {

@@ -861,6 +861,17 @@ int cu_count() {
   return n;
 }
 
+// Persistent workgroups for nb blocks: one per CU when there are no more
+// blocks than CUs, else as few as keep the per-workgroup block count at its
+// minimum, ceil(nb / CUs), so nearly every workgroup streams the same bytes
+// and none runs a last block alone (LLaMA-7B gate/up, 1376 blocks: 230
+// workgroups of 6 blocks instead of 96 of 6 and 160 of 5; 16.3 / 16.7 / 17.0
+// against 16.6 / 16.8 / 17.2 us at M = 1 / 4 / 8, graphs of 32 layers).
+int balanced_grid(int64_t nb) {
+  const int64_t cus = cu_count();
+  return static_cast<int>(nb <= cus ? nb : ceil_div(nb, ceil_div(nb, cus)));
+}
+
 // Decode shapes: up to 8 rows of 16-bit activations, K <= 12288 and at most
 // 64 output blocks per workgroup (N <= 1024 * CUs).  Each CU fetches and
 // quantizes all M x K activations (the quantization itself takes 0.8 us at
@@ -924,7 +935,7 @@ hipError_t launch_gemv_fused(const void* x, int x_dtype, int64_t ldx, const Line
   p.K = static_cast<int>(op.K);
   p.KB = static_cast<int>(ceil_div(op.K, kTileK));
   p.NB = static_cast<int>(ceil_div(op.N, kTileRows));
-  p.G = static_cast<int>(p.NB < cu_count() ? p.NB : cu_count());
+  p.G = balanced_grid(p.NB);
   if (p.NB == 0 || p.M == 0) return hipSuccess;
   if (x_dtype == kF16) return dispatch_f<__half>(p, op.epi, op.y_dtype, op.h_dtype, st);
   if (x_dtype == kBF16) return dispatch_f<__hip_bfloat16>(p, op.epi, op.y_dtype, op.h_dtype, st);
@@ -998,7 +1009,7 @@ hipError_t launch_gemv_fused_norm(const void* x, int x_dtype, int64_t ldx, const
   p.K = static_cast<int>(op.K);
   p.KB = static_cast<int>(ceil_div(op.K, kTileK));
   p.NB = static_cast<int>(ceil_div(op.N, kTileRows));
-  p.G = static_cast<int>(p.NB < cu_count() ? p.NB : cu_count());
+  p.G = balanced_grid(p.NB);
   if (p.NB == 0 || p.M == 0) return hipSuccess;
   if (x_dtype == kF16) return dispatch_norm_f<__half>(p, op.epi, op.y_dtype, op.h_dtype, st);
   if (x_dtype == kBF16)
@@ -1057,7 +1068,7 @@ hipError_t launch_gemv_fused_i8(const LinearOperands& op, hipStream_t st) {
   p.K = static_cast<int>(op.K);
   p.KB = static_cast<int>(ceil_div(op.K, kTileK));
   p.NB = static_cast<int>(ceil_div(op.N, kTileRows));
-  p.G = static_cast<int>(p.NB < cu_count() ? p.NB : cu_count());
+  p.G = balanced_grid(p.NB);
   if (p.NB == 0 || p.M == 0) return hipSuccess;
   return dispatch_f<int8_t>(p, op.epi, op.y_dtype, op.h_dtype, st);
 }

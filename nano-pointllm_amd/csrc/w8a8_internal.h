@@ -144,6 +144,9 @@ constexpr int64_t kGemvMaxRows = 64;
 // N <= 1024 * CUs, and enough weight bytes per CU to hide the quantization.
 // Compute units of the current device.
 int cu_count();
+// Persistent workgroups for nb output blocks: nb up to the CU count, else the
+// fewest that keep every workgroup at ceil(nb / CUs) blocks or one less.
+int balanced_grid(int64_t nb);
 bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
                           int64_t K);
 // The fused kernel's weight stream on int8 activations (op.a row-major as for
