@@ -188,7 +188,9 @@ def profile_timeline(device, m: int) -> dict:
     torch.cuda.synchronize()
     cus = torch.cuda.get_device_properties(device).multi_processor_count
     nb = -(-spec.n // 16)
-    groups = min(nb, cus)
+    # The library's persistent grid (balanced_grid): every workgroup holds
+    # ceil(nb / CUs) blocks or one less.
+    groups = nb if nb <= cus else -(-nb // -(-nb // cus))
     buf = (ctypes.c_ulonglong * (groups * 16))()
     if lib.w8a8_timeline_read(ctypes.addressof(buf), groups) != 0:
         raise RuntimeError("w8a8_timeline_read failed")
