@@ -58,7 +58,7 @@ typedef enum w8a8_status {
 } w8a8_status;
 
 /* Bytes of the static device scratch of w8a8_linear_noalloc (per GPU). */
-#define W8A8_NOALLOC_SCRATCH_BYTES (64 << 20)
+#define W8A8_NOALLOC_SCRATCH_BYTES (16 << 20)
 
 typedef enum w8a8_epilogue {
   /* y[m, n] = int32 accumulator */
@@ -202,7 +202,8 @@ int w8a8_linear(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
  * no scratch; every other shape stages its quantized activations in a static
  * device array of W8A8_NOALLOC_SCRATCH_BYTES per GPU, and a problem with
  * w8a8_workspace_bytes(m, k) above that returns W8A8_ERR_TOO_LARGE before any
- * launch.  All calls on one GPU share that array, so calls that overlap on
+ * launch (16 MiB: every LLaMA-7B projection up to M = 1024, and up to 2048
+ * rows at K = 4096; the array is reserved on every GPU the library loads on).  All calls on one GPU share that array, so calls that overlap on
  * one GPU (concurrent streams, or host threads) race: serialize them, e.g. on
  * one stream.  Arguments, results and errors are otherwise w8a8_linear's.
  */

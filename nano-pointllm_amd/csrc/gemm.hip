@@ -1,4 +1,4 @@
-// Prefill-regime W8A8 GEMM (M > 64, or M > 32 with N > 12288):
+// Prefill-regime W8A8 GEMM (M > 64, or M > 32 with N > 12288 and K > 4096):
 // y = epi(xq @ wq^T) with int8 MFMA.
 //
 // Replaces the prefill/mixed projections (llama/paged_attention.py:1349-1352,

@@ -278,10 +278,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(GemvParams p) {
 // 64 in 10.8 / 11.9 / 16.6 us against 11.0 / 12.4 / 17.0, gate/up + SiLU*mul
 // at M = 17 / 32 in 17.6 / 19.0 against 18.1 / 21.4, O at M = 32 / 64 in
 // 7.4 / 10.7 against 7.9 / 12.0, and gate/up at M = 48 / 64 in 22.9 / 24.8
-// against 26.2 / 27.3 on the GEMM after a packing pass.  With the
-// quantization in front (graphs of 32 layers, 16-bit x) the GEMM keeps
-// gate/up past 32 rows: the quantization writes its packed tiles directly
-// (M = 64: 28.4 against 29.1 us with this kernel).
+// against 26.2 / 27.3 on the GEMM after a packing pass (x in fragment
+// loads; with x in whole lines and the quantization in front, gate/up at
+// M = 48 / 64 takes 24.2 / 25.4 us here against 26.5 / 27.2 on the GEMM).
 constexpr int kRowsWaves = 16;
 constexpr int kRowsThreads = kRowsWaves * 64;
 constexpr int kRowsMaxBlocks = 64;  // blocks per workgroup: N <= 1024 * CUs

@@ -24,7 +24,7 @@ OK = 0
 ERR_NULL, ERR_SHAPE, ERR_DTYPE, ERR_ALIGN, ERR_WORKSPACE, ERR_HIP = -1, -2, -3, -4, -5, -6
 ERR_TOO_LARGE = -7
 ERR_OVERLAP = -8
-NOALLOC_SCRATCH_BYTES = 64 << 20
+NOALLOC_SCRATCH_BYTES = 16 << 20
 
 # Names of the GEMM tiles w8a8_gemm_tile_config returns, by code.
 GEMM_TILE_NAMES = ("tiny-deep", "small-deep", "big-deep", "big", "w192", "w224", "w256",
