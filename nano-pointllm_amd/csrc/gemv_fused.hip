@@ -26,6 +26,9 @@
 // Quantizing x once per CU costs M*K*~10 VALU ops per CU; for decode shapes
 // that hides behind the weight loads already in flight, and it saves the
 // separate quantization launch and its round trip through memory.
+// gemv_split_kernel (below) serves the shapes with one output block per CU
+// (o_proj, down): there half the wavefronts stream the block's weights from
+// entry while the other half quantize one row each.
 #include <atomic>
 #include <type_traits>
 
@@ -138,7 +141,8 @@ typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
 
 // Sums the per-wave partials of output block nb and writes its outputs.
 // `ops` holds the block's 16 weight scales followed by its 16 biases.
-template <int EPI, typename TY, typename TH, bool RES>
+// NW: wavefronts whose partials red[0 .. NW-1] hold.
+template <int EPI, typename TY, typename TH, bool RES, int NW = kFusedWaves>
 __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
                                 const float* row_s, int64_t nb, int tid, const float* ops,
                                 const TY* res_pre) {
@@ -156,7 +160,7 @@ __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
       if (ok) {
         int32_t s = 0;
 #pragma unroll
-        for (int w = 0; w < kFusedWaves; ++w) s += red[w][tid];
+        for (int w = 0; w < NW; ++w) s += red[w][tid];
         const int r = tid & 15;
         const TY rv = res_pre != nullptr ? *res_pre
                                          : static_cast<const TY*>(p.add_res)[m * p.ld_add_res + n];
@@ -177,7 +181,7 @@ __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
       if (m < M && n < p.N) {
         int32_t s = 0;
 #pragma unroll
-        for (int w = 0; w < kFusedWaves; ++w) s += red[w][tid];
+        for (int w = 0; w < NW; ++w) s += red[w][tid];
         TY* y = static_cast<TY*>(p.y) + static_cast<int64_t>(m) * p.ldy + n;
         if constexpr (EPI == kEpiI32) {
           *y = s;
@@ -201,7 +205,7 @@ __device__ inline void epilogue(const FusedParams& p, const int32_t (*red)[256],
         const int base = m * 16 + 2 * cc;
         int32_t sg = 0, su = 0;
 #pragma unroll
-        for (int w = 0; w < kFusedWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
           sg += red[w][base];
           su += red[w][base + 1];
         }
@@ -746,8 +750,179 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
 #endif
 }
 
+// One 16-output block per workgroup (NB <= CUs), M <= 8, K <= 4096, 16-bit
+// x, the dequant epilogue (o_proj at decode): the wavefronts split into two
+// groups.  Wavefronts 8-15 issue all of the block's weight loads at entry
+// (8 k-blocks each; they do not depend on x); wavefronts 0-7 fetch row
+// `wave` of x, its absmax and scale, and quantize it into the A fragments in
+// LDS.  A wavefront's loads retire in order, so a row never waits behind
+// weight loads, and the weights stream from the first cycle instead of
+// after the quantization (the kernel above issues its first weight step
+// once x has arrived, and every wavefront quantizes a share of all rows).
+// After one barrier the weight wavefronts run their MFMAs and hand their
+// partials to wavefronts 0-3 for the epilogue.
+// CAP: k-blocks per weight wavefront, which is also the number of 16-byte x
+// chunks per lane of a row wavefront (K <= CAP * 8 * 64).
+constexpr int kSplitXWaves = kFusedMaxRows;
+constexpr int kSplitWWaves = kFusedWaves - kSplitXWaves;
+constexpr int kSplitCapSmall = 8;   // K <= 4096
+constexpr int kSplitCapLarge = 22;  // K <= 11264
+
+template <int EPI, typename TX, typename TY, typename TH, bool RES, int CAP>
+__global__ __launch_bounds__(kFusedThreads) void gemv_split_kernel(FusedParams p) {
+  static_assert(EPI == kEpiDequant && !std::is_same<TX, int8_t>::value, "o_proj shape");
+  constexpr int kSplitMaxKB = CAP * kSplitWWaves;
+  // A fragments: [kb][g][row < 8][16 bytes]
+  __shared__ __attribute__((aligned(16))) int8_t a_lds[kSplitMaxKB * 512];
+  __shared__ int32_t red[kSplitWWaves][256];
+  __shared__ float row_s[kFusedMaxRows];
+  __shared__ float ops_lds[32];  // the block's 16 weight scales, then 16 biases
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int KB = p.KB;
+  const int M = p.M;
+  const int64_t nb = blockIdx.x;
+  const bool loader = wave >= kSplitXWaves;
+
+  // ------------------------------------------- weight wavefronts: issue all
+  // Wavefront ww takes k-blocks [kb0, kb1); the descriptor's range ends at
+  // kb1, so its loads past the range read zeros without a memory access.
+  const int ww = wave - kSplitXWaves;
+  const int kbw = (KB + kSplitWWaves - 1) / kSplitWWaves;
+  const int kb0 = loader ? min(ww * kbw, KB) : 0;
+  const int kb1 = loader ? min(kb0 + kbw, KB) : 0;
+  // One register array serves both roles (weights, or the row's chunks),
+  // so the kernel needs CAP x 4 of them, not twice that.
+  u32x4 buf[CAP];
+  if (loader) {
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<i32x4*>(p.w + nb * KB * 64), 0,
+        __builtin_amdgcn_readfirstlane(kb1 * kBlockBytes), kBufferWord3);
+#pragma unroll
+    for (int i = 0; i < CAP; ++i) {
+      buf[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                             rsrc, (kb0 + i) * kBlockBytes + lane * 16, 0,
+                                             kCacheNT));
+    }
+  }
+
+  // ---------------------------------------- row wavefronts: quantize row
+  [[maybe_unused]] TY res0{};
+  const int row = wave;
+  const bool row_live = !loader && row < M;
+  const int K = p.K;
+  u32x4(&raw)[CAP] = buf;
+  // The epilogue operands: wavefront 0 (row 0 is always live) holds the
+  // block's scales and biases for lanes 0-15, wavefronts 0-3 the residual
+  // element of their output (a wavefront w >= M has no output row:
+  // 4 w >= M).  They are loaded behind x, unconditionally from clamped
+  // addresses: with every load of the wavefront issued on one path, the
+  // quantization waits for x only (a conditional load here would make the
+  // compiler wait for all of them).
+  float op_s = 0.0f, op_b = 0.0f;
+  if (row_live) {
+    // The row's K elements; chunks past K read zeros (zero int8 columns up
+    // to the k-block end).
+    const __amdgpu_buffer_rsrc_t xrsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(static_cast<const uint16_t*>(p.x) + row * p.ldx), 0,
+        __builtin_amdgcn_readfirstlane(K * 2), kBufferWord3);
+#pragma unroll
+    for (int i = 0; i < CAP; ++i) {
+      raw[i] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, (lane + 64 * i) * 16, 0, 0));
+    }
+    const int64_t n = nb * 16 + (tid & 15);
+    const int64_t nc = min(n, static_cast<int64_t>(p.N) - 1);
+    if constexpr (RES) {
+      const int m = min(tid >> 4, M - 1);
+      res0 = static_cast<const TY*>(p.add_res)[m * p.ld_add_res + nc];
+    }
+    op_s = p.sw[nc];
+    // Without a bias the epilogue ignores op_b (a select here would wait
+    // for the load).
+    op_b = (p.bias != nullptr ? p.bias : p.sw)[nc];
+    u16x2 am2 = {0, 0};
+#pragma unroll
+    for (int i = 0; i < CAP; ++i) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        am2 = __builtin_elementwise_max(am2, __builtin_bit_cast(u16x2, raw[i][q] & 0x7fff7fffu));
+    }
+    const uint32_t am =
+        wave_max_u32(max(static_cast<uint32_t>(am2[0]), static_cast<uint32_t>(am2[1])));
+    const float s = scale_from_absmax(bits_to_f32<TX>(am));
+    const float r = 1.0f / s;
+    if (lane == 0) {
+      row_s[row] = s;
+      if (blockIdx.x == 0 && p.sx_out != nullptr) p.sx_out[row] = s;
+    }
+    const int nchunk = KB * 8;
+#pragma unroll
+    for (int i = 0; i < CAP; ++i) {
+      const int c = lane + 64 * i;
+      if (c < nchunk) {
+        float xv[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          xv[2 * q] = bits_to_f32<TX>(raw[i][q] & 0xffffu);
+          xv[2 * q + 1] = bits_to_f32<TX>(raw[i][q] >> 16);
+        }
+        const int k = c * 8;
+        const int off = (((k >> 6) * 4 + ((k & 63) >> 4)) * kFusedMaxRows + row) * 16 + (k & 15);
+        *reinterpret_cast<u32x2*>(a_lds + off) = quant8_dyn(xv, s, r);
+      }
+    }
+  }
+  if (tid < 16) {
+    ops_lds[tid] = op_s;
+    ops_lds[16 + tid] = op_b;
+  }
+  __syncthreads();
+
+  // ------------------------------------------------ products and epilogue
+  if (loader) {
+    const int li = lane & 15;
+    const int lg = lane >> 4;
+    const bool a_live = li < M;
+    const int a_off = (lg * kFusedMaxRows + li) * 16;
+    i32x4 acc = i32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int i = 0; i < CAP; ++i) {
+      const int kb = kb0 + i;
+      if (kb < kb1) {
+        const i32x4 a = a_live ? *reinterpret_cast<const i32x4*>(a_lds + kb * 512 + a_off)
+                               : i32x4{0, 0, 0, 0};
+        acc = mfma_16x16x64(a, __builtin_bit_cast(i32x4, buf[i]), acc);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[ww][(4 * lg + q) * 16 + li] = acc[q];
+  }
+  __syncthreads();
+  epilogue<EPI, TY, TH, RES, kSplitWWaves>(p, red, row_s, nb, tid, ops_lds, &res0);
+}
+
+// The o_proj / down shapes gemv_split_kernel takes.
+bool split_shape(int64_t M, int64_t NB, int64_t KB) {
+  return M >= 1 && M <= kFusedMaxRows && KB >= 1 && KB <= kSplitCapLarge * kSplitWWaves &&
+         NB <= cu_count();
+}
+
 template <int EPI, typename TX, typename TY, typename TH, bool RES = false>
 hipError_t launch_f(const FusedParams& p, hipStream_t st) {
+  if constexpr (EPI == kEpiDequant && !std::is_same<TX, int8_t>::value) {
+    if (split_shape(p.M, p.NB, p.KB)) {
+      if (p.KB <= kSplitCapSmall * kSplitWWaves)
+        hipLaunchKernelGGL((gemv_split_kernel<EPI, TX, TY, TH, RES, kSplitCapSmall>),
+                           dim3(p.NB), dim3(kFusedThreads), 0, st, p);
+      else
+        hipLaunchKernelGGL((gemv_split_kernel<EPI, TX, TY, TH, RES, kSplitCapLarge>),
+                           dim3(p.NB), dim3(kFusedThreads), 0, st, p);
+      return hipGetLastError();
+    }
+  }
   // x chunks per thread: rows spread over 1024 / mpad(M) threads each.
   const int mpad = p.M <= 1 ? 1 : (p.M <= 2 ? 2 : (p.M <= 4 ? 4 : (p.M <= 8 ? 8 : 16)));
   const int per_thread = static_cast<int>(ceil_div(static_cast<int64_t>(p.KB) * 8,
@@ -885,8 +1060,14 @@ int balanced_grid(int64_t nb) {
 // fused, O 4-7% faster than quantize + GEMV, down within 1%).  With 9-16 rows
 // the quantize + GEMV route pays more per row, and 2 bytes per element
 // suffice (packed QKV at M = 13-16: 12-17% faster fused).
+// The dequant epilogue at one block per CU (N <= 16 * CUs, K <= 11264, the
+// o_proj / down shapes) takes gemv_split_kernel at any M <= 8 instead: its
+// weights stream from the first cycle while half the wavefronts quantize,
+// so the CU's share of the weights no longer has to cover the quantization
+// (graphs of 32 layers at M = 1 / 4 / 8: O 5.3 / 5.3 / 5.9 against
+// 6.6 / 7.2 / 8.1 us, down 9.9 / 10.5 / 11.4 against 11.0 / 13.4 / 14.3 us).
 bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
-                          int64_t K) {
+                          int64_t K, int epi) {
   if (!((x_dtype == kF16 || x_dtype == kBF16) && M >= 1 && M <= kFusedMaxRows16 && K >= 8 &&
         K % 8 == 0 &&
         ceil_div(K, kTileK) <= (M <= kFusedMaxRows ? kFusedMaxKB : kFusedMaxKB16) &&
@@ -894,6 +1075,7 @@ bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, in
         (reinterpret_cast<uintptr_t>(x) & 15u) == 0))
     return false;
   const int64_t nb = ceil_div(N, kTileRows);
+  if (epi == kEpiDequant && split_shape(M, nb, ceil_div(K, kTileK))) return true;
   const int64_t g = nb < cu_count() ? nb : cu_count();
   const int64_t blocks_per_cu = ceil_div(nb, g);
   const int64_t weight_bytes_per_cu = blocks_per_cu * kTileRows * ceil_div(K, kTileK) * kTileK;

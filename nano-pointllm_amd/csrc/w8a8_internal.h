@@ -147,8 +147,10 @@ int cu_count();
 // Persistent workgroups for nb output blocks: nb up to the CU count, else the
 // fewest that keep every workgroup at ceil(nb / CUs) blocks or one less.
 int balanced_grid(int64_t nb);
+// epi: the epilogue (kEpiDequant also admits the o_proj shapes of the
+// split kernel), or -1.
 bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
-                          int64_t K);
+                          int64_t K, int epi = -1);
 // The fused kernel's weight stream on int8 activations (op.a row-major as for
 // the GEMV, op.sx per-row scales); decode shapes only.
 bool fused_gemv_i8_supported(int64_t M, int64_t N, int64_t K, int64_t lda, int epi);

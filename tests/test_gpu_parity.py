@@ -461,12 +461,61 @@ def test_fused_decode_exact_ties(cuda, m):
     np.testing.assert_array_equal(acc.cpu().numpy(), O.int32_matmul_f64(xq, qw))
 
 
-def test_fused_path_not_taken_for_small_shapes(cuda):
-    """O-sized projections at M = 8 and 12 and tiny ones go through
-    quantization + GEMV (they need a workspace) and give the same results."""
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (4096, 11008), (16, 11264), (1000, 4104),
+                                 (4095, 5000), (40, 64), (16, 8)])
+def test_split_decode_path(cuda, m, n, k):
+    """At most one 16-output block per CU (N <= 16 * CUs), M <= 8, K <= 11264,
+    the dequant epilogue: the workspace-free kernel whose wavefronts split
+    into row quantizers and weight loaders (o_proj and down at decode).
+    Outputs with a bias, row scales, and the binary32 output, against the
+    oracle; K = 4104 and 5000 are the first k-blocks past the short-row
+    variant, 11264 the largest K it takes, N = 16 one block."""
     from nanopointllm_amd import _lib, w8a8
 
-    for m, n, k in [(8, 4096, 4096), (12, 4096, 4096), (8, 40, 64), (8, 16, 8)]:
+    g = torch.Generator().manual_seed(m * 100 + k)
+    x = torch.randn(m, k, generator=g) * 2.5
+    x[:, :: max(1, k // 5)] *= 40
+    x = x.to(torch.float16)
+    _, qw, sw = weight_q(n, k, seed=n + k)
+    bias = np.linspace(-2, 2, n).astype(np.float32)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    swt, bt, xc = torch.from_numpy(sw).to(cuda), torch.from_numpy(bias).to(cuda), x.to(cuda)
+    note(f"split decode m={m} n={n} k={k}")
+    rc, y, sx = _linear_without_workspace(xc, wp, swt, bt, n, _lib.EPI_DEQUANT, torch.float16)
+    assert rc == 0, _lib.load().w8a8_status_string(rc)
+    exp, _, _, esx = O.w8a8_linear_dynamic(x.float().numpy(), qw, sw, bias)
+    np.testing.assert_array_equal(sx.cpu().numpy(), esx[:, 0])
+    np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+    rc, y32, _ = _linear_without_workspace(xc, wp, swt, bt, n, _lib.EPI_DEQUANT, torch.float32)
+    assert rc == 0
+    np.testing.assert_array_equal(y32.cpu().numpy(), exp)
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 4096, 4096), (3, 4096, 11008), (6, 700, 2000)])
+def test_split_decode_path_bf16(cuda, m, n, k):
+    from nanopointllm_amd import w8a8
+
+    g = torch.Generator().manual_seed(m + k)
+    x = (torch.randn(m, k, generator=g) * 3).to(torch.bfloat16)
+    _, qw, sw = weight_q(n, k, seed=k)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    note(f"split decode bf16 m={m} n={n} k={k}")
+    y = w8a8.linear_dynamic(x.to(cuda), wp, torch.from_numpy(sw).to(cuda), None, n)
+    exp, _, _, _ = O.w8a8_linear_dynamic(x.float().numpy(), qw, sw)
+    assert y.dtype == torch.bfloat16
+    assert torch.equal(y.cpu(), torch.from_numpy(exp).to(torch.bfloat16))
+
+
+def test_fused_path_not_taken_for_small_shapes(cuda):
+    """Projections that neither fused kernel takes on a 256-CU MI355X (12
+    rows of a 4096 x 4096 weight, K = 12288 beyond the split kernel's rows,
+    257 blocks of short rows) and the int32 epilogue of the split shapes go
+    through quantization + GEMV (they need a workspace) and give the same
+    results."""
+    from nanopointllm_amd import _lib, w8a8
+
+    for m, n, k in [(12, 4096, 4096), (8, 4096, 12288), (8, 4112, 1024)]:
         _, qw, sw = weight_q(n, k, seed=n + k)
         wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
         x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.float16)
@@ -477,6 +526,14 @@ def test_fused_path_not_taken_for_small_shapes(cuda):
         y = w8a8.linear_dynamic(x.to(cuda), wp, torch.from_numpy(sw).to(cuda), None, n)
         exp, _, _, _ = O.w8a8_linear_dynamic(x.float().numpy(), qw, sw)
         np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+    m, n, k = 8, 4096, 4096
+    _, qw, sw = weight_q(n, k, seed=n + k)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.float16)
+    note("unfused int32 epilogue m=8 n=4096 k=4096")
+    rc, _, _ = _linear_without_workspace(x.to(cuda), wp, torch.from_numpy(sw).to(cuda), None, n,
+                                         _lib.EPI_I32, torch.int32)
+    assert rc == _lib.ERR_WORKSPACE
 
 
 def test_fused_path_strided_rows_and_fallbacks(cuda):
