@@ -283,7 +283,7 @@ int linear_impl(const void* x, int x_dtype, int64_t ldx, const int8_t* w_packed,
   if (!aligned(x, static_cast<uintptr_t>(elem_size(x_dtype)))) return W8A8_ERR_ALIGN;
   if (x_scale_out != nullptr && !aligned(x_scale_out, 4)) return W8A8_ERR_ALIGN;
   if (k > 0 && epilogue <= W8A8_EPI_SILU_MUL_Q8 &&
-      fused_gemv_supported(x, x_dtype, ldx, m, n, k, epilogue)) {
+      fused_gemv_supported(x, x_dtype, ldx, m, n, k, epilogue, ra != nullptr)) {
     // Decode: quantization fused into the GEMV, no workspace.
     LinearOperands op = make_ops(nullptr, 0, nullptr, w_packed, w_scale, bias, epilogue, y,
                                  y_dtype, ldy, y_scale, inter_dtype, m, n, k);

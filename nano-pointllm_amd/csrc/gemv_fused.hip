@@ -750,12 +750,12 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_fused_kernel(FusedParams p
 #endif
 }
 
-// One 16-output block per workgroup (NB <= CUs), M <= 8, K <= 4096, 16-bit
-// x, the dequant epilogue (o_proj at decode): the wavefronts split into two
+// One 16-output block per workgroup (NB <= CUs), 16-bit x, the dequant
+// epilogue (o_proj and down at decode): the wavefronts split into two
 // groups.  Wavefronts 8-15 issue all of the block's weight loads at entry
-// (8 k-blocks each; they do not depend on x); wavefronts 0-7 fetch row
-// `wave` of x, its absmax and scale, and quantize it into the A fragments in
-// LDS.  A wavefront's loads retire in order, so a row never waits behind
+// (CAP k-blocks each; they do not depend on x); wavefronts 0-7 fetch row
+// `wave` of x (and row `wave` + 8 with ROWS = 16), its absmax and scale, and
+// quantize it into the A fragments in LDS.  A wavefront's loads retire in order, so a row never waits behind
 // weight loads, and the weights stream from the first cycle instead of
 // after the quantization (the kernel above issues its first weight step
 // once x has arrived, and every wavefront quantizes a share of all rows).
@@ -768,14 +768,16 @@ constexpr int kSplitWWaves = kFusedWaves - kSplitXWaves;
 constexpr int kSplitCapSmall = 8;   // K <= 4096
 constexpr int kSplitCapLarge = 22;  // K <= 11264
 
-template <int EPI, typename TX, typename TY, typename TH, bool RES, int CAP>
+template <int EPI, typename TX, typename TY, typename TH, bool RES, int CAP, int ROWS>
 __global__ __launch_bounds__(kFusedThreads) void gemv_split_kernel(FusedParams p) {
   static_assert(EPI == kEpiDequant && !std::is_same<TX, int8_t>::value, "o_proj shape");
   constexpr int kSplitMaxKB = CAP * kSplitWWaves;
+  static_assert(ROWS == kFusedMaxRows || (ROWS == kFusedMaxRows16 && CAP == kSplitCapSmall),
+                "8 rows, or 16 rows of K <= 4096");
   // A fragments: [kb][g][row < 8][16 bytes]
-  __shared__ __attribute__((aligned(16))) int8_t a_lds[kSplitMaxKB * 512];
+  __shared__ __attribute__((aligned(16))) int8_t a_lds[kSplitMaxKB * ROWS * 64];
   __shared__ int32_t red[kSplitWWaves][256];
-  __shared__ float row_s[kFusedMaxRows];
+  __shared__ float row_s[ROWS];
   __shared__ float ops_lds[32];  // the block's 16 weight scales, then 16 biases
 
   const int tid = threadIdx.x;
@@ -822,6 +824,9 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_split_kernel(FusedParams p
   // quantization waits for x only (a conditional load here would make the
   // compiler wait for all of them).
   float op_s = 0.0f, op_b = 0.0f;
+  // 9-16 rows: wavefront w also takes row w + 8, loaded behind row w.
+  const int row2 = row + kSplitXWaves;
+  [[maybe_unused]] u32x4 raw2[ROWS > kFusedMaxRows ? CAP : 1];
   if (row_live) {
     // The row's K elements; chunks past K read zeros (zero int8 columns up
     // to the k-block end).
@@ -832,6 +837,17 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_split_kernel(FusedParams p
     for (int i = 0; i < CAP; ++i) {
       raw[i] = __builtin_bit_cast(
           u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc, (lane + 64 * i) * 16, 0, 0));
+    }
+    if constexpr (ROWS > kFusedMaxRows) {
+      // Row w + 8, or an empty range past M (the loads stay on one path).
+      const __amdgpu_buffer_rsrc_t xrsrc2 = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint16_t*>(static_cast<const uint16_t*>(p.x) + min(row2, M - 1) * p.ldx),
+          0, __builtin_amdgcn_readfirstlane(row2 < M ? K * 2 : 0), kBufferWord3);
+#pragma unroll
+      for (int i = 0; i < CAP; ++i) {
+        raw2[i] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrsrc2, (lane + 64 * i) * 16, 0, 0));
+      }
     }
     const int64_t n = nb * 16 + (tid & 15);
     const int64_t nc = min(n, static_cast<int64_t>(p.N) - 1);
@@ -870,8 +886,44 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_split_kernel(FusedParams p
           xv[2 * q + 1] = bits_to_f32<TX>(raw[i][q] >> 16);
         }
         const int k = c * 8;
-        const int off = (((k >> 6) * 4 + ((k & 63) >> 4)) * kFusedMaxRows + row) * 16 + (k & 15);
+        const int off = (((k >> 6) * 4 + ((k & 63) >> 4)) * ROWS + row) * 16 + (k & 15);
         *reinterpret_cast<u32x2*>(a_lds + off) = quant8_dyn(xv, s, r);
+      }
+    }
+    if constexpr (ROWS > kFusedMaxRows) {
+      if (row2 < M) {
+        // The same steps on row w + 8.
+        u16x2 bm2 = {0, 0};
+#pragma unroll
+        for (int i = 0; i < CAP; ++i) {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            bm2 = __builtin_elementwise_max(bm2,
+                                            __builtin_bit_cast(u16x2, raw2[i][q] & 0x7fff7fffu));
+        }
+        const uint32_t bm =
+            wave_max_u32(max(static_cast<uint32_t>(bm2[0]), static_cast<uint32_t>(bm2[1])));
+        const float s2 = scale_from_absmax(bits_to_f32<TX>(bm));
+        const float r2 = 1.0f / s2;
+        if (lane == 0) {
+          row_s[row2] = s2;
+          if (blockIdx.x == 0 && p.sx_out != nullptr) p.sx_out[row2] = s2;
+        }
+#pragma unroll
+        for (int i = 0; i < CAP; ++i) {
+          const int c = lane + 64 * i;
+          if (c < nchunk) {
+            float xv[8];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              xv[2 * q] = bits_to_f32<TX>(raw2[i][q] & 0xffffu);
+              xv[2 * q + 1] = bits_to_f32<TX>(raw2[i][q] >> 16);
+            }
+            const int k = c * 8;
+            const int off = (((k >> 6) * 4 + ((k & 63) >> 4)) * ROWS + row2) * 16 + (k & 15);
+            *reinterpret_cast<u32x2*>(a_lds + off) = quant8_dyn(xv, s2, r2);
+          }
+        }
       }
     }
   }
@@ -886,13 +938,13 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_split_kernel(FusedParams p
     const int li = lane & 15;
     const int lg = lane >> 4;
     const bool a_live = li < M;
-    const int a_off = (lg * kFusedMaxRows + li) * 16;
+    const int a_off = (lg * ROWS + li) * 16;
     i32x4 acc = i32x4{0, 0, 0, 0};
 #pragma unroll
     for (int i = 0; i < CAP; ++i) {
       const int kb = kb0 + i;
       if (kb < kb1) {
-        const i32x4 a = a_live ? *reinterpret_cast<const i32x4*>(a_lds + kb * 512 + a_off)
+        const i32x4 a = a_live ? *reinterpret_cast<const i32x4*>(a_lds + kb * (ROWS * 64) + a_off)
                                : i32x4{0, 0, 0, 0};
         acc = mfma_16x16x64(a, __builtin_bit_cast(i32x4, buf[i]), acc);
       }
@@ -904,22 +956,34 @@ __global__ __launch_bounds__(kFusedThreads) void gemv_split_kernel(FusedParams p
   epilogue<EPI, TY, TH, RES, kSplitWWaves>(p, red, row_s, nb, tid, ops_lds, &res0);
 }
 
-// The o_proj / down shapes gemv_split_kernel takes.
+// The o_proj / down shapes gemv_split_kernel takes: M <= 8 with K <= 11264,
+// or 9-16 rows of K <= 4096 (O at 9-12 / 16 rows: 7.0 / 6.6 / 8.4 against
+// 8.3 / 8.5 / 9.3 us for quantization + gemv_kernel, graphs of 32 layers).
+// With the residual add, 13-16 rows measured 0.5-0.9 us slower than the
+// two-launch route and keep it (kSplitResMaxRows).
+constexpr int kSplitResMaxRows = 12;
 bool split_shape(int64_t M, int64_t NB, int64_t KB) {
-  return M >= 1 && M <= kFusedMaxRows && KB >= 1 && KB <= kSplitCapLarge * kSplitWWaves &&
+  return M >= 1 && KB >= 1 &&
+         ((M <= kFusedMaxRows && KB <= kSplitCapLarge * kSplitWWaves) ||
+          (M <= kFusedMaxRows16 && KB <= kSplitCapSmall * kSplitWWaves)) &&
          NB <= cu_count();
 }
 
 template <int EPI, typename TX, typename TY, typename TH, bool RES = false>
 hipError_t launch_f(const FusedParams& p, hipStream_t st) {
   if constexpr (EPI == kEpiDequant && !std::is_same<TX, int8_t>::value) {
-    if (split_shape(p.M, p.NB, p.KB)) {
-      if (p.KB <= kSplitCapSmall * kSplitWWaves)
-        hipLaunchKernelGGL((gemv_split_kernel<EPI, TX, TY, TH, RES, kSplitCapSmall>),
-                           dim3(p.NB), dim3(kFusedThreads), 0, st, p);
+    if (split_shape(p.M, p.NB, p.KB) && (!RES || p.M <= kSplitResMaxRows)) {
+      constexpr int R8 = kFusedMaxRows, R16 = kFusedMaxRows16;
+      const dim3 grid(p.NB), block(kFusedThreads);
+      if (p.M > R8)
+        hipLaunchKernelGGL((gemv_split_kernel<EPI, TX, TY, TH, RES, kSplitCapSmall, R16>), grid,
+                           block, 0, st, p);
+      else if (p.KB <= kSplitCapSmall * kSplitWWaves)
+        hipLaunchKernelGGL((gemv_split_kernel<EPI, TX, TY, TH, RES, kSplitCapSmall, R8>), grid,
+                           block, 0, st, p);
       else
-        hipLaunchKernelGGL((gemv_split_kernel<EPI, TX, TY, TH, RES, kSplitCapLarge>),
-                           dim3(p.NB), dim3(kFusedThreads), 0, st, p);
+        hipLaunchKernelGGL((gemv_split_kernel<EPI, TX, TY, TH, RES, kSplitCapLarge, R8>), grid,
+                           block, 0, st, p);
       return hipGetLastError();
     }
   }
@@ -1060,14 +1124,15 @@ int balanced_grid(int64_t nb) {
 // fused, O 4-7% faster than quantize + GEMV, down within 1%).  With 9-16 rows
 // the quantize + GEMV route pays more per row, and 2 bytes per element
 // suffice (packed QKV at M = 13-16: 12-17% faster fused).
-// The dequant epilogue at one block per CU (N <= 16 * CUs, K <= 11264, the
-// o_proj / down shapes) takes gemv_split_kernel at any M <= 8 instead: its
+// The dequant epilogue at one block per CU (N <= 16 * CUs, K <= 11264 at
+// M <= 8, K <= 4096 at 9-16 rows: the o_proj / down shapes) takes
+// gemv_split_kernel instead (split_shape): its
 // weights stream from the first cycle while half the wavefronts quantize,
 // so the CU's share of the weights no longer has to cover the quantization
 // (graphs of 32 layers at M = 1 / 4 / 8: O 5.3 / 5.3 / 5.9 against
 // 6.6 / 7.2 / 8.1 us, down 9.9 / 10.5 / 11.4 against 11.0 / 13.4 / 14.3 us).
 bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
-                          int64_t K, int epi) {
+                          int64_t K, int epi, bool residual) {
   if (!((x_dtype == kF16 || x_dtype == kBF16) && M >= 1 && M <= kFusedMaxRows16 && K >= 8 &&
         K % 8 == 0 &&
         ceil_div(K, kTileK) <= (M <= kFusedMaxRows ? kFusedMaxKB : kFusedMaxKB16) &&
@@ -1075,7 +1140,9 @@ bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, in
         (reinterpret_cast<uintptr_t>(x) & 15u) == 0))
     return false;
   const int64_t nb = ceil_div(N, kTileRows);
-  if (epi == kEpiDequant && split_shape(M, nb, ceil_div(K, kTileK))) return true;
+  if (epi == kEpiDequant && split_shape(M, nb, ceil_div(K, kTileK)) &&
+      (!residual || M <= kSplitResMaxRows))
+    return true;
   const int64_t g = nb < cu_count() ? nb : cu_count();
   const int64_t blocks_per_cu = ceil_div(nb, g);
   const int64_t weight_bytes_per_cu = blocks_per_cu * kTileRows * ceil_div(K, kTileK) * kTileK;

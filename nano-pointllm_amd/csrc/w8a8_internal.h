@@ -148,9 +148,9 @@ int cu_count();
 // fewest that keep every workgroup at ceil(nb / CUs) blocks or one less.
 int balanced_grid(int64_t nb);
 // epi: the epilogue (kEpiDequant also admits the o_proj shapes of the
-// split kernel), or -1.
+// split kernel), or -1; residual: the call adds a residual in its epilogue.
 bool fused_gemv_supported(const void* x, int x_dtype, int64_t ldx, int64_t M, int64_t N,
-                          int64_t K, int epi = -1);
+                          int64_t K, int epi = -1, bool residual = false);
 // The fused kernel's weight stream on int8 activations (op.a row-major as for
 // the GEMV, op.sx per-row scales); decode shapes only.
 bool fused_gemv_i8_supported(int64_t M, int64_t N, int64_t K, int64_t lda, int epi);

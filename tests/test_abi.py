@@ -70,9 +70,9 @@ def test_invalid_arguments_return_status_without_launch():
     assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_SILU_MUL_Q8, fake,
                            _lib.I8, 8, 0.0, _lib.F16, 1, 16, 64, None, fake, 1 << 20,
                            None) == _lib.ERR_SHAPE
-    # workspace too small (m = 9 is outside the workspace-free decode path)
+    # workspace too small (m = 17 is outside the workspace-free decode paths)
     assert lib.w8a8_linear(fake, _lib.F16, 64, fake, fake, None, _lib.EPI_DEQUANT, fake,
-                           _lib.F16, 16, 0.0, _lib.F16, 9, 16, 64, None, fake, 10,
+                           _lib.F16, 16, 0.0, _lib.F16, 17, 16, 64, None, fake, 10,
                            None) == _lib.ERR_WORKSPACE
     # packed activations: misaligned, or a missing scale vector
     assert lib.w8a8_linear_packed(ctypes.c_void_p(0x1008), fake, fake, fake, None,

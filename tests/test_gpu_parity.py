@@ -492,7 +492,32 @@ def test_split_decode_path(cuda, m, n, k):
     np.testing.assert_array_equal(y32.cpu().numpy(), exp)
 
 
-@pytest.mark.parametrize("m,n,k", [(8, 4096, 4096), (3, 4096, 11008), (6, 700, 2000)])
+@pytest.mark.parametrize("m", [9, 10, 12, 13, 16])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (1000, 4096), (40, 64), (4095, 2000)])
+def test_split_decode_path_16_rows(cuda, m, n, k):
+    """9-16 rows of K <= 4096 on the split kernel (each row wavefront takes
+    rows w and w + 8): outputs with a bias and row scales against the
+    oracle, through the workspace-free call."""
+    from nanopointllm_amd import _lib, w8a8
+
+    g = torch.Generator().manual_seed(m * 31 + k)
+    x = torch.randn(m, k, generator=g) * 2
+    x[:, :: max(1, k // 3)] *= 25
+    x = x.to(torch.float16)
+    _, qw, sw = weight_q(n, k, seed=n + 2 * k)
+    bias = np.linspace(-1, 1, n).astype(np.float32)
+    wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
+    swt, bt, xc = torch.from_numpy(sw).to(cuda), torch.from_numpy(bias).to(cuda), x.to(cuda)
+    note(f"split decode 16 rows m={m} n={n} k={k}")
+    rc, y, sx = _linear_without_workspace(xc, wp, swt, bt, n, _lib.EPI_DEQUANT, torch.float16)
+    assert rc == 0, _lib.load().w8a8_status_string(rc)
+    exp, _, _, esx = O.w8a8_linear_dynamic(x.float().numpy(), qw, sw, bias)
+    np.testing.assert_array_equal(sx.cpu().numpy(), esx[:, 0])
+    np.testing.assert_array_equal(f16_to_np(y), exp.astype(np.float16))
+
+
+@pytest.mark.parametrize("m,n,k", [(8, 4096, 4096), (3, 4096, 11008), (6, 700, 2000),
+                                   (14, 4096, 4096)])
 def test_split_decode_path_bf16(cuda, m, n, k):
     from nanopointllm_amd import w8a8
 
@@ -509,13 +534,13 @@ def test_split_decode_path_bf16(cuda, m, n, k):
 
 def test_fused_path_not_taken_for_small_shapes(cuda):
     """Projections that neither fused kernel takes on a 256-CU MI355X (12
-    rows of a 4096 x 4096 weight, K = 12288 beyond the split kernel's rows,
-    257 blocks of short rows) and the int32 epilogue of the split shapes go
-    through quantization + GEMV (they need a workspace) and give the same
-    results."""
+    rows of K = 4104 and 17 rows of K = 4096, beyond the split kernel's 16
+    rows of K <= 4096; K = 12288 beyond its 8 rows; 257 blocks of short
+    rows) and the int32 epilogue of the split shapes go through quantization
+    + GEMV (they need a workspace) and give the same results."""
     from nanopointllm_amd import _lib, w8a8
 
-    for m, n, k in [(12, 4096, 4096), (8, 4096, 12288), (8, 4112, 1024)]:
+    for m, n, k in [(12, 4096, 4104), (17, 4096, 4096), (8, 4096, 12288), (8, 4112, 1024)]:
         _, qw, sw = weight_q(n, k, seed=n + k)
         wp = w8a8.pack_rows(torch.from_numpy(qw).to(cuda))
         x = torch.randn(m, k, generator=torch.Generator().manual_seed(k)).to(torch.float16)

@@ -71,7 +71,8 @@ def _expected(xq, sx, wq, sw, bias, res16, dtype):
     (8, 1004, 1000, torch.float16), (100, 1004, 1000, torch.float16),
     (8, 4096, 4096, torch.bfloat16), (100, 4100, 700, torch.bfloat16),
     (5, 4096, 11008, torch.float16), (2, 300, 11264, torch.bfloat16),
-    (7, 4096, 4104, torch.float16),
+    (7, 4096, 4104, torch.float16), (11, 4096, 4096, torch.float16),
+    (16, 4096, 4096, torch.bfloat16),
 ])
 def test_linear_residual_matches_the_oracle(cuda, m, n, k, dtype):
     from nanopointllm_amd import w8a8
